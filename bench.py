@@ -1,0 +1,248 @@
+"""Throughput benchmark of the LCT codec hot path on one MI355X.
+
+Workload (the north-star configuration): randn(16384, 8192) with CPU seed 0,
+cast to BF16 (256 MiB), Distribution(GAUSSIAN), CLEAN layout.  A step is one
+decompression of the whole tensor through the public API; compression is
+timed the same way.  Inputs stay resident in HBM; two input/compressed sets
+alternate so the 256 MB Infinity Cache cannot serve repeats.
+
+Prints one JSON line: ``value`` is decompression throughput in GB/s of
+uncompressed BF16 (2n bytes / time), with compression throughput, the
+compression ratio, the decoder kernel's roofline fraction and a host-core
+CPU baseline (the C oracle, OpenMP over codec blocks) beside it.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "decompress/compress GB/s (BF16 bytes) & % HBM peak; compression ratio"
+HBM_PEAK_GBPS = 8000.0   # MI355X HBM3E, 8 TB/s
+SHAPE = (16384, 8192)
+
+
+def _log(message: str) -> None:
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+def decode_bytes(ct) -> int:
+    """Algorithmic bytes of one decode: payload + side + tails + 2/entry +
+    block metadata read, 2n written."""
+    B, L, S, W = ct.codec_geometry
+    nb = ct.size // B
+    count = int(ct.fallback_count.item())
+    tails = int(ct.fallback_used.item())
+    return nb * L * W * 4 + ct.size + tails + 2 * count + 12 * nb + 2 * ct.logical_numel
+
+
+def encode_bytes(ct) -> int:
+    """Algorithmic bytes of one encode: 2n read; side, payload, extra starts,
+    tails, 2/entry and block metadata written."""
+    B, L, S, W = ct.codec_geometry
+    nb = ct.size // B
+    count = int(ct.fallback_count.item())
+    tails = int(ct.fallback_used.item())
+    return 2 * ct.logical_numel + ct.size + nb * L * W * 4 + nb * L + tails + 2 * count + 12 * nb
+
+
+def _time_events(fn, steps: int, warmup: int, torch) -> float:
+    """Average milliseconds per call over ``steps`` calls (after warm-up)."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def _kernel_ms(launch, steps: int, torch) -> float:
+    """Average duration of single launches bracketed by events on the launch stream."""
+    total = 0.0
+    for i in range(steps):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        launch(i)
+        end.record()
+        end.synchronize()
+        total += start.elapsed_time(end)
+    return total / steps
+
+
+def cpu_baseline(x_cpu, dist, min_seconds: float):
+    """Time the C oracle (OpenMP over blocks) compress + decompress on host cores."""
+    import numpy as np
+
+    import oracle
+    from losslessly_compressed_tensors_amd.compression.huffman_tables import distribution_codebook
+
+    book = distribution_codebook(dist)
+    geometry = oracle.geometry_of("gaussian", "clean")
+    bits = x_cpu.view(-1).view(__import__("torch").int16).numpy()
+    reps = 0
+    enc_s = dec_s = 0.0
+    compressed = None
+    while reps < 2 or enc_s + dec_s < min_seconds:
+        t0 = time.perf_counter()
+        compressed = oracle.compress(bits, geometry, book.encode, book.decode, book.rare_length)
+        t1 = time.perf_counter()
+        restored = oracle.decompress(compressed)
+        t2 = time.perf_counter()
+        enc_s += t1 - t0
+        dec_s += t2 - t1
+        reps += 1
+    assert np.array_equal(restored, bits.view(np.uint16))
+    nbytes = 2 * bits.size
+    return {
+        "value": round(nbytes * reps / dec_s / 1e9, 3),
+        "unit": "GB/s",
+        "cores": oracle.num_threads(),
+        "kind": "port",
+        "sample": f"full workload tensor ({bits.size} BF16), {reps} decompressions "
+                  f"({dec_s:.1f} s) and compressions ({enc_s:.1f} s)",
+        "compress_value": round(nbytes * reps / enc_s / 1e9, 3),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--cpu-seconds", type=float, default=8.0)
+    parser.add_argument("--skip-cpu", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: the codec path has no multi-GPU form here "
+              "(see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from losslessly_compressed_tensors_amd.codec.decode import overlay_of, shifted_decode_table
+    from losslessly_compressed_tensors_amd.comp_format import DistType, Distribution
+    from losslessly_compressed_tensors_amd.compression.huffman_tables import (
+        get_distribution_tables,
+    )
+    from losslessly_compressed_tensors_amd.kernels import dispatch
+    from losslessly_compressed_tensors_amd.operations import compress, decompress
+    from losslessly_compressed_tensors_amd.tensor_buffer import TensorBuffer
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    device = torch.device("cuda", 0)
+    dist = Distribution(DistType.GAUSSIAN)
+    _log("generating inputs")
+    host_inputs = []
+    for seed in (0, 1):
+        gen = torch.Generator().manual_seed(seed)
+        host_inputs.append(torch.randn(*SHAPE, generator=gen).to(torch.bfloat16))
+    xs = [h.to(device) for h in host_inputs]
+    n = xs[0].numel()
+    nbytes = 2 * n
+
+    _log("correctness pass")
+    private = compress(xs[0], dist)
+    restored = decompress(private)
+    if not torch.equal(restored.view(torch.int16), xs[0].view(torch.int16)):
+        raise AssertionError("round trip is not bit-exact")
+    ratio = nbytes / private.memory_size()
+
+    buffer = TensorBuffer(64 << 20, device=device)
+    cts = [compress(x, dist, buffer=buffer) for x in xs]
+    for ct, x in zip(cts, xs):
+        if not torch.equal(decompress(ct).view(torch.int16), x.view(torch.int16)):
+            raise AssertionError("buffered round trip is not bit-exact")
+
+    _log("timing decompress")
+    dec_ms = _time_events(lambda i: decompress(cts[i % 2]), args.steps, args.warmup, torch)
+
+    # Decoder kernel alone, outputs preallocated, one event pair per launch.
+    _, _, rare = get_distribution_tables(dist, device)
+    B, L, S, W = cts[0].codec_geometry
+    outs = [torch.empty(n, dtype=torch.int16, device=device) for _ in range(2)]
+
+    def launch_decode(i):
+        ct = cts[i % 2]
+        dispatch.decode_kernel(ct.data, ct.sign_mantissa, outs[i % 2], shifted_decode_table(ct),
+                               ct.center, ct.size, logical_numel=n, block_symbols=B, lanes=L,
+                               steps=S, fixed_words=W, rare_length=rare, overflow=overlay_of(ct))
+
+    for i in range(args.warmup):
+        launch_decode(i)
+    kernel_ms = _kernel_ms(launch_decode, args.steps, torch)
+    dec_alg = decode_bytes(cts[0])
+
+    _log("timing compress")
+
+    def compress_step(i):
+        compress(xs[i % 2], dist, buffer=buffer).free()
+
+    enc_ms = _time_events(compress_step, args.steps, args.warmup, torch)
+    enc_private_ms = _time_events(lambda i: compress(xs[i % 2], dist), max(5, args.steps // 5),
+                                  2, torch)
+    enc_alg = encode_bytes(cts[0])
+
+    result = {
+        "metric": METRIC,
+        "value": round(nbytes / (dec_ms * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32",
+        "data": "synthetic",
+        "config": {
+            "workload": "NS: randn(16384, 8192), CPU seed 0, cast to BF16 (256 MiB); "
+                        "Distribution(GAUSSIAN) CLEAN; step = one public-API decompress",
+            "elements": n,
+            "geometry": [B, L, S, W],
+            "sets_rotated": 2,
+        },
+        "decompress_gbps": round(nbytes / (dec_ms * 1e-3) / 1e9, 2),
+        "decompress_hbm_frac": round(dec_alg / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "compress_gbps": round(nbytes / (enc_ms * 1e-3) / 1e9, 2),
+        "compress_hbm_frac": round(enc_alg / (enc_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "compress_private_gbps": round(nbytes / (enc_private_ms * 1e-3) / 1e9, 2),
+        "compress_ms": round(enc_ms, 5),
+        "compression_ratio": round(ratio, 5),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode_kernel",
+            "achieved": round(dec_alg / (kernel_ms * 1e-3) / 1e9, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(dec_alg / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "algorithmic_bytes": dec_alg,
+            "kernel_us": round(kernel_ms * 1e3, 2),
+        },
+    }
+    if not args.skip_cpu:
+        _log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(host_inputs[0], dist, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,205 @@
+/* C ABI of the MI355X (gfx950) LCT codec library, liblct_hip.so.
+ *
+ * Each entry point replaces one kernel-launch function of the reference's
+ * operator boundary, LCT/kernels/dispatch.py (cited per function; paths are
+ * relative to the reference repository root).  Conventions:
+ *
+ *  - every pointer argument is a device pointer unless documented otherwise;
+ *    sizes are element counts; nothing is allocated, synchronised or thrown;
+ *  - work is enqueued on `stream` (NULL = the default stream);
+ *  - the return value is LCT_OK, a negative LCT_E* argument error (nothing
+ *    was launched), or a positive hipError_t from the launch;
+ *  - device-side failures (allocator) are reported through the allocator
+ *    descriptor/status words, as in the reference.
+ *
+ * Storage format (identical to the reference's): a tensor of n BF16 values is
+ * padded to N = nb*B storage elements in nb blocks of L=256 lanes x S steps.
+ * Storage (block k, step t, lane l) holds logical element
+ * (k*S+t)*256 + (l ^ ((k*S+t) & 254)).  Each lane's exponents form one Huffman
+ * stream whose first W 32-bit words live at encoded[w*nb*256 + k*256 + l];
+ * sign+mantissa bytes are stored separately in storage order.
+ */
+#ifndef LCT_H
+#define LCT_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LCT_OK 0
+#define LCT_E_NULL (-1)        /* a required pointer is NULL */
+#define LCT_E_GEOMETRY (-2)    /* geometry not (B, 256, B/256, W) with even S, 2 <= W <= 64 */
+#define LCT_E_SIZE (-3)        /* sizes inconsistent or out of the supported range */
+#define LCT_E_ARG (-4)         /* another argument out of range */
+
+/* Stream geometry (B, L, S, W): LCT/codec/geometry.py:13-39. */
+typedef struct {
+    int32_t block_symbols; /* B = L * S */
+    int32_t lanes;         /* L, always 256 */
+    int32_t steps;         /* S, even */
+    int32_t fixed_words;   /* W, 32-bit payload words per stream */
+} lct_geometry;
+
+/* Overflow (fallback) storage of one compressed tensor, as
+ * LCT/kernels/backends.py:36-50 (FallbackStorage) + decode.py:195-240 read it.
+ * Private layout: lanes/starts/tail are separate arrays, `base` is the tail
+ * base (CompressedTensor.fallback_base).  Buffered layout: lanes, starts and
+ * tail all point at the TensorBuffer arena; entries sit at descriptor[0],
+ * starts at descriptor[0]+count, tails at descriptor[0]+2*count. */
+typedef struct {
+    const uint8_t *lanes;
+    const uint8_t *starts;
+    const uint8_t *tail;
+    const int32_t *blocks;     /* int32[3*nb]: count, first entry, tail byte base */
+    const int32_t *count;      /* int32[1]: total entries (buffered offsets) */
+    const int32_t *descriptor; /* int32[4] TensorBuffer descriptor, or NULL = private */
+    int64_t base;              /* private tail base */
+} lct_overflow;
+
+/* Pointwise operation selectors: LCT/codec/pointwise.py:289-304. */
+#define LCT_OP_ADD 0
+#define LCT_OP_MULTIPLY 1
+#define LCT_OP_SCALAR_MUL_ADD 2
+/* Output policies: LCT/kernels/generic/pointwise.py:14-15. */
+#define LCT_DENSE_OUTPUT 0
+#define LCT_COMPRESSED_OUTPUT 1
+
+/* Library version string (host pointer, static storage). */
+const char *lct_version(void);
+
+/* Human-readable text for an LCT_* or hipError_t return code. */
+const char *lct_error_string(int32_t code);
+
+/* ---- tables: replaces dispatch.py:33-48 (estimate_and_shift_encoding_table)
+ * Sample min(logical_numel, 4096)=sample_size exponents of `source` (int16 BF16
+ * bits, or uint8 exponent bytes if `precomputed`), store their rounded mean in
+ * center[0], and build the center-shifted tables: shifted_encode int32[256]
+ * indexed by raw exponent byte, shifted_decode int32[1024] holding
+ * len | exponent<<8.  base_encode/base_decode are the distribution's tables. */
+int32_t lct_estimate_and_shift_tables(const void *source, int32_t precomputed,
+                                      int64_t logical_numel, int64_t sample_size,
+                                      const int32_t *base_encode,
+                                      const int32_t *base_decode,
+                                      int32_t *center, int32_t *shifted_encode,
+                                      int32_t *shifted_decode, hipStream_t stream);
+
+/* ---- replaces dispatch.py:16-30 (shift_encoding_table): same tables for a
+ * given device-resident center. */
+int32_t lct_shift_tables(const int32_t *base_encode, const int32_t *center,
+                         int32_t *shifted_encode, const int32_t *base_decode,
+                         int32_t *shifted_decode, hipStream_t stream);
+
+/* ---- replaces dispatch.py:51-62 (shift_decoding_table). */
+int32_t lct_shift_decoding_table(const int32_t *base_decode,
+                                 const int32_t *center, int32_t *shifted_decode,
+                                 hipStream_t stream);
+
+/* ---- encoder: replaces dispatch.py:294-316 (encode_kernel).
+ * source: int16 BF16 bits [logical_numel] or, if precomputed, uint8 exponent
+ * bytes [logical_numel] (logical order).  side: uint8[size] sign+mantissa in
+ * storage order -- written here unless precomputed (padding is written as 0).
+ * encoded: int32[nb*256*W + 4]; every one of the first nb*256*W words is
+ * written (words a stream does not use are 0).  extra_starts: uint8[nb*256],
+ * the first overflowing (even) step of each stream or 255.  summaries:
+ * int32[4*nb] (per-block overflow count and tail bytes in the first 2*nb) when
+ * write_summary, else unused.  size = nb*B. */
+int32_t lct_encode(const void *source, uint8_t *side, int32_t *encoded,
+                   const int32_t *shifted_encode, uint8_t *extra_starts,
+                   int32_t *summaries, int64_t size, int64_t logical_numel,
+                   lct_geometry geometry, int32_t precomputed,
+                   int32_t write_summary, hipStream_t stream);
+
+/* ---- replaces dispatch.py:70-85 (prefix_allocate): exclusive scans of the
+ * per-block overflow counts/bytes into summaries[2nb..4nb), counts[4] =
+ * {total_count, total_bytes, 0, 0}; if buffered, reserve
+ * align16(total_bytes + 2*total_count) bytes from the TensorBuffer whose
+ * metadata starts at buffer_meta (int32 free_starts[R] | free_sizes[R] | count
+ * | lock | generation) and write descriptor[4] = {offset, size, status, gen}.
+ * n_blocks <= 8192 (LCT/kernels/autotune.py:54). */
+int32_t lct_prefix_allocate(int32_t *summaries, int32_t *counts,
+                            int32_t *descriptor, int32_t *buffer_meta,
+                            int64_t n_blocks, int32_t buffered,
+                            int32_t max_free_regions, hipStream_t stream);
+
+/* ---- replaces dispatch.py:113-130 (compact_extra, summaries path): per block
+ * write the overflowing streams' lane and start bytes (ascending lane) and
+ * their exponent tails int8(e-127) for steps start..S-1, plus
+ * blocks[3*nb] = {count, first, byte_base}.  Private: lanes/starts/tail are
+ * exact-size arrays, tails at tail + base.  Buffered: all three point at the
+ * arena; offsets from descriptor and count as in lct_overflow.  A buffered
+ * allocation whose status is not 0 gets no entries or tails written. */
+int32_t lct_compact_extra(const void *source, uint8_t *lanes, uint8_t *starts,
+                          uint8_t *tail, const int32_t *descriptor,
+                          const int32_t *count, int32_t *blocks, int64_t base,
+                          const uint8_t *extra_starts, const int32_t *summaries,
+                          int64_t size, int64_t logical_numel,
+                          lct_geometry geometry, int32_t precomputed,
+                          int32_t buffered, hipStream_t stream);
+
+/* ---- decoder: replaces dispatch.py:319-361 (decode_kernel), with the
+ * overflow overlay fused (overflow != NULL) as _decode_overflow_kernel does.
+ * output: int16[logical_numel] BF16 bits in logical order. */
+int32_t lct_decode(const int32_t *encoded, const uint8_t *side, int16_t *output,
+                   const int32_t *shifted_decode, const int32_t *center,
+                   int64_t size, int64_t logical_numel, lct_geometry geometry,
+                   int32_t rare_length, const lct_overflow *overflow,
+                   hipStream_t stream);
+
+/* ---- fused pointwise, one compressed + one dense operand: replaces
+ * dispatch.py:168-187 (pointwise_dense) together with dispatch.py:190-212
+ * (pointwise_fallback); overflow rows are overlaid in the same pass.
+ * other: bf16[logical_numel].  alpha/beta: float32[1] device scalars, read
+ * only for LCT_OP_SCALAR_MUL_ADD when !alpha_is_one / !beta_is_one.
+ * Dense policy: output bf16[logical_numel]; auxiliary unused.  Compressed
+ * policy: output uint8[size] side bytes (storage order, padding 0) and
+ * auxiliary uint8[>= logical_numel] exponent bytes (logical order). */
+int32_t lct_pointwise_dense(const int32_t *encoded, const uint8_t *side,
+                            const void *other, void *output, uint8_t *auxiliary,
+                            const int32_t *shifted_decode, const int32_t *center,
+                            const float *alpha, const float *beta,
+                            int64_t size, int64_t logical_numel,
+                            lct_geometry geometry, int32_t rare_length,
+                            int32_t op, int32_t alpha_is_one,
+                            int32_t beta_is_one, int32_t output_policy,
+                            const lct_overflow *overflow, hipStream_t stream);
+
+/* ---- fused alpha*A + B with both operands compressed (same geometry):
+ * replaces dispatch.py:215-286 (dual_maps_init + dual_tables_and_maps +
+ * dual_mapped) with one launch; a_shifted/b_shifted are each operand's
+ * shifted decode table.  Outputs as lct_pointwise_dense. */
+int32_t lct_dual(const int32_t *a_encoded, const uint8_t *a_side,
+                 const int32_t *a_shifted_decode, const int32_t *a_center,
+                 const lct_overflow *a_overflow, const int32_t *b_encoded,
+                 const uint8_t *b_side, const int32_t *b_shifted_decode,
+                 const int32_t *b_center, const lct_overflow *b_overflow,
+                 const float *alpha, void *output, uint8_t *auxiliary,
+                 int64_t size, int64_t logical_numel, lct_geometry geometry,
+                 int32_t rare_length, int32_t output_policy,
+                 hipStream_t stream);
+
+/* ---- TensorBuffer allocator kernels: replace LCT/tensor_buffer.py:130-136
+ * (_reset_kernel launch), :93-120 (_allocate_kernel launches) and
+ * LCT/kernels/tensor_buffer_ops.py:5-15 (_free_storage_kernel launch).
+ * meta: the int32 metadata block at the start of the buffer's storage.
+ * requested/item_count: device int32[1]; item_count may be NULL when
+ * item_bytes == 0.  descriptor: int32[4] {offset, size, status, generation};
+ * status 0 ok, 1 no fit, 2 empty request, 5 freed, 6 lock not acquired.
+ * free writes status_out[0]: 0 ok, 3 free list full, 4 invalid descriptor,
+ * 6 lock not acquired. */
+int32_t lct_buffer_reset(int32_t *meta, int32_t max_free_regions,
+                         int32_t capacity_bytes, hipStream_t stream);
+int32_t lct_buffer_allocate(int32_t *meta, int32_t max_free_regions,
+                            const int32_t *requested, const int32_t *item_count,
+                            int32_t item_bytes, int32_t *descriptor,
+                            hipStream_t stream);
+int32_t lct_buffer_free(int32_t *meta, int32_t max_free_regions,
+                        int32_t *descriptor, int32_t *status_out,
+                        hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,161 @@
+"""Compression pipeline: center + tables, encoder, scans/allocation, compaction.
+
+Host sequencing of ``LCT/codec/encode.py:22-218`` on the gfx950 library:
+
+1. ``lct_estimate_and_shift_tables`` samples the center and builds the
+   center-shifted encode/decode tables (or shifts them for a given center);
+2. ``lct_encode`` splits fields and writes the fixed payload, per-stream
+   overflow starts and per-block overflow summaries;
+3. ``lct_prefix_allocate`` scans the summaries and, for a shared
+   ``TensorBuffer``, reserves the overflow region on the device;
+4. private storage only: one device->host sync reads the overflow totals so
+   exact-size lane/start/tail arrays can be allocated (as the reference does);
+5. ``lct_compact_extra`` writes the per-block overflow list and tails.
+
+The tensors allocated (and hence ``memory_size()``) match the reference's.
+"""
+from __future__ import annotations
+
+import torch
+
+from ..comp_format import Distribution, StorageLayout
+from ..comp_tensor import CompressedTensor
+from ..compression.huffman_tables import get_distribution_tables
+from ..kernels import dispatch
+from ..kernels.dispatch import SUMMARY_BLOCK_LIMIT, FallbackStorage
+from ..tensor_buffer import TensorBuffer
+from .geometry import geometry
+
+CENTER_SAMPLE_SIZE = 4096
+
+
+def _cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def encode_components(
+    source_values: torch.Tensor,
+    sign_mantissa: torch.Tensor,
+    size: int,
+    distribution: Distribution,
+    buffer: TensorBuffer | None,
+    shape: tuple[int, ...],
+    *,
+    precomputed: bool,
+    center: torch.Tensor | None = None,
+    logical_numel: int,
+) -> CompressedTensor:
+    """Encode BF16 bits (or precomputed exponent bytes + side bytes).
+
+    Args mirror ``LCT/codec/encode.py:22-47``: ``source_values`` is int16 BF16
+    bits, or uint8 raw exponent bytes in logical order when ``precomputed``
+    (``sign_mantissa`` then already holds the side bytes); ``size`` is the
+    padded storage element count; ``center`` an optional device int32[1].
+    """
+    if buffer is not None and buffer.capacity_bytes % 4:
+        raise ValueError("TensorBuffer capacity must be divisible by 4")
+    device = source_values.device
+    stream_geometry = geometry(distribution)
+    block_symbols, lanes, steps, fixed_words = stream_geometry
+    blocks = _cdiv(size, block_symbols)
+    streams = blocks * lanes
+    if blocks > SUMMARY_BLOCK_LIMIT:
+        raise NotImplementedError(
+            f"tensors above {SUMMARY_BLOCK_LIMIT} codec blocks "
+            f"({SUMMARY_BLOCK_LIMIT * block_symbols} elements for this layout) are not supported")
+    encode_table, decode_table, _ = get_distribution_tables(distribution, device)
+    shifted_encode = torch.empty(256, dtype=torch.int32, device=device)
+    shifted_decode = torch.empty_like(decode_table)
+    if center is None:
+        center = torch.empty(1, dtype=torch.int32, device=device)
+        if logical_numel > 0:
+            dispatch.estimate_and_shift_encoding_table(
+                source_values, center, logical_numel, encode_table, shifted_encode,
+                decode_table, shifted_decode, min(logical_numel, CENTER_SAMPLE_SIZE),
+                precomputed)
+        else:
+            center.zero_()   # an empty sample has center 0 (tables.py:47)
+            dispatch.shift_encoding_table(encode_table, center, shifted_encode, decode_table,
+                                          shifted_decode)
+    else:
+        dispatch.shift_encoding_table(encode_table, center, shifted_encode, decode_table,
+                                      shifted_decode)
+
+    encoded = torch.empty(streams * fixed_words + 4, dtype=torch.int32, device=device)
+    extra_starts = torch.empty(streams, dtype=torch.uint8, device=device)
+    summaries = torch.empty(4 * blocks, dtype=torch.int32, device=device)
+    counts = torch.empty(4, dtype=torch.int32, device=device)
+    buffered = buffer is not None
+    descriptor = torch.empty(4, dtype=torch.int32, device=device) if buffered else counts
+    if blocks > 0:
+        dispatch.encode_kernel(
+            source_values, sign_mantissa, encoded, shifted_encode, extra_starts, summaries,
+            size, streams, precomputed=precomputed, logical_numel=logical_numel,
+            block_symbols=block_symbols, lanes=lanes, steps=steps, fixed_words=fixed_words,
+            write_summary=True)
+        dispatch.prefix_allocate(summaries, counts, descriptor, buffer, blocks, buffered,
+                                 buffer.max_free_regions if buffered else 256)
+    else:
+        counts.zero_()
+        if buffered:
+            # An empty request still yields a descriptor (status 2).
+            buffer_descriptor = buffer.allocate(counts[1:2])
+            descriptor = buffer_descriptor.descriptor
+
+    blocks_out = torch.empty(3 * blocks, dtype=torch.int32, device=device)
+    final_count, final_total = counts[:1], counts[1:2]
+    if buffered:
+        arena = buffer.data
+        storage = FallbackStorage(tail=arena, count=final_count, lanes=arena, starts=arena,
+                                  blocks=blocks_out, descriptor=descriptor,
+                                  allocation=descriptor)
+    else:
+        count, tail_bytes = (int(v) for v in counts[:2].tolist())
+        storage = FallbackStorage(
+            tail=torch.empty(tail_bytes, dtype=torch.uint8, device=device),
+            count=final_count,
+            lanes=torch.empty(count, dtype=torch.uint8, device=device),
+            starts=torch.empty(count, dtype=torch.uint8, device=device),
+            blocks=blocks_out, allocation=counts[2:3], base=0)
+    if blocks > 0:
+        dispatch.compact_extra(
+            source_values, storage, blocks, size, precomputed=precomputed, buffered=buffered,
+            logical_numel=logical_numel, block_symbols=block_symbols, lanes=lanes,
+            steps=steps, extra_starts=extra_starts, summaries=summaries)
+    return CompressedTensor(
+        encoded, size, sign_mantissa,
+        fallback_starts=None if buffered else storage.starts,
+        fallback_lanes=None if buffered else storage.lanes,
+        fallback_blocks=storage.blocks,
+        fallback_buffer=storage.tail,
+        fallback_descriptor=descriptor if buffered else None,
+        buffer=buffer,
+        fallback_count=final_count,
+        fallback_used=final_total,
+        distribution=distribution, center=center, decode_table=shifted_decode,
+        shape=shape, layout=StorageLayout.COMPRESSED, stream_geometry=stream_geometry,
+    )
+
+
+def encode(data: torch.Tensor, distribution: Distribution, buffer: TensorBuffer | None = None,
+           *, allow_raw: bool = False) -> CompressedTensor:
+    """Compress a BF16 tensor through the flattened 1-D block layout
+    (``LCT/codec/encode.py:189-218``)."""
+    shape = tuple(data.shape)
+    source = data.contiguous().view(-1)
+    logical_numel = source.numel()
+    block_symbols, lanes, _, fixed_words = geometry(distribution)
+    blocks = _cdiv(logical_numel, block_symbols)
+    storage_numel = blocks * block_symbols
+    streams = blocks * lanes
+    minimum_bytes = storage_numel + (streams * fixed_words + 4) * 4
+    if allow_raw and minimum_bytes > logical_numel * data.element_size():
+        return CompressedTensor(source, logical_numel, buffer=buffer,
+                                distribution=distribution, shape=shape,
+                                layout=StorageLayout.RAW)
+    if source.element_size() != 2:
+        raise TypeError(f"LCT compresses 16-bit (bfloat16) tensors, got {source.dtype}")
+    sign_mantissa = torch.empty(storage_numel, dtype=torch.uint8, device=source.device)
+    return encode_components(source.view(torch.int16), sign_mantissa, storage_numel,
+                             distribution, buffer, shape, precomputed=False,
+                             logical_numel=logical_numel)

@@ -1,0 +1,160 @@
+// Stream decoder shared by the decode, pointwise and dual kernels (gfx950).
+//
+// Semantics: LCT/kernels/generic/decode.py:12-256 and
+// LCT/kernels/primitives.py:7-36.  Each thread owns one stream of its block
+// and decodes it two symbols at a time.
+//
+// MI355X mapping:
+//  * the block's W payload rows (1 KiB each) are staged in LDS with 16-byte
+//    loads; a lane's 32-bit window at bit position `pos` is
+//    alignbit(row[pos/32 + 1], row[pos/32], pos) -- one ds_read2st64 and one
+//    v_alignbit per pair, no 64-bit shifts and no per-lane global gathers;
+//  * the lookup table has 256 entries (direct codes are at most 8 bits,
+//    LCT/compression/huffman_tables.py:106-107) holding the exponent already
+//    in BF16 position: entry = len | e_raw << 7, so a decoded value is one
+//    bit-field insert away from its BF16 bits.  An ESC prefix (or any code
+//    longer than 8 bits) is marked by len = 31, which makes len0 + len1 >= 32;
+//    those pairs take a wave-uniform branch that reads the 8-bit literal;
+//  * a second 256-entry table maps an escaped table index to its exponent
+//    field under the tensor's center.
+#pragma once
+
+#include "lct_device.h"
+
+namespace lct {
+
+struct DecodeTables {
+    uint32_t entry[256];
+    uint32_t escape[256];
+};
+
+// Build both tables from the 1024-entry shifted decode table (len | exp << 8).
+__device__ __forceinline__ void build_decode_tables(DecodeTables &tb,
+                                                    const int32_t *__restrict__ shifted_decode,
+                                                    int32_t center) {
+    const int t = threadIdx.x;
+    const int32_t packed = shifted_decode[t];
+    const int32_t length = packed & 255;
+    const uint32_t field = static_cast<uint32_t>(((packed >> 8) + 127) & 255) << 7;
+    tb.entry[t] = (length >= 1 && length <= 8) ? (static_cast<uint32_t>(length) | field)
+                                               : static_cast<uint32_t>(kEscapeLength);
+    tb.escape[t] = static_cast<uint32_t>((index_to_exponent(t, center) + 127) & 255) << 7;
+}
+
+// Copy the W payload rows of `block` into stage rows 0..W-1 and zero the two
+// pad rows W, W+1 that a window at pos <= 32W may touch.
+__device__ __forceinline__ void stage_payload(uint32_t *stage, const int32_t *__restrict__ encoded,
+                                              int64_t n_streams, int64_t block, int W) {
+    const int t = threadIdx.x;
+    const int chunks = W * (kLanes / 4);
+    for (int c = t; c < chunks; c += kLanes) {
+        const int row = c / (kLanes / 4);
+        const int quad = c % (kLanes / 4);
+        const uint4 *src = reinterpret_cast<const uint4 *>(encoded + row * n_streams + block * kLanes);
+        reinterpret_cast<uint4 *>(stage + row * kLanes)[quad] = src[quad];
+    }
+    stage[W * kLanes + t] = 0u;
+    stage[(W + 1) * kLanes + t] = 0u;
+}
+
+// Per-lane view of the overflow tails of one block.
+struct LaneOverlay {
+    const uint8_t *tail;   // tail bytes of this lane start at tail[offset]
+    int32_t start;         // first overflow step, S if none
+    int32_t offset;
+    int32_t wave_start;    // minimum `start` over the wave (wave-uniform)
+};
+
+// Expand the block's compact overflow list into per-lane (start, offset), as
+// decode.py:195-240 does.  `ov` may be null.  Contains barriers; every thread
+// of the block must call it.  A buffered tensor whose allocation failed
+// (descriptor status != 0) has no tails and is decoded without overlay.
+__device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, bool present,
+                                                     int64_t block, int64_t n_blocks, int S,
+                                                     int32_t *map_start, int32_t *map_offset,
+                                                     int32_t *scratch) {
+    const int t = threadIdx.x;
+    LaneOverlay lane{nullptr, S, 0, S};
+    int32_t count = 0;
+    if (present) {
+        count = ov.blocks[block];
+        if (ov.descriptor != nullptr && ov.descriptor[2] != 0) count = 0;
+    }
+    if (count <= 0) return lane;   // uniform across the block
+    int64_t lane_off = 0, start_off = 0, tail_base = ov.base;
+    if (ov.descriptor != nullptr) {
+        const int64_t arena = ov.descriptor[0];
+        const int64_t total = ov.count[0];
+        lane_off = arena;
+        start_off = arena + total;
+        tail_base = arena + 2 * total;
+    }
+    const int32_t first = ov.blocks[n_blocks + block];
+    const int32_t byte_base = ov.blocks[2 * n_blocks + block];
+    map_start[t] = S;
+    map_offset[t] = 0;
+    const bool valid = t < count;
+    int32_t entry_lane = 0, entry_start = S;
+    if (valid) {
+        entry_lane = ov.lanes[lane_off + first + t];
+        entry_start = ov.starts[start_off + first + t];
+    }
+    int32_t ignored;
+    const int32_t local = block_exclusive_scan(valid ? S - entry_start : 0, scratch, &ignored);
+    if (valid) {
+        map_start[entry_lane] = entry_start;
+        map_offset[entry_lane] = byte_base + local;
+    }
+    __syncthreads();
+    lane.tail = ov.tail + tail_base;
+    lane.start = map_start[t];
+    lane.offset = map_offset[t];
+    lane.wave_start = __builtin_amdgcn_readfirstlane(wave_min(lane.start));
+    return lane;
+}
+
+// One lane's stream cursor.
+struct StreamCursor {
+    const uint32_t *stage;    // stage + lane; row r at stage[r * 256]
+    const DecodeTables *tb;
+    uint32_t pos;
+    uint32_t last_row;        // W: clamp so corrupt payloads stay inside the stage
+    int32_t rare;
+
+    // Decode the next two symbols: exponent fields (bits 7..14) and lengths.
+    __device__ __forceinline__ void next_pair(uint32_t &f0, uint32_t &len0, uint32_t &f1,
+                                              uint32_t &len1) const {
+        const uint32_t row = min(pos >> 5, last_row);
+        const uint32_t lo = stage[row * kLanes];
+        const uint32_t hi = stage[(row + 1) * kLanes];
+        const uint32_t bits = __builtin_amdgcn_alignbit(hi, lo, pos);
+        uint32_t t0 = tb->entry[bits & 255u];
+        uint32_t l0 = t0 & 31u;
+        uint32_t t1 = tb->entry[(bits >> l0) & 255u];
+        uint32_t l1 = t1 & 31u;
+        if (__any(l0 + l1 >= 32u)) {
+            // ESC + 8-bit literal table index (primitives.py:29-35).
+            if (l0 == kEscapeLength) {
+                t0 = tb->escape[(bits >> rare) & 255u];
+                l0 = static_cast<uint32_t>(rare) + 8u;
+                t1 = tb->entry[(bits >> l0) & 255u];
+                l1 = t1 & 31u;
+            }
+            if (l1 == kEscapeLength) {
+                t1 = tb->escape[(bits >> (l0 + static_cast<uint32_t>(rare))) & 255u];
+                l1 = static_cast<uint32_t>(rare) + 8u;
+            }
+        }
+        f0 = t0;
+        f1 = t1;
+        len0 = l0;
+        len1 = l1;
+    }
+};
+
+// Exponent field of an overflow tail byte int8(e - 127).
+__device__ __forceinline__ uint32_t tail_field(uint32_t byte) {
+    return ((byte + 127u) & 255u) << 7;
+}
+
+}  // namespace lct

@@ -1,0 +1,129 @@
+// Device-side helpers shared by the gfx950 codec kernels.
+//
+// Format facts used throughout (LCT/kernels/generic/layout.py:15-18,
+// LCT/kernels/primitives.py:7-36, LCT/kernels/common/tables.py:53-118):
+//  * storage row r = k*S + t, lane l  <->  logical r*256 + (l ^ (r & 254));
+//    rows 2j and 2j+1 share the XOR mask, so one step pair uses one column;
+//  * a BF16 value b splits into exponent byte (b >> 7) & 255 and side byte
+//    (b & 0x7F) | ((b >> 8) & 0x80);
+//  * Huffman table index 0 is exact zero; other indices are centred exponent
+//    deltas with the zero delta removed.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/lct.h"
+
+namespace lct {
+
+constexpr int kLanes = 256;     // streams per codec block (= threads per workgroup)
+constexpr int kWave = 64;
+constexpr int kWavesPerBlock = kLanes / kWave;
+constexpr int kMaxWords = 64;   // largest fixed payload per stream accepted
+constexpr int kEscapeLength = 31;  // decode-table length field marking an escape
+
+// Unbiased exponent of Huffman table index `symbol` under `center`
+// (tables.py:109-116, primitives.py:29-35).
+__device__ __forceinline__ int32_t index_to_exponent(int32_t symbol, int32_t center) {
+    const int32_t zero_delta = (-127 - center) & 255;
+    int32_t delta = symbol - (symbol <= zero_delta ? 1 : 0);
+    delta = delta >= 128 ? delta - 256 : delta;
+    return symbol == 0 ? -127 : delta + center;
+}
+
+// Table index of a raw exponent byte under `center` (tables.py:53-67).
+__device__ __forceinline__ int32_t byte_to_index(int32_t raw, int32_t center) {
+    const int32_t zero_delta = (-127 - center) & 255;
+    const int32_t exp = raw - 127;
+    const int32_t delta = (exp - center) & 255;
+    return exp == -127 ? 0 : delta + (delta < zero_delta ? 1 : 0);
+}
+
+// Side byte -> its bits in BF16 position: sign to bit 15, mantissa to 0..6.
+// sm * 257 copies the byte into bits 8..15; the mask keeps bit 15 and 0..6.
+__device__ __forceinline__ uint32_t side_bits(uint32_t sm) {
+    return (sm * 257u) & 0x807Fu;
+}
+
+// BF16 bits from an exponent field already at bits 7..14 and a side byte.
+__device__ __forceinline__ uint32_t join_bf16(uint32_t exponent_field, uint32_t sm) {
+    return (exponent_field & 0x7F80u) | side_bits(sm);
+}
+
+__device__ __forceinline__ uint32_t side_byte_of(uint32_t bits) {
+    return (bits & 0x7Fu) | ((bits >> 8) & 0x80u);
+}
+
+__device__ __forceinline__ float bf16_to_float(uint32_t bits) {
+    return __uint_as_float(bits << 16);
+}
+
+// FP32 -> BF16, round to nearest even; NaN becomes the canonical 0x7FFF.
+__device__ __forceinline__ uint32_t float_to_bf16(float value) {
+    uint32_t u = __float_as_uint(value);
+    const bool nan = (u & 0x7FFFFFFFu) > 0x7F800000u;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return nan ? 0x7FFFu : (u >> 16);
+}
+
+__device__ __forceinline__ int wave_lane() { return threadIdx.x & (kWave - 1); }
+
+__device__ __forceinline__ int32_t wave_sum(int32_t v) {
+#pragma unroll
+    for (int offset = kWave / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+    return v;
+}
+
+__device__ __forceinline__ int32_t wave_min(int32_t v) {
+#pragma unroll
+    for (int offset = kWave / 2; offset > 0; offset >>= 1) v = min(v, __shfl_xor(v, offset, kWave));
+    return v;
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave.
+__device__ __forceinline__ int32_t wave_inclusive_scan(int32_t v) {
+    const int lane = wave_lane();
+#pragma unroll
+    for (int offset = 1; offset < kWave; offset <<= 1) {
+        const int32_t other = __shfl_up(v, offset, kWave);
+        if (lane >= offset) v += other;
+    }
+    return v;
+}
+
+// Exclusive prefix sum over the 256 threads of a block; returns the total in
+// *total.  `scratch` holds kWavesPerBlock ints of LDS.  Contains barriers.
+__device__ __forceinline__ int32_t block_exclusive_scan(int32_t v, int32_t *scratch, int32_t *total) {
+    const int wave = threadIdx.x / kWave;
+    const int32_t inclusive = wave_inclusive_scan(v);
+    if (wave_lane() == kWave - 1) scratch[wave] = inclusive;
+    __syncthreads();
+    int32_t before = 0, sum = 0;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) {
+        const int32_t s = scratch[w];
+        before += w < wave ? s : 0;
+        sum += s;
+    }
+    __syncthreads();
+    *total = sum;
+    return before + inclusive - v;
+}
+
+__device__ __forceinline__ int32_t block_sum(int32_t v, int32_t *scratch) {
+    int32_t total;
+    block_exclusive_scan(v, scratch, &total);
+    return total;
+}
+
+// Geometry check shared by every entry point.
+inline bool geometry_ok(const lct_geometry &g) {
+    // Every geometry of LCT/codec/geometry.py:13-39 (and the legacy layout of
+    // LCT/comp_tensor.py:50-54) has 128 or 256 steps.
+    return g.lanes == kLanes && (g.steps == 128 || g.steps == 256)
+        && g.block_symbols == g.lanes * g.steps && g.fixed_words >= 2
+        && g.fixed_words <= kMaxWords;
+}
+
+}  // namespace lct

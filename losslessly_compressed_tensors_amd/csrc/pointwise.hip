@@ -1,0 +1,349 @@
+// Fused pointwise operations on compressed BF16 operands (gfx950).
+//
+// lct_pointwise_dense: decode one compressed operand, combine it with a dense
+// BF16 operand and emit dense BF16 or the split components a re-encode
+// consumes (LCT/kernels/generic/pointwise.py:84-337).  The reference runs a
+// second "fallback" kernel over overflow rows; here the overflow tails are
+// overlaid during the same pass, which gives identical results.
+//
+// lct_dual: alpha * A + B with both operands compressed in the same geometry
+// (LCT/kernels/generic/pointwise_scalar_dual.py:17-346); the reference's
+// per-stream map kernels are folded into each workgroup's prologue.
+//
+// Arithmetic (pointwise.py:340-363, _store_result :43-65): operands are
+// widened to FP32; add and multiply round once; scalar_mul_add uses FP32
+// fma(a, alpha, b) (b pre-scaled by beta in FP32 when beta is given, or
+// fma(b, beta, a) when alpha is one); the result is rounded to BF16 to
+// nearest-even.  Compressed output: side byte at the storage offset (0 for
+// padding), exponent byte at the logical offset.
+#include "decode_core.h"
+
+namespace lct {
+namespace {
+
+struct OpParams {
+    int32_t op;
+    int32_t alpha_is_one;
+    int32_t beta_is_one;
+    float alpha;
+    float beta;
+};
+
+__device__ __forceinline__ uint32_t apply_op(const OpParams &p, uint32_t left, uint32_t right) {
+    const float a = bf16_to_float(left);
+    float b = bf16_to_float(right);
+    float r;
+    if (p.op == LCT_OP_ADD) {
+        r = a + b;
+    } else if (p.op == LCT_OP_MULTIPLY) {
+        r = a * b;
+    } else if (p.alpha_is_one) {
+        r = p.beta_is_one ? a + b : __builtin_fmaf(b, p.beta, a);
+    } else {
+        if (!p.beta_is_one) b = b * p.beta;
+        r = __builtin_fmaf(a, p.alpha, b);
+    }
+    return float_to_bf16(r);
+}
+
+// Emits one result.  Dense: bf16 at the logical offset.  Compressed: side byte
+// at the storage slot (0 when the position is padding) and exponent byte at
+// the logical offset.
+template <int kPolicy>
+__device__ __forceinline__ void store_result(uint32_t bits, bool logical_valid, uint32_t slot,
+                                             uint32_t logical, uint16_t *dense_block,
+                                             uint8_t *side_out_block, uint8_t *exp_out_block) {
+    if (kPolicy == LCT_DENSE_OUTPUT) {
+        if (logical_valid) dense_block[logical] = static_cast<uint16_t>(bits);
+    } else {
+        bits = logical_valid ? bits : 0u;
+        side_out_block[slot] = static_cast<uint8_t>(side_byte_of(bits));
+        if (logical_valid) exp_out_block[logical] = static_cast<uint8_t>((bits >> 7) & 0xFFu);
+    }
+}
+
+// Overlay one lane's pair if it is at/after its overflow start.
+__device__ __forceinline__ void overlay_pair(const LaneOverlay &lane, int step, uint32_t &f0,
+                                             uint32_t &len0, uint32_t &f1, uint32_t &len1) {
+    if (step >= lane.wave_start) {
+        if (step >= lane.start) {
+            const uint8_t *src = lane.tail + lane.offset + (step - lane.start);
+            f0 = tail_field(src[0]);
+            f1 = tail_field(src[1]);
+            len0 = 0;
+            len1 = 0;
+        }
+    }
+}
+
+template <bool kFull, int S, int kPolicy>
+__device__ __forceinline__ void pointwise_rows(const StreamCursor &cursor_in, const LaneOverlay &lane,
+                                               const uint8_t *__restrict__ side_block,
+                                               const uint16_t *__restrict__ other_block,
+                                               uint16_t *dense_block, uint8_t *side_out_block,
+                                               uint8_t *exp_out_block, int64_t row_base,
+                                               int64_t valid_in_block, const OpParams &p) {
+    StreamCursor cursor = cursor_in;
+    const uint32_t t = threadIdx.x;
+#pragma unroll 2
+    for (int step = 0; step < S; step += 2) {
+        uint32_t f0, len0, f1, len1;
+        cursor.next_pair(f0, len0, f1, len1);
+        const uint32_t slot = static_cast<uint32_t>(step) * kLanes + t;
+        const uint32_t sm0 = side_block[slot];
+        const uint32_t sm1 = side_block[slot + kLanes];
+        overlay_pair(lane, step, f0, len0, f1, len1);
+        const uint32_t col = t ^ static_cast<uint32_t>((row_base + step) & 254);
+        const uint32_t off0 = static_cast<uint32_t>(step) * kLanes + col;
+        const uint32_t off1 = off0 + kLanes;
+        bool v0 = true, v1 = true;
+        if (!kFull) {
+            v0 = off0 < valid_in_block;
+            v1 = off1 < valid_in_block;
+            len0 = v0 ? len0 : 0u;
+            len1 = v1 ? len1 : 0u;
+        }
+        cursor.pos += len0 + len1;
+        const uint32_t b0 = v0 ? other_block[off0] : 0u;
+        const uint32_t b1 = v1 ? other_block[off1] : 0u;
+        const uint32_t r0 = apply_op(p, join_bf16(f0, sm0), b0);
+        const uint32_t r1 = apply_op(p, join_bf16(f1, sm1), b1);
+        store_result<kPolicy>(r0, v0, slot, off0, dense_block, side_out_block, exp_out_block);
+        store_result<kPolicy>(r1, v1, slot + kLanes, off1, dense_block, side_out_block,
+                              exp_out_block);
+    }
+}
+
+__global__ __launch_bounds__(kLanes) void pointwise_kernel(
+    const int32_t *__restrict__ encoded, const uint8_t *__restrict__ side,
+    const uint16_t *__restrict__ other, void *output, uint8_t *auxiliary,
+    const int32_t *__restrict__ shifted_decode, const int32_t *__restrict__ center_ptr,
+    const float *__restrict__ alpha, const float *__restrict__ beta, int64_t n_blocks,
+    int64_t logical_numel, int S, int W, int rare, int op, int alpha_is_one, int beta_is_one,
+    int policy, lct_overflow ov, int has_overlay) {
+    extern __shared__ uint32_t stage[];
+    __shared__ DecodeTables tb;
+    __shared__ int32_t map_start[kLanes], map_offset[kLanes], scratch[kWavesPerBlock];
+    const int64_t block = blockIdx.x;
+    build_decode_tables(tb, shifted_decode, center_ptr[0]);
+    stage_payload(stage, encoded, n_blocks * kLanes, block, W);
+    const LaneOverlay lane = build_overlay(ov, has_overlay != 0, block, n_blocks, S, map_start,
+                                           map_offset, scratch);
+    __syncthreads();
+
+    OpParams p{op, alpha_is_one, beta_is_one, 1.0f, 1.0f};
+    if (op == LCT_OP_SCALAR_MUL_ADD) {
+        if (!alpha_is_one) p.alpha = alpha[0];
+        if (!beta_is_one) p.beta = beta[0];
+    }
+    const StreamCursor cursor{stage + threadIdx.x, &tb, 0u, static_cast<uint32_t>(W), rare};
+    const int64_t row_base = block * S;
+    const int64_t logical_base = row_base * kLanes;
+    const uint8_t *side_block = side + logical_base;
+    const uint16_t *other_block = other + logical_base;
+    uint16_t *dense_block = static_cast<uint16_t *>(output) + logical_base;
+    uint8_t *side_out_block = static_cast<uint8_t *>(output) + logical_base;
+    uint8_t *exp_out_block = auxiliary + logical_base;
+    const int64_t valid = logical_numel - logical_base;
+    const bool full = valid >= static_cast<int64_t>(S) * kLanes;
+#define LCT_POINTWISE_CASE(FULL, POLICY)                                                       \
+    if (S == 128)                                                                              \
+        pointwise_rows<FULL, 128, POLICY>(cursor, lane, side_block, other_block, dense_block, \
+                                          side_out_block, exp_out_block, row_base, valid, p);  \
+    else                                                                                       \
+        pointwise_rows<FULL, 256, POLICY>(cursor, lane, side_block, other_block, dense_block, \
+                                          side_out_block, exp_out_block, row_base, valid, p);
+    if (policy == LCT_DENSE_OUTPUT) {
+        if (full) { LCT_POINTWISE_CASE(true, LCT_DENSE_OUTPUT) }
+        else { LCT_POINTWISE_CASE(false, LCT_DENSE_OUTPUT) }
+    } else {
+        if (full) { LCT_POINTWISE_CASE(true, LCT_COMPRESSED_OUTPUT) }
+        else { LCT_POINTWISE_CASE(false, LCT_COMPRESSED_OUTPUT) }
+    }
+#undef LCT_POINTWISE_CASE
+}
+
+template <bool kFull, int S, int kPolicy>
+__device__ __forceinline__ void dual_rows(const StreamCursor &a_in, const LaneOverlay &a_lane,
+                                          const uint8_t *__restrict__ a_side,
+                                          const StreamCursor &b_in, const LaneOverlay &b_lane,
+                                          const uint8_t *__restrict__ b_side, uint16_t *dense_block,
+                                          uint8_t *side_out_block, uint8_t *exp_out_block,
+                                          int64_t row_base, int64_t valid_in_block, float alpha) {
+    StreamCursor a = a_in, b = b_in;
+    const uint32_t t = threadIdx.x;
+#pragma unroll 2
+    for (int step = 0; step < S; step += 2) {
+        uint32_t af0, alen0, af1, alen1, bf0, blen0, bf1, blen1;
+        a.next_pair(af0, alen0, af1, alen1);
+        b.next_pair(bf0, blen0, bf1, blen1);
+        const uint32_t slot = static_cast<uint32_t>(step) * kLanes + t;
+        const uint32_t asm0 = a_side[slot], asm1 = a_side[slot + kLanes];
+        const uint32_t bsm0 = b_side[slot], bsm1 = b_side[slot + kLanes];
+        overlay_pair(a_lane, step, af0, alen0, af1, alen1);
+        overlay_pair(b_lane, step, bf0, blen0, bf1, blen1);
+        const uint32_t col = t ^ static_cast<uint32_t>((row_base + step) & 254);
+        const uint32_t off0 = static_cast<uint32_t>(step) * kLanes + col;
+        const uint32_t off1 = off0 + kLanes;
+        bool v0 = true, v1 = true;
+        if (!kFull) {
+            v0 = off0 < valid_in_block;
+            v1 = off1 < valid_in_block;
+            alen0 = v0 ? alen0 : 0u;
+            alen1 = v1 ? alen1 : 0u;
+            blen0 = v0 ? blen0 : 0u;
+            blen1 = v1 ? blen1 : 0u;
+        }
+        a.pos += alen0 + alen1;
+        b.pos += blen0 + blen1;
+        const uint32_t r0 = float_to_bf16(__builtin_fmaf(bf16_to_float(join_bf16(af0, asm0)), alpha,
+                                                         bf16_to_float(join_bf16(bf0, bsm0))));
+        const uint32_t r1 = float_to_bf16(__builtin_fmaf(bf16_to_float(join_bf16(af1, asm1)), alpha,
+                                                         bf16_to_float(join_bf16(bf1, bsm1))));
+        store_result<kPolicy>(r0, v0, slot, off0, dense_block, side_out_block, exp_out_block);
+        store_result<kPolicy>(r1, v1, slot + kLanes, off1, dense_block, side_out_block,
+                              exp_out_block);
+    }
+}
+
+struct DualOperand {
+    const int32_t *encoded;
+    const uint8_t *side;
+    const int32_t *shifted_decode;
+    const int32_t *center;
+    lct_overflow ov;
+    int32_t has_overlay;
+};
+
+__global__ __launch_bounds__(kLanes) void dual_kernel(DualOperand a, DualOperand b,
+                                                      const float *__restrict__ alpha,
+                                                      void *output, uint8_t *auxiliary,
+                                                      int64_t n_blocks, int64_t logical_numel,
+                                                      int S, int W, int rare, int policy) {
+    extern __shared__ uint32_t stage[];   // two stages of (W + 2) rows x 256
+    __shared__ DecodeTables tb_a, tb_b;
+    __shared__ int32_t map_start[kLanes], map_offset[kLanes], scratch[kWavesPerBlock];
+    const int64_t block = blockIdx.x;
+    uint32_t *stage_a = stage;
+    uint32_t *stage_b = stage + (W + 2) * kLanes;
+    build_decode_tables(tb_a, a.shifted_decode, a.center[0]);
+    build_decode_tables(tb_b, b.shifted_decode, b.center[0]);
+    stage_payload(stage_a, a.encoded, n_blocks * kLanes, block, W);
+    stage_payload(stage_b, b.encoded, n_blocks * kLanes, block, W);
+    const LaneOverlay a_lane = build_overlay(a.ov, a.has_overlay != 0, block, n_blocks, S,
+                                             map_start, map_offset, scratch);
+    __syncthreads();
+    const LaneOverlay b_lane = build_overlay(b.ov, b.has_overlay != 0, block, n_blocks, S,
+                                             map_start, map_offset, scratch);
+    __syncthreads();
+
+    const float alpha_value = alpha[0];
+    const StreamCursor ca{stage_a + threadIdx.x, &tb_a, 0u, static_cast<uint32_t>(W), rare};
+    const StreamCursor cb{stage_b + threadIdx.x, &tb_b, 0u, static_cast<uint32_t>(W), rare};
+    const int64_t row_base = block * S;
+    const int64_t logical_base = row_base * kLanes;
+    uint16_t *dense_block = static_cast<uint16_t *>(output) + logical_base;
+    uint8_t *side_out_block = static_cast<uint8_t *>(output) + logical_base;
+    uint8_t *exp_out_block = auxiliary + logical_base;
+    const uint8_t *a_side = a.side + logical_base;
+    const uint8_t *b_side = b.side + logical_base;
+    const int64_t valid = logical_numel - logical_base;
+    const bool full = valid >= static_cast<int64_t>(S) * kLanes;
+#define LCT_DUAL_CASE(FULL, POLICY)                                                             \
+    if (S == 128)                                                                               \
+        dual_rows<FULL, 128, POLICY>(ca, a_lane, a_side, cb, b_lane, b_side, dense_block,      \
+                                     side_out_block, exp_out_block, row_base, valid,           \
+                                     alpha_value);                                             \
+    else                                                                                        \
+        dual_rows<FULL, 256, POLICY>(ca, a_lane, a_side, cb, b_lane, b_side, dense_block,      \
+                                     side_out_block, exp_out_block, row_base, valid,           \
+                                     alpha_value);
+    if (policy == LCT_DENSE_OUTPUT) {
+        if (full) { LCT_DUAL_CASE(true, LCT_DENSE_OUTPUT) }
+        else { LCT_DUAL_CASE(false, LCT_DENSE_OUTPUT) }
+    } else {
+        if (full) { LCT_DUAL_CASE(true, LCT_COMPRESSED_OUTPUT) }
+        else { LCT_DUAL_CASE(false, LCT_COMPRESSED_OUTPUT) }
+    }
+#undef LCT_DUAL_CASE
+}
+
+int32_t check_overflow(const lct_overflow *o) {
+    if (o == nullptr) return LCT_OK;
+    if (!o->lanes || !o->starts || !o->tail || !o->blocks) return LCT_E_NULL;
+    if (o->descriptor != nullptr && o->count == nullptr) return LCT_E_NULL;
+    return LCT_OK;
+}
+
+int32_t check_sizes(int64_t size, int64_t logical_numel, const lct_geometry &g) {
+    if (!geometry_ok(g)) return LCT_E_GEOMETRY;
+    if (logical_numel <= 0 || size <= 0 || size % g.block_symbols != 0 || logical_numel > size
+        || logical_numel <= size - g.block_symbols || size / g.block_symbols > 0x7FFFFFFF)
+        return LCT_E_SIZE;
+    return LCT_OK;
+}
+
+}  // namespace
+}  // namespace lct
+
+using namespace lct;
+
+extern "C" int32_t lct_pointwise_dense(const int32_t *encoded, const uint8_t *side,
+                                       const void *other, void *output, uint8_t *auxiliary,
+                                       const int32_t *shifted_decode, const int32_t *center,
+                                       const float *alpha, const float *beta, int64_t size,
+                                       int64_t logical_numel, lct_geometry g,
+                                       int32_t rare_length, int32_t op, int32_t alpha_is_one,
+                                       int32_t beta_is_one, int32_t output_policy,
+                                       const lct_overflow *overflow, hipStream_t stream) {
+    if (!encoded || !side || !other || !output || !shifted_decode || !center) return LCT_E_NULL;
+    if (output_policy == LCT_COMPRESSED_OUTPUT && !auxiliary) return LCT_E_NULL;
+    if (op == LCT_OP_SCALAR_MUL_ADD && ((!alpha_is_one && !alpha) || (!beta_is_one && !beta)))
+        return LCT_E_NULL;
+    if (int32_t e = check_sizes(size, logical_numel, g)) return e;
+    if (int32_t e = check_overflow(overflow)) return e;
+    if (op < LCT_OP_ADD || op > LCT_OP_SCALAR_MUL_ADD) return LCT_E_ARG;
+    if (output_policy != LCT_DENSE_OUTPUT && output_policy != LCT_COMPRESSED_OUTPUT) return LCT_E_ARG;
+    if (rare_length < 0 || rare_length > 8) return LCT_E_ARG;
+    if ((reinterpret_cast<uintptr_t>(encoded) & 15) != 0) return LCT_E_ARG;
+    const lct_overflow ov = overflow ? *overflow : lct_overflow{};
+    const int64_t n_blocks = size / g.block_symbols;
+    const size_t lds = static_cast<size_t>(g.fixed_words + 2) * kLanes * sizeof(uint32_t);
+    hipLaunchKernelGGL(pointwise_kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes), lds,
+                       stream, encoded, side, static_cast<const uint16_t *>(other), output,
+                       auxiliary, shifted_decode, center, alpha, beta, n_blocks, logical_numel,
+                       g.steps, g.fixed_words, rare_length, op, alpha_is_one, beta_is_one,
+                       output_policy, ov, overflow != nullptr ? 1 : 0);
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_dual(const int32_t *a_encoded, const uint8_t *a_side,
+                            const int32_t *a_shifted_decode, const int32_t *a_center,
+                            const lct_overflow *a_overflow, const int32_t *b_encoded,
+                            const uint8_t *b_side, const int32_t *b_shifted_decode,
+                            const int32_t *b_center, const lct_overflow *b_overflow,
+                            const float *alpha, void *output, uint8_t *auxiliary, int64_t size,
+                            int64_t logical_numel, lct_geometry g, int32_t rare_length,
+                            int32_t output_policy, hipStream_t stream) {
+    if (!a_encoded || !a_side || !a_shifted_decode || !a_center || !b_encoded || !b_side
+        || !b_shifted_decode || !b_center || !alpha || !output)
+        return LCT_E_NULL;
+    if (output_policy == LCT_COMPRESSED_OUTPUT && !auxiliary) return LCT_E_NULL;
+    if (int32_t e = check_sizes(size, logical_numel, g)) return e;
+    if (int32_t e = check_overflow(a_overflow)) return e;
+    if (int32_t e = check_overflow(b_overflow)) return e;
+    if (output_policy != LCT_DENSE_OUTPUT && output_policy != LCT_COMPRESSED_OUTPUT) return LCT_E_ARG;
+    if (rare_length < 0 || rare_length > 8) return LCT_E_ARG;
+    if (((reinterpret_cast<uintptr_t>(a_encoded) | reinterpret_cast<uintptr_t>(b_encoded)) & 15) != 0)
+        return LCT_E_ARG;
+    const DualOperand a{a_encoded, a_side, a_shifted_decode, a_center,
+                        a_overflow ? *a_overflow : lct_overflow{}, a_overflow != nullptr};
+    const DualOperand b{b_encoded, b_side, b_shifted_decode, b_center,
+                        b_overflow ? *b_overflow : lct_overflow{}, b_overflow != nullptr};
+    const int64_t n_blocks = size / g.block_symbols;
+    const size_t lds = 2 * static_cast<size_t>(g.fixed_words + 2) * kLanes * sizeof(uint32_t);
+    hipLaunchKernelGGL(dual_kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes), lds,
+                       stream, a, b, alpha, output, auxiliary, n_blocks, logical_numel, g.steps,
+                       g.fixed_words, rare_length, output_policy);
+    return static_cast<int32_t>(hipGetLastError());
+}

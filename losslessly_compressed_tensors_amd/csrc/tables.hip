@@ -1,0 +1,121 @@
+// Center estimation and center-shifted Huffman tables (one workgroup).
+//
+// Follows LCT/kernels/common/tables.py:9-128: the center is the mean unbiased
+// exponent of min(n, 4096) hashed sample positions (one jittered position per
+// equal-width region, exponents below -120 excluded), rounded half away from
+// zero and clamped to [-128, 127]; the encode table is re-indexed by raw
+// exponent byte and the decode table stores exponents instead of indices.
+#include "lct_device.h"
+
+namespace lct {
+namespace {
+
+constexpr int kMaxSamples = 4096;
+
+__global__ __launch_bounds__(kLanes) void tables_kernel(
+    const void *__restrict__ source, int32_t precomputed, int64_t logical_numel,
+    int64_t sample_size, const int32_t *__restrict__ base_encode,
+    const int32_t *__restrict__ base_decode, int32_t *__restrict__ center_io,
+    int32_t estimate, int32_t *__restrict__ shifted_encode,
+    int32_t *__restrict__ shifted_decode) {
+    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ int32_t shared_center;
+    const int t = threadIdx.x;
+    int32_t center;
+    if (estimate) {
+        int32_t sum = 0, kept = 0;
+        for (int64_t i = t; i < sample_size; i += kLanes) {
+            const uint32_t hashed = static_cast<uint32_t>(i) * 0x9E3779B9u;
+            const int64_t start = i * logical_numel / sample_size;
+            const int64_t end = (i + 1) * logical_numel / sample_size;
+            const uint64_t jitter =
+                (static_cast<uint64_t>(hashed) * static_cast<uint64_t>(end - start)) >> 32;
+            const int64_t pos = start + static_cast<int64_t>(jitter);
+            int32_t exp;
+            if (precomputed) {
+                exp = static_cast<int32_t>(static_cast<const uint8_t *>(source)[pos]) - 127;
+            } else {
+                const int32_t bits = static_cast<const int16_t *>(source)[pos];
+                exp = ((bits >> 7) & 0xFF) - 127;
+            }
+            if (exp >= -120) {
+                sum += exp;
+                kept += 1;
+            }
+        }
+        const int32_t total = block_sum(sum, scratch);
+        const int32_t count = block_sum(kept, scratch);
+        if (t == 0) {
+            int32_t c = 0;
+            if (count > 0) {
+                c = total >= 0 ? (total + count / 2) / count
+                               : -((-total + count / 2) / count);
+                c = min(max(c, -128), 127);
+            }
+            center_io[0] = c;
+            shared_center = c;
+        }
+        __syncthreads();
+        center = shared_center;
+    } else {
+        center = center_io[0];
+    }
+
+    if (shifted_encode != nullptr) {
+        shifted_encode[t] = base_encode[byte_to_index(t, center)];
+    }
+    if (shifted_decode != nullptr) {
+#pragma unroll
+        for (int i = t; i < 1024; i += kLanes) {
+            const int32_t packed = base_decode[i];
+            const int32_t length = packed & 255;
+            const int32_t exponent = index_to_exponent((packed >> 8) & 255, center);
+            shifted_decode[i] = length == 0
+                ? 0 : static_cast<int32_t>(static_cast<uint32_t>(length)
+                                           | (static_cast<uint32_t>(exponent) << 8));
+        }
+    }
+}
+
+}  // namespace
+}  // namespace lct
+
+using namespace lct;
+
+extern "C" int32_t lct_estimate_and_shift_tables(
+    const void *source, int32_t precomputed, int64_t logical_numel,
+    int64_t sample_size, const int32_t *base_encode, const int32_t *base_decode,
+    int32_t *center, int32_t *shifted_encode, int32_t *shifted_decode,
+    hipStream_t stream) {
+    if (!source || !base_encode || !base_decode || !center || !shifted_encode || !shifted_decode)
+        return LCT_E_NULL;
+    if (logical_numel <= 0 || sample_size <= 0 || sample_size > kMaxSamples
+        || sample_size > logical_numel)
+        return LCT_E_SIZE;
+    hipLaunchKernelGGL(tables_kernel, dim3(1), dim3(kLanes), 0, stream, source,
+                       precomputed, logical_numel, sample_size, base_encode,
+                       base_decode, center, 1, shifted_encode, shifted_decode);
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_shift_tables(const int32_t *base_encode, const int32_t *center,
+                                    int32_t *shifted_encode, const int32_t *base_decode,
+                                    int32_t *shifted_decode, hipStream_t stream) {
+    if (!base_encode || !center || !shifted_encode || !base_decode || !shifted_decode)
+        return LCT_E_NULL;
+    hipLaunchKernelGGL(tables_kernel, dim3(1), dim3(kLanes), 0, stream, nullptr, 0,
+                       int64_t{0}, int64_t{0}, base_encode, base_decode,
+                       const_cast<int32_t *>(center), 0, shifted_encode, shifted_decode);
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_shift_decoding_table(const int32_t *base_decode,
+                                            const int32_t *center,
+                                            int32_t *shifted_decode,
+                                            hipStream_t stream) {
+    if (!base_decode || !center || !shifted_decode) return LCT_E_NULL;
+    hipLaunchKernelGGL(tables_kernel, dim3(1), dim3(kLanes), 0, stream, nullptr, 0,
+                       int64_t{0}, int64_t{0}, nullptr, base_decode,
+                       const_cast<int32_t *>(center), 0, nullptr, shifted_decode);
+    return static_cast<int32_t>(hipGetLastError());
+}

@@ -1,0 +1,98 @@
+// TensorBuffer allocator kernels: reset, allocate, free (one workgroup each).
+//
+// Launch-for-launch replacements of LCT/kernels/tensor_buffer.py:18-34
+// (_reset_kernel), :37-91 (_allocate_kernel) and :182-192
+// (_free_storage_kernel); the algorithms live in allocator.h.
+#include "allocator.h"
+
+namespace lct {
+namespace {
+
+__global__ __launch_bounds__(kLanes) void buffer_reset_kernel(int32_t *__restrict__ meta,
+                                                              int32_t regions,
+                                                              int32_t capacity) {
+    const AllocatorMeta m(meta, regions);
+    for (int32_t i = threadIdx.x; i < regions; i += kLanes) {
+        m.starts[i] = 0;
+        m.sizes[i] = i == 0 ? capacity : 0;
+    }
+    if (threadIdx.x == 0) {
+        *m.count = 1;
+        *m.lock = 0;
+        *m.generation = *m.generation + 1;
+    }
+}
+
+__global__ __launch_bounds__(kLanes) void buffer_allocate_kernel(
+    int32_t *__restrict__ meta, int32_t regions, const int32_t *__restrict__ requested,
+    const int32_t *__restrict__ item_count, int32_t item_bytes,
+    int32_t *__restrict__ descriptor) {
+    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ int32_t flag;
+    int32_t request = requested[0];
+    if (item_bytes) request += item_count[0] * item_bytes;
+    allocator_allocate(AllocatorMeta(meta, regions), request, descriptor, scratch, &flag);
+}
+
+__global__ __launch_bounds__(kLanes) void buffer_free_kernel(int32_t *__restrict__ meta,
+                                                             int32_t regions,
+                                                             int32_t *__restrict__ descriptor,
+                                                             int32_t *__restrict__ status_out) {
+    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ int32_t flag;
+    const int32_t status = allocator_free(AllocatorMeta(meta, regions), descriptor, scratch, &flag);
+    if (threadIdx.x == 0) status_out[0] = status;
+}
+
+bool regions_ok(int32_t r) { return r > 0 && r <= 4096 && (r & (r - 1)) == 0; }
+
+}  // namespace
+}  // namespace lct
+
+using namespace lct;
+
+extern "C" int32_t lct_buffer_reset(int32_t *meta, int32_t max_free_regions,
+                                    int32_t capacity_bytes, hipStream_t stream) {
+    if (!meta) return LCT_E_NULL;
+    if (!regions_ok(max_free_regions) || capacity_bytes < 0) return LCT_E_ARG;
+    hipLaunchKernelGGL(buffer_reset_kernel, dim3(1), dim3(kLanes), 0, stream, meta,
+                       max_free_regions, capacity_bytes);
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_buffer_allocate(int32_t *meta, int32_t max_free_regions,
+                                       const int32_t *requested, const int32_t *item_count,
+                                       int32_t item_bytes, int32_t *descriptor,
+                                       hipStream_t stream) {
+    if (!meta || !requested || !descriptor) return LCT_E_NULL;
+    if (item_bytes != 0 && !item_count) return LCT_E_NULL;
+    if (!regions_ok(max_free_regions) || item_bytes < 0) return LCT_E_ARG;
+    hipLaunchKernelGGL(buffer_allocate_kernel, dim3(1), dim3(kLanes), 0, stream, meta,
+                       max_free_regions, requested, item_count, item_bytes, descriptor);
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_buffer_free(int32_t *meta, int32_t max_free_regions,
+                                   int32_t *descriptor, int32_t *status_out,
+                                   hipStream_t stream) {
+    if (!meta || !descriptor || !status_out) return LCT_E_NULL;
+    if (!regions_ok(max_free_regions)) return LCT_E_ARG;
+    hipLaunchKernelGGL(buffer_free_kernel, dim3(1), dim3(kLanes), 0, stream, meta,
+                       max_free_regions, descriptor, status_out);
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" const char *lct_version(void) { return "lct-hip-gfx950 0.1"; }
+
+extern "C" const char *lct_error_string(int32_t code) {
+    switch (code) {
+        case LCT_OK: return "ok";
+        case LCT_E_NULL: return "a required pointer is NULL";
+        case LCT_E_GEOMETRY: return "unsupported stream geometry";
+        case LCT_E_SIZE: return "sizes inconsistent or out of range";
+        case LCT_E_ARG: return "argument out of range";
+        default: break;
+    }
+    if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+    return "unknown error";
+}

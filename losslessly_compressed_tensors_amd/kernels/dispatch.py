@@ -1,0 +1,207 @@
+"""Launch wrappers: one function per codec kernel launch.
+
+Mirrors the reference's operator boundary ``LCT/kernels/dispatch.py``: each
+function takes caller-allocated torch tensors, enqueues exactly one HIP
+kernel on the current stream through ``liblct_hip.so`` and returns nothing
+(except ``shift_decoding_table``, which returns its new table as the
+reference's does).  There is no backend selection: the gfx950 library is the
+only engine.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import hip
+
+# Largest block count the single-workgroup prefix scan handles
+# (LCT/kernels/autotune.py:54).
+SUMMARY_BLOCK_LIMIT = 8192
+
+
+def _ptr(tensor: torch.Tensor | None):
+    return None if tensor is None else tensor.data_ptr()
+
+
+def _stream(tensor: torch.Tensor) -> int:
+    return torch.cuda.current_stream(tensor.device).cuda_stream
+
+
+def _require_device(*tensors: torch.Tensor) -> None:
+    for tensor in tensors:
+        if tensor is not None and tensor.device.type != "cuda":
+            raise ValueError(f"LCT kernels require GPU tensors, got {tensor.device}")
+
+
+@dataclass
+class FallbackStorage:
+    """Overflow lanes/starts/tails of one tensor (``LCT/kernels/backends.py:36-50``).
+
+    Buffered storage has ``descriptor`` set and all three arrays pointing at
+    the TensorBuffer arena; private storage has exact-size arrays.
+    """
+
+    tail: torch.Tensor
+    count: torch.Tensor
+    lanes: torch.Tensor
+    starts: torch.Tensor
+    blocks: torch.Tensor
+    descriptor: torch.Tensor | None = None
+    allocation: torch.Tensor | None = None
+    base: int = 0
+
+    @property
+    def buffered(self) -> bool:
+        return self.descriptor is not None
+
+    def as_overflow(self) -> hip.Overflow:
+        return hip.Overflow(
+            _ptr(self.lanes), _ptr(self.starts), _ptr(self.tail), _ptr(self.blocks),
+            _ptr(self.count), _ptr(self.descriptor), int(self.base))
+
+
+# ---------------------------------------------------------------------------
+# Tables (dispatch.py:16-62)
+# ---------------------------------------------------------------------------
+
+
+def shift_encoding_table(encode_table, center, shifted_encode, decode_table,
+                         shifted_decode=None) -> None:
+    """Encode/decode tables for a given device center (``dispatch.py:16-30``)."""
+    _require_device(encode_table, center)
+    if shifted_decode is None:
+        shifted_decode = torch.empty_like(decode_table)
+    hip.call("lct_shift_tables", _ptr(encode_table), _ptr(center), _ptr(shifted_encode),
+             _ptr(decode_table), _ptr(shifted_decode), _stream(encode_table))
+
+
+def estimate_and_shift_encoding_table(source, center, size, encode_table, shifted_encode,
+                                      decode_table, shifted_decode, sample_size,
+                                      precomputed) -> None:
+    """Sample the center from ``source`` and shift both tables (``dispatch.py:33-48``)."""
+    _require_device(source, center)
+    if shifted_decode is None:
+        shifted_decode = torch.empty_like(decode_table)
+    hip.call("lct_estimate_and_shift_tables", _ptr(source), int(bool(precomputed)), int(size),
+             int(sample_size), _ptr(encode_table), _ptr(decode_table), _ptr(center),
+             _ptr(shifted_encode), _ptr(shifted_decode), _stream(source))
+
+
+def shift_decoding_table(decode_table, center) -> torch.Tensor:
+    """Return a center-shifted copy of ``decode_table`` (``dispatch.py:51-62``)."""
+    _require_device(decode_table, center)
+    shifted = torch.empty(1024, dtype=torch.int32, device=decode_table.device)
+    hip.call("lct_shift_decoding_table", _ptr(decode_table), _ptr(center), _ptr(shifted),
+             _stream(decode_table))
+    return shifted
+
+
+# ---------------------------------------------------------------------------
+# Encoder, scans, compaction (dispatch.py:70-130, 294-316)
+# ---------------------------------------------------------------------------
+
+
+def encode_kernel(source, side, encoded, encode_table, extra_starts, summaries, size, streams,
+                  *, precomputed, logical_numel, block_symbols, lanes, steps, fixed_words,
+                  write_summary) -> None:
+    """Field split + fixed-payload encoder (``dispatch.py:294-316``)."""
+    _require_device(source, side, encoded)
+    geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
+    hip.call("lct_encode", _ptr(source), _ptr(side), _ptr(encoded), _ptr(encode_table),
+             _ptr(extra_starts), _ptr(summaries) if write_summary else None, int(size),
+             int(logical_numel), geometry, int(bool(precomputed)), int(bool(write_summary)),
+             _stream(source))
+
+
+def prefix_allocate(summaries, counts, descriptor, buffer, blocks, buffered,
+                    max_free_regions) -> None:
+    """Block scans + optional arena reservation (``dispatch.py:70-85``)."""
+    _require_device(summaries, counts)
+    meta = buffer.storage if buffer is not None else None
+    hip.call("lct_prefix_allocate", _ptr(summaries), _ptr(counts),
+             _ptr(descriptor) if buffered else None, _ptr(meta) if buffered else None,
+             int(blocks), int(bool(buffered)), int(max_free_regions), _stream(summaries))
+
+
+def compact_extra(source, storage: FallbackStorage, n_blocks, n_elements, *, precomputed,
+                  buffered, logical_numel, block_symbols, lanes, steps, extra_starts,
+                  summaries) -> None:
+    """Per-block overflow entries, tails and block metadata (``dispatch.py:113-130``)."""
+    _require_device(source, extra_starts, summaries)
+    geometry = hip.Geometry(block_symbols, lanes, steps, 2)
+    hip.call("lct_compact_extra", _ptr(source), _ptr(storage.lanes), _ptr(storage.starts),
+             _ptr(storage.tail), _ptr(storage.descriptor), _ptr(storage.count),
+             _ptr(storage.blocks), int(storage.base), _ptr(extra_starts), _ptr(summaries),
+             int(n_elements), int(logical_numel), geometry, int(bool(precomputed)),
+             int(bool(buffered)), _stream(source))
+
+
+# ---------------------------------------------------------------------------
+# Decoder and fused pointwise (dispatch.py:168-286, 319-361)
+# ---------------------------------------------------------------------------
+
+
+def decode_kernel(encoded, side, output, shifted_decode, center, size, *, logical_numel,
+                  block_symbols, lanes, steps, fixed_words, rare_length,
+                  overflow: FallbackStorage | None = None) -> None:
+    """Decoder with the overflow overlay fused when ``overflow`` is given."""
+    _require_device(encoded, side, output)
+    geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
+    ov = overflow.as_overflow() if overflow is not None else None
+    hip.call("lct_decode", _ptr(encoded), _ptr(side), _ptr(output), _ptr(shifted_decode),
+             _ptr(center), int(size), int(logical_numel), geometry, int(rare_length),
+             ov if ov is None else hip.ctypes.byref(ov), _stream(encoded))
+
+
+def pointwise_dense(encoded, sign_mantissa, other, output, auxiliary, shifted_decode, size,
+                    center, alpha, beta, *, rare_length, logical_numel, block_symbols, lanes,
+                    steps, fixed_words, output_policy, op, alpha_is_one, beta_is_one,
+                    overflow: FallbackStorage | None = None) -> None:
+    """Decode + op against a dense operand, overflow rows overlaid in the same pass."""
+    _require_device(encoded, sign_mantissa, other, output)
+    geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
+    ov = overflow.as_overflow() if overflow is not None else None
+    hip.call("lct_pointwise_dense", _ptr(encoded), _ptr(sign_mantissa), _ptr(other),
+             _ptr(output), _ptr(auxiliary), _ptr(shifted_decode), _ptr(center), _ptr(alpha),
+             _ptr(beta), int(size), int(logical_numel), geometry, int(rare_length), int(op),
+             int(bool(alpha_is_one)), int(bool(beta_is_one)), int(output_policy),
+             ov if ov is None else hip.ctypes.byref(ov), _stream(encoded))
+
+
+def dual_mapped(a_encoded, a_sign_mantissa, a_shifted_decode, a_center, a_storage,
+                b_encoded, b_sign_mantissa, b_shifted_decode, b_center, b_storage,
+                output, auxiliary, alpha, size, *, rare_length, logical_numel,
+                block_symbols, lanes, steps, fixed_words, output_policy) -> None:
+    """Fused ``alpha * A + B`` over two compressed operands (one launch)."""
+    _require_device(a_encoded, b_encoded, output, alpha)
+    geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
+    a_ov = a_storage.as_overflow() if a_storage is not None else None
+    b_ov = b_storage.as_overflow() if b_storage is not None else None
+    hip.call("lct_dual", _ptr(a_encoded), _ptr(a_sign_mantissa), _ptr(a_shifted_decode),
+             _ptr(a_center), a_ov if a_ov is None else hip.ctypes.byref(a_ov), _ptr(b_encoded),
+             _ptr(b_sign_mantissa), _ptr(b_shifted_decode), _ptr(b_center),
+             b_ov if b_ov is None else hip.ctypes.byref(b_ov), _ptr(alpha), _ptr(output),
+             _ptr(auxiliary), int(size), int(logical_numel), geometry, int(rare_length),
+             int(output_policy), _stream(a_encoded))
+
+
+# ---------------------------------------------------------------------------
+# TensorBuffer allocator (LCT/tensor_buffer.py:93-136, tensor_buffer_ops.py)
+# ---------------------------------------------------------------------------
+
+
+def buffer_reset(storage, max_free_regions, capacity_bytes) -> None:
+    hip.call("lct_buffer_reset", _ptr(storage), int(max_free_regions), int(capacity_bytes),
+             _stream(storage))
+
+
+def buffer_allocate(storage, max_free_regions, requested, item_count, item_bytes,
+                    descriptor) -> None:
+    hip.call("lct_buffer_allocate", _ptr(storage), int(max_free_regions), _ptr(requested),
+             _ptr(item_count), int(item_bytes), _ptr(descriptor), _stream(storage))
+
+
+def buffer_free(storage, max_free_regions, descriptor, status) -> None:
+    hip.call("lct_buffer_free", _ptr(storage), int(max_free_regions), _ptr(descriptor),
+             _ptr(status), _stream(storage))

@@ -1,0 +1,121 @@
+"""ctypes binding of ``liblct_hip.so`` (declared in ``include/lct.h``).
+
+The library is the only compute path: if it is missing, every codec call
+raises.  Tensors cross the boundary as raw device pointers, sizes as int64
+and the current torch stream as the ``hipStream_t`` argument.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().parent.parent / "lib" / "liblct_hip.so"
+
+LCT_OP_ADD = 0
+LCT_OP_MULTIPLY = 1
+LCT_OP_SCALAR_MUL_ADD = 2
+LCT_DENSE_OUTPUT = 0
+LCT_COMPRESSED_OUTPUT = 1
+
+_c_int32 = ctypes.c_int32
+_c_int64 = ctypes.c_int64
+_ptr = ctypes.c_void_p
+
+
+class Geometry(ctypes.Structure):
+    """``lct_geometry``: (block_symbols, lanes, steps, fixed_words)."""
+
+    _fields_ = [
+        ("block_symbols", _c_int32),
+        ("lanes", _c_int32),
+        ("steps", _c_int32),
+        ("fixed_words", _c_int32),
+    ]
+
+
+class Overflow(ctypes.Structure):
+    """``lct_overflow``: one tensor's overflow lanes/starts/tails metadata."""
+
+    _fields_ = [
+        ("lanes", _ptr),
+        ("starts", _ptr),
+        ("tail", _ptr),
+        ("blocks", _ptr),
+        ("count", _ptr),
+        ("descriptor", _ptr),
+        ("base", _c_int64),
+    ]
+
+
+# name -> argument types (all entry points return int32).
+_SIGNATURES = {
+    "lct_estimate_and_shift_tables": [_ptr, _c_int32, _c_int64, _c_int64, _ptr, _ptr, _ptr, _ptr,
+                                      _ptr, _ptr],
+    "lct_shift_tables": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr],
+    "lct_shift_decoding_table": [_ptr, _ptr, _ptr, _ptr],
+    "lct_encode": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64, _c_int64, Geometry, _c_int32,
+                   _c_int32, _ptr],
+    "lct_prefix_allocate": [_ptr, _ptr, _ptr, _ptr, _c_int64, _c_int32, _c_int32, _ptr],
+    "lct_compact_extra": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64, _ptr, _ptr,
+                          _c_int64, _c_int64, Geometry, _c_int32, _c_int32, _ptr],
+    "lct_decode": [_ptr, _ptr, _ptr, _ptr, _ptr, _c_int64, _c_int64, Geometry, _c_int32,
+                   ctypes.POINTER(Overflow), _ptr],
+    "lct_pointwise_dense": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64,
+                            _c_int64, Geometry, _c_int32, _c_int32, _c_int32, _c_int32, _c_int32,
+                            ctypes.POINTER(Overflow), _ptr],
+    "lct_dual": [_ptr, _ptr, _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _ptr, _ptr,
+                 ctypes.POINTER(Overflow), _ptr, _ptr, _ptr, _c_int64, _c_int64, Geometry,
+                 _c_int32, _c_int32, _ptr],
+    "lct_buffer_reset": [_ptr, _c_int32, _c_int32, _ptr],
+    "lct_buffer_allocate": [_ptr, _c_int32, _ptr, _ptr, _c_int32, _ptr, _ptr],
+    "lct_buffer_free": [_ptr, _c_int32, _ptr, _ptr, _ptr],
+}
+
+EXPORTED = tuple(_SIGNATURES) + ("lct_version", "lct_error_string")
+
+_lock = threading.Lock()
+_library = None
+
+
+def load_library(path: Path | str | None = None) -> ctypes.CDLL:
+    """Load (once) and type the codec library; raise if it is not built."""
+    global _library
+    with _lock:
+        if _library is not None and path is None:
+            return _library
+        target = Path(path) if path is not None else LIBRARY_PATH
+        if not target.exists():
+            raise RuntimeError(
+                f"LCT HIP library not found at {target}; build it with "
+                "`python -m losslessly_compressed_tensors_amd.build`")
+        lib = ctypes.CDLL(str(target))
+        for name, argtypes in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = _c_int32
+        lib.lct_version.argtypes = []
+        lib.lct_version.restype = ctypes.c_char_p
+        lib.lct_error_string.argtypes = [_c_int32]
+        lib.lct_error_string.restype = ctypes.c_char_p
+        if path is None:
+            _library = lib
+        return lib
+
+
+class LCTKernelError(RuntimeError):
+    """A codec entry point rejected its arguments or failed to launch."""
+
+
+def call(name: str, *args) -> None:
+    """Invoke entry point ``name`` and raise on a non-zero return code."""
+    lib = load_library()
+    code = getattr(lib, name)(*args)
+    if code != 0:
+        message = lib.lct_error_string(code).decode()
+        raise LCTKernelError(f"{name} failed with code {code}: {message}")
+
+
+def geometry(stream_geometry) -> Geometry:
+    block_symbols, lanes, steps, fixed_words = stream_geometry
+    return Geometry(int(block_symbols), int(lanes), int(steps), int(fixed_words))

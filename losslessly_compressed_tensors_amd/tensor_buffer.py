@@ -1,0 +1,180 @@
+"""GPU-resident first-fit allocator for overflow tails (``TensorBuffer``).
+
+Same interface and semantics as ``LCT/tensor_buffer.py:13-201``: one device
+byte array holds ``free_starts[R] | free_sizes[R] | free_count | lock |
+generation`` (padded to 16 bytes) followed by the payload arena; allocation
+and free run on the device (``lct_buffer_allocate`` / ``lct_buffer_free``)
+and return ``[offset, size, status, generation]`` descriptors without a host
+sync.  ``reset()`` bumps the generation so older descriptors become stale.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from .kernels import dispatch
+
+_ALIGNMENT = 16
+
+
+@dataclass(frozen=True)
+class Allocation:
+    """A device ``[offset, aligned_size, status, generation]`` descriptor."""
+
+    descriptor: torch.Tensor
+    owner: object
+
+    @property
+    def offset(self) -> torch.Tensor:
+        return self.descriptor[0]
+
+    @property
+    def size(self) -> torch.Tensor:
+        return self.descriptor[1]
+
+    @property
+    def status(self) -> torch.Tensor:
+        return self.descriptor[2]
+
+    @property
+    def generation(self) -> torch.Tensor:
+        return self.descriptor[3]
+
+
+@torch.library.custom_op("lct::tensor_buffer_free", mutates_args=("storage", "descriptor"))
+def tensor_buffer_free(storage: torch.Tensor, descriptor: torch.Tensor,
+                       max_free_regions: int) -> torch.Tensor:
+    """Opaque free for ``torch.compile`` (``LCT/kernels/tensor_buffer_ops.py:5-15``)."""
+    status = torch.empty(1, dtype=torch.int32, device=storage.device)
+    dispatch.buffer_free(storage, max_free_regions, descriptor, status)
+    return status
+
+
+@tensor_buffer_free.register_fake
+def _tensor_buffer_free_fake(storage, descriptor, max_free_regions):
+    return torch.empty(1, dtype=torch.int32, device=storage.device)
+
+
+class TensorBuffer:
+    """Device-resident first-fit allocator returning device-side descriptors."""
+
+    def __init__(self, capacity_bytes: int, *, max_free_regions: int = 256,
+                 device: torch.device | str | None = None) -> None:
+        if capacity_bytes > torch.iinfo(torch.int32).max:
+            raise ValueError("capacity_bytes must fit in int32")
+        if max_free_regions <= 0 or max_free_regions & (max_free_regions - 1):
+            raise ValueError("max_free_regions must be a positive power of two")
+        if max_free_regions > 4096:
+            raise ValueError("max_free_regions above 4096 is not supported")
+        self.capacity_bytes = int(capacity_bytes)
+        self.max_free_regions = int(max_free_regions)
+        self._metadata_bytes = self._align(8 * self.max_free_regions + 12)
+        self._storage = torch.zeros(self._metadata_bytes + self.capacity_bytes,
+                                    dtype=torch.uint8, device=torch.device(device or "cuda"))
+        self.device = self._storage.device
+        regions = self.max_free_regions
+        meta = self._storage.narrow(0, 0, 8 * regions + 12).view(torch.int32)
+        self._free_starts = meta.narrow(0, 0, regions)
+        self._free_sizes = meta.narrow(0, regions, regions)
+        self._free_count = meta.narrow(0, 2 * regions, 1)
+        self._lock = meta.narrow(0, 2 * regions + 1, 1)
+        self._generation = meta.narrow(0, 2 * regions + 2, 1)
+        self._data = self._storage.narrow(0, self._metadata_bytes, self.capacity_bytes)
+        self.reset()
+
+    @staticmethod
+    def _align(nbytes: int) -> int:
+        return (nbytes + _ALIGNMENT - 1) // _ALIGNMENT * _ALIGNMENT
+
+    @property
+    def data(self) -> torch.Tensor:
+        """The payload arena (descriptor offsets index into it)."""
+        return self._data
+
+    @property
+    def storage(self) -> torch.Tensor:
+        """Metadata followed by the arena; the allocator kernels take its base."""
+        return self._storage
+
+    def allocate(self, nbytes: torch.Tensor) -> Allocation:
+        """Reserve ``nbytes`` (a one-element device int32 tensor) without a sync."""
+        descriptor = torch.empty(4, dtype=torch.int32, device=self.device)
+        dispatch.buffer_allocate(self._storage, self.max_free_regions, nbytes, None, 0,
+                                 descriptor)
+        return Allocation(descriptor, self)
+
+    def allocate_with_items(self, payload_bytes: torch.Tensor, item_count: torch.Tensor,
+                            item_bytes: int) -> Allocation:
+        """Reserve ``payload_bytes + item_count * item_bytes`` asynchronously."""
+        if item_bytes <= 0:
+            raise ValueError("item_bytes must be positive")
+        descriptor = torch.empty(4, dtype=torch.int32, device=self.device)
+        dispatch.buffer_allocate(self._storage, self.max_free_regions, payload_bytes,
+                                 item_count, int(item_bytes), descriptor)
+        return Allocation(descriptor, self)
+
+    def free(self, allocation: Allocation) -> torch.Tensor:
+        """Return an allocation; the device status comes back asynchronously."""
+        if allocation.owner is not self:
+            raise ValueError("allocation belongs to a different allocator")
+        if allocation.descriptor.device != self.device:
+            raise ValueError("allocation must be on the allocator device")
+        return tensor_buffer_free(self._storage, allocation.descriptor, self.max_free_regions)
+
+    def reset(self) -> None:
+        """Reset asynchronously; previously returned descriptors become stale."""
+        dispatch.buffer_reset(self._storage, self.max_free_regions, self.capacity_bytes)
+
+
+def _free_regions_snapshot(buffer: TensorBuffer) -> list[tuple[int, int]]:
+    """Synchronize and copy the free list as ``[(start, size), ...]``."""
+    regions = buffer.max_free_regions
+    meta = buffer._storage.narrow(0, 0, buffer._metadata_bytes).view(torch.int32).cpu()
+    count = int(meta[2 * regions].item())
+    if not 0 <= count <= regions:
+        raise RuntimeError(f"corrupt free-list count: {count}")
+    return [(int(meta[i].item()), int(meta[regions + i].item())) for i in range(count)]
+
+
+def verify_buffer(buffer: TensorBuffer) -> None:
+    """Synchronize and check the free-list invariants (``tensor_buffer.py:158-170``)."""
+    previous_end = 0
+    free_bytes = 0
+    for start, size in _free_regions_snapshot(buffer):
+        if size <= 0 or start < previous_end or start + size > buffer.capacity_bytes:
+            raise RuntimeError(f"invalid free region: [{start}, {start + size})")
+        if start == previous_end and previous_end != 0:
+            raise RuntimeError("adjacent free regions were not coalesced")
+        previous_end = start + size
+        free_bytes += size
+    if free_bytes > buffer.capacity_bytes:
+        raise RuntimeError("free regions exceed payload capacity")
+
+
+def visualize_buffer(buffer: TensorBuffer, width: int = 80) -> str:
+    """Synchronize and return an ASCII map of arena usage."""
+    if buffer is None:
+        return ""
+    if width < 8:
+        raise ValueError("width must be at least 8")
+    free_regions = _free_regions_snapshot(buffer)
+    capacity = buffer.capacity_bytes
+    free_bytes = sum(size for _, size in free_regions)
+    used_bytes = capacity - free_bytes
+    cells = ["#"] * width
+    for start, size in free_regions:
+        left = start * width // capacity
+        right = ((start + size) * width + capacity - 1) // capacity
+        for cell in range(left, min(width, max(left + 1, right))):
+            cells[cell] = "."
+    ranges = [f"[{start}, {start + size})" for start, size in free_regions]
+    if len(ranges) > 8:
+        ranges = [*ranges[:4], "...", *ranges[-4:]]
+    return "\n".join((
+        f"payload: {used_bytes}/{capacity} B used ({used_bytes / capacity:.1%}); "
+        f"{len(free_regions)} free region(s)",
+        f"0 [{''.join(cells)}] {capacity}",
+        "# used  . free",
+        f"free: {', '.join(ranges) or 'none'}",
+    ))

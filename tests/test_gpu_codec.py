@@ -1,0 +1,111 @@
+"""GPU parity: compress/decompress through the C-ABI against the CPU oracle.
+
+Every written field of the GPU CompressedTensor (center, shifted decode table,
+payload words, side bytes, overflow list, tails, block metadata, descriptor,
+memory_size) must equal the oracle's bit for bit, and decompression must
+restore the input bits exactly.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import assert_matches_oracle, bits_of, oracle_compress, require_gpu
+
+pytestmark = pytest.mark.gpu
+
+from losslessly_compressed_tensors_amd.comp_format import DistType, Distribution, NoiseLevel
+from losslessly_compressed_tensors_amd.operations import compress, decompress
+from losslessly_compressed_tensors_amd.tensor_buffer import TensorBuffer, verify_buffer
+
+
+def _gaussian(shape, seed, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).to(torch.bfloat16)
+
+
+def _laplace(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    u = torch.rand(*shape, generator=g) - 0.5
+    return (-scale * torch.sign(u) * torch.log1p(-2.0 * u.abs())).to(torch.bfloat16)
+
+
+LAYOUTS = [
+    (DistType.GAUSSIAN, NoiseLevel.CLEAN),
+    (DistType.GAUSSIAN, NoiseLevel.MEDIUM),
+    (DistType.LAPLACE, NoiseLevel.HIGH),
+    (DistType.LAPLACE, NoiseLevel.SPARSE),
+    (DistType.EMPIRICAL, NoiseLevel.CLEAN),
+]
+
+
+@pytest.mark.parametrize("family,noise", LAYOUTS)
+@pytest.mark.parametrize("shape", [(1024, 1024), (3, 50001), (7,)])
+def test_private_roundtrip_matches_oracle(family, noise, shape):
+    require_gpu()
+    print(f"case private {family.name} {noise.name} {shape}", flush=True)
+    dist = Distribution(family, noise_level=noise)
+    x = _gaussian(shape, 0) if family == DistType.GAUSSIAN else _laplace(shape, 1)
+    ct = compress(x.cuda(), dist)
+    o = oracle_compress(x, dist)
+    assert_matches_oracle(ct, o)
+    y = decompress(ct)
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == tuple(shape)
+    assert np.array_equal(bits_of(y), bits_of(x))
+
+
+@pytest.mark.parametrize("family,noise", LAYOUTS)
+def test_all_bf16_patterns_roundtrip(family, noise):
+    """All 65536 bit patterns (NaNs, infs, subnormals): heavy escapes and overflow."""
+    require_gpu()
+    print(f"case patterns {family.name} {noise.name}", flush=True)
+    rng = np.random.default_rng(7)
+    bits = np.arange(65536, dtype=np.uint16)
+    rng.shuffle(bits)
+    x = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16)
+    dist = Distribution(family, noise_level=noise)
+    ct = compress(x.cuda(), dist)
+    o = oracle_compress(x, dist)
+    assert o.counts[0] > 0
+    assert_matches_oracle(ct, o)
+    assert np.array_equal(bits_of(decompress(ct)), bits)
+
+
+@pytest.mark.parametrize("family,noise", LAYOUTS)
+def test_buffered_roundtrip_matches_oracle(family, noise):
+    require_gpu()
+    import oracle
+    print(f"case buffered {family.name} {noise.name}", flush=True)
+    dist = Distribution(family, noise_level=noise)
+    capacity = 1 << 20
+    buffer = TensorBuffer(capacity, max_free_regions=64, device="cuda")
+    host = oracle.Buffer(capacity, 64)
+    tensors = []
+    for seed in range(3):
+        rng = np.random.default_rng(seed)
+        bits = rng.integers(0, 65536, size=40000 + 977 * seed, dtype=np.uint16)
+        x = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16)
+        ct = compress(x.cuda(), dist, buffer=buffer)
+        o = oracle_compress(x, dist, buffer=host)
+        assert_matches_oracle(ct, o)
+        assert np.array_equal(bits_of(decompress(ct)), bits)
+        tensors.append((ct, o))
+    # Free the middle one, then the rest; the free list must coalesce back.
+    for index in (1, 0, 2):
+        ct, o = tensors[index]
+        ct.free()
+        host.free(o.descriptor)
+    verify_buffer(buffer)
+    meta = buffer.storage[: 4 * (2 * 64 + 3)].view(torch.int32).cpu().numpy()
+    assert np.array_equal(meta[:2 * 64 + 1], host.meta[:2 * 64 + 1])
+    assert host.free_regions() == [(0, capacity)]
+
+
+def test_c1_ratio_and_size():
+    """Config 1: randn(1024,1024) seed 0, GAUSSIAN CLEAN, private."""
+    require_gpu()
+    x = _gaussian((1024, 1024), 0)
+    ct = compress(x.cuda(), Distribution(DistType.GAUSSIAN))
+    o = oracle_compress(x, Distribution(DistType.GAUSSIAN))
+    assert ct.memory_size() == o.memory_size()
+    assert np.array_equal(bits_of(decompress(ct)), bits_of(x))
+    assert x.numel() * 2 / ct.memory_size() > 1.42
