@@ -198,6 +198,11 @@ def main() -> int:
                                   2, torch)
     enc_alg = encode_bytes(cts[0])
 
+    # Reference traffic for counter calibration: a plain 256 MiB device copy
+    # (reads and writes exactly 2n bytes each).
+    copy_out = torch.empty_like(xs[0])
+    copy_ms = _time_events(lambda i: copy_out.copy_(xs[i % 2]), 5, 2, torch)
+
     result = {
         "metric": METRIC,
         "value": round(nbytes / (dec_ms * 1e-3) / 1e9, 2),
@@ -225,6 +230,7 @@ def main() -> int:
         "compress_private_gbps": round(nbytes / (enc_private_ms * 1e-3) / 1e9, 2),
         "compress_ms": round(enc_ms, 5),
         "compression_ratio": round(ratio, 5),
+        "copy_gbps": round(2 * nbytes / (copy_ms * 1e-3) / 1e9, 1),
         "roofline": {
             "bound": "hbm",
             "kernel": "decode_kernel",

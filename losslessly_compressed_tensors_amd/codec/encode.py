@@ -155,6 +155,9 @@ def encode(data: torch.Tensor, distribution: Distribution, buffer: TensorBuffer 
                                 layout=StorageLayout.RAW)
     if source.element_size() != 2:
         raise TypeError(f"LCT compresses 16-bit (bfloat16) tensors, got {source.dtype}")
+    if source.data_ptr() % 16:
+        # The encoder reads its input with 16-byte vector loads.
+        source = source.clone()
     sign_mantissa = torch.empty(storage_numel, dtype=torch.uint8, device=source.device)
     return encode_components(source.view(torch.int16), sign_mantissa, storage_numel,
                              distribution, buffer, shape, precomputed=False,

@@ -21,23 +21,33 @@ __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     __shared__ int32_t scratch[kWavesPerBlock];
     __shared__ int32_t flag;
     const int t = threadIdx.x;
+    // Thread t owns the contiguous run [t*per, t*per + per) and keeps it in
+    // registers between the load, the block scan and the store.
     const int per = (n_blocks + kLanes - 1) / kLanes;
-    const int begin = min(t * per, n_blocks);
-    const int end = min(begin + per, n_blocks);
+    const int begin = t * per;
+    int32_t counts_local[kPrefixPerThread], bytes_local[kPrefixPerThread];
     int32_t local_count = 0, local_bytes = 0;
-    for (int b = begin; b < end; ++b) {
-        local_count += summaries[b];
-        local_bytes += summaries[n_blocks + b];
+#pragma unroll
+    for (int j = 0; j < kPrefixPerThread; ++j) {
+        const int b = begin + j;
+        const bool in = j < per && b < n_blocks;
+        counts_local[j] = in ? summaries[b] : 0;
+        bytes_local[j] = in ? summaries[n_blocks + b] : 0;
+        local_count += counts_local[j];
+        local_bytes += bytes_local[j];
     }
     int32_t total_count, total_bytes;
     int32_t count_run = block_exclusive_scan(local_count, scratch, &total_count);
     int32_t byte_run = block_exclusive_scan(local_bytes, scratch, &total_bytes);
-    for (int b = begin; b < end; ++b) {
-        const int32_t c = summaries[b], bytes = summaries[n_blocks + b];
-        summaries[2 * n_blocks + b] = count_run;
-        summaries[3 * n_blocks + b] = byte_run;
-        count_run += c;
-        byte_run += bytes;
+#pragma unroll
+    for (int j = 0; j < kPrefixPerThread; ++j) {
+        const int b = begin + j;
+        if (j < per && b < n_blocks) {
+            summaries[2 * n_blocks + b] = count_run;
+            summaries[3 * n_blocks + b] = byte_run;
+        }
+        count_run += counts_local[j];
+        byte_run += bytes_local[j];
     }
     if (t == 0) {
         counts[0] = total_count;

@@ -7,53 +7,72 @@
 // byte and storing the BF16 bits at the swizzled logical offset.  Steps at or
 // past a stream's overflow start take their exponent from the tail bytes and
 // consume no payload bits.
+//
+// The step loop runs in 32-step chunks: while a chunk is decoded from the
+// wave's LDS side slice, the next chunk's side bytes are already in flight,
+// and the overflow check is only compiled into chunks that reach the wave's
+// first overflow start.
 #include "decode_core.h"
 
 namespace lct {
 namespace {
 
-// S is a template parameter so the pair loop (which holds convergent
-// wave-uniform branches) can be unrolled.
-template <bool kFull, int S>
-__device__ __forceinline__ void decode_rows(const StreamCursor &cursor_in, const LaneOverlay &lane,
-                                            const uint8_t *__restrict__ side_block,
-                                            uint16_t *__restrict__ out_block, int64_t row_base,
-                                            int64_t valid_in_block) {
-    StreamCursor cursor = cursor_in;
-    const uint32_t t = threadIdx.x;
-#pragma unroll 2
-    for (int step = 0; step < S; step += 2) {
+template <bool kFull, bool kOverlay>
+__device__ __forceinline__ void decode_chunk(StreamCursor &cursor, const LaneOverlay &lane,
+                                             const uint8_t *slice, __amdgpu_buffer_rsrc_t out,
+                                             int first_step, int64_t row_base,
+                                             uint32_t valid_in_block) {
+    const uint32_t t2 = threadIdx.x * 2u;
+#pragma unroll
+    for (int j = 0; j < kChunkSteps; j += 2) {
+        const int step = first_step + j;
         uint32_t f0, len0, f1, len1;
         cursor.next_pair(f0, len0, f1, len1);
-        const uint32_t slot = static_cast<uint32_t>(step) * kLanes + t;
-        const uint32_t sm0 = side_block[slot];
-        const uint32_t sm1 = side_block[slot + kLanes];
-        if (step >= lane.wave_start) {
-            if (step >= lane.start) {
-                const uint8_t *src = lane.tail + lane.offset + (step - lane.start);
-                f0 = tail_field(src[0]);
-                f1 = tail_field(src[1]);
-                len0 = 0;
-                len1 = 0;
-            }
-        }
-        const uint32_t col = t ^ static_cast<uint32_t>((row_base + step) & 254);
-        const uint32_t off0 = static_cast<uint32_t>(step) * kLanes + col;
-        const uint32_t off1 = off0 + kLanes;
-        const uint16_t out0 = static_cast<uint16_t>(join_bf16(f0, sm0));
-        const uint16_t out1 = static_cast<uint16_t>(join_bf16(f1, sm1));
+        if (kOverlay) overlay_pair(lane, step, f0, len0, f1, len1);
+        // Byte offset of the lane's logical column within its row; rows step
+        // and step+1 share the swizzle mask.
+        const uint32_t col2 = t2 ^ (static_cast<uint32_t>((row_base + step) & 254) * 2u);
+        const uint32_t out0 = join_bf16(f0, side_byte(slice, j));
+        const uint32_t out1 = join_bf16(f1, side_byte(slice, j + 1));
+        const int row_bytes = step * kLanes * 2;
         if (kFull) {
-            out_block[off0] = out0;
-            out_block[off1] = out1;
+            __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(out0), out, col2, row_bytes, 0);
+            __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(out1), out, col2,
+                                                  row_bytes + kLanes * 2, 0);
         } else {
+            const uint32_t off0 = static_cast<uint32_t>(step) * kLanes + (col2 >> 1);
             const bool v0 = off0 < valid_in_block;
-            const bool v1 = off1 < valid_in_block;
-            if (v0) out_block[off0] = out0;
-            if (v1) out_block[off1] = out1;
+            const bool v1 = off0 + kLanes < valid_in_block;
+            if (v0)
+                __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(out0), out, col2,
+                                                      row_bytes, 0);
+            if (v1)
+                __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(out1), out, col2,
+                                                      row_bytes + kLanes * 2, 0);
             len0 = v0 ? len0 : 0u;
             len1 = v1 ? len1 : 0u;
         }
         cursor.pos += len0 + len1;
+    }
+}
+
+// S is a template parameter so the chunk loop has a fixed trip count.
+// `next` holds the side bytes of chunk 0, fetched by the caller.
+template <bool kFull, int S>
+__device__ __forceinline__ void decode_rows(StreamCursor cursor, const LaneOverlay &lane,
+                                            uint8_t *slice, __amdgpu_buffer_rsrc_t side,
+                                            SideChunk next, __amdgpu_buffer_rsrc_t out,
+                                            int64_t row_base, uint32_t valid_in_block) {
+    static_assert(S % kChunkSteps == 0, "whole chunks");
+    const uint32_t voffset = side_fetch_offset();
+#pragma unroll 1
+    for (int c = 0; c < S; c += kChunkSteps) {
+        store_side_chunk(slice, next);
+        if (c + kChunkSteps < S) next = fetch_side_chunk(side, voffset, c + kChunkSteps);
+        if (c + kChunkSteps > lane.wave_start)
+            decode_chunk<kFull, true>(cursor, lane, slice, out, c, row_base, valid_in_block);
+        else
+            decode_chunk<kFull, false>(cursor, lane, slice, out, c, row_base, valid_in_block);
     }
 }
 
@@ -65,7 +84,18 @@ __global__ __launch_bounds__(kLanes) void decode_kernel(
     extern __shared__ uint32_t stage[];   // (W + 2) rows x 256
     __shared__ DecodeTables tb;
     __shared__ int32_t map_start[kLanes], map_offset[kLanes], scratch[kWavesPerBlock];
+    __shared__ __attribute__((aligned(16))) uint8_t side_slices[kWavesPerBlock][kChunkSteps * kWave];
     const int64_t block = blockIdx.x;
+    const int64_t row_base = block * S;
+    const int64_t logical_base = row_base * kLanes;
+    const uint32_t block_elems = static_cast<uint32_t>(S) * kLanes;
+    const int64_t remaining = logical_numel - logical_base;
+    const uint32_t valid = remaining < block_elems ? static_cast<uint32_t>(remaining) : block_elems;
+    const __amdgpu_buffer_rsrc_t side_rsrc = make_rsrc(side + logical_base, block_elems);
+    const __amdgpu_buffer_rsrc_t out_rsrc = make_rsrc(output + logical_base, 2u * valid);
+    // The first side chunk is in flight while the prologue stages the payload.
+    const SideChunk first = fetch_side_chunk(side_rsrc, side_fetch_offset(), 0);
+
     const int32_t center = center_ptr[0];
     build_decode_tables(tb, shifted_decode, center);
     stage_payload(stage, encoded, n_blocks * kLanes, block, W);
@@ -74,19 +104,18 @@ __global__ __launch_bounds__(kLanes) void decode_kernel(
     __syncthreads();
 
     const StreamCursor cursor{stage + threadIdx.x, &tb, 0u, static_cast<uint32_t>(W), rare};
-    const int64_t row_base = block * S;
-    const int64_t logical_base = row_base * kLanes;
-    const uint8_t *side_block = side + logical_base;
-    uint16_t *out_block = output + logical_base;
-    const int64_t valid = logical_numel - logical_base;
-    const bool full = valid >= static_cast<int64_t>(S) * kLanes;
-#define LCT_DECODE_CASE(FULL)                                                          \
-    if (S == 128)                                                                      \
-        decode_rows<FULL, 128>(cursor, lane, side_block, out_block, row_base, valid);  \
-    else                                                                               \
-        decode_rows<FULL, 256>(cursor, lane, side_block, out_block, row_base, valid);
-    if (full) { LCT_DECODE_CASE(true) } else { LCT_DECODE_CASE(false) }
-#undef LCT_DECODE_CASE
+    uint8_t *slice = side_slices[threadIdx.x / kWave];
+    if (valid == block_elems) {
+        if (S == 128)
+            decode_rows<true, 128>(cursor, lane, slice, side_rsrc, first, out_rsrc, row_base, valid);
+        else
+            decode_rows<true, 256>(cursor, lane, slice, side_rsrc, first, out_rsrc, row_base, valid);
+    } else {
+        if (S == 128)
+            decode_rows<false, 128>(cursor, lane, slice, side_rsrc, first, out_rsrc, row_base, valid);
+        else
+            decode_rows<false, 256>(cursor, lane, slice, side_rsrc, first, out_rsrc, row_base, valid);
+    }
 }
 
 }  // namespace

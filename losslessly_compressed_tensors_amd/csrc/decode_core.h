@@ -9,22 +9,37 @@
 //    loads; a lane's 32-bit window at bit position `pos` is
 //    alignbit(row[pos/32 + 1], row[pos/32], pos) -- one ds_read2st64 and one
 //    v_alignbit per pair, no 64-bit shifts and no per-lane global gathers;
-//  * the lookup table has 256 entries (direct codes are at most 8 bits,
+//  * the lookup table has 256 16-bit entries (direct codes are at most 8 bits,
 //    LCT/compression/huffman_tables.py:106-107) holding the exponent already
 //    in BF16 position: entry = len | e_raw << 7, so a decoded value is one
-//    bit-field insert away from its BF16 bits.  An ESC prefix (or any code
-//    longer than 8 bits) is marked by len = 31, which makes len0 + len1 >= 32;
-//    those pairs take a wave-uniform branch that reads the 8-bit literal;
+//    bit-field insert away from its BF16 bits.  16-bit entries keep the table
+//    in 128 dwords, which bounds LDS bank conflicts of the data-dependent
+//    lookups.  An ESC prefix (or any code longer than 8 bits) is marked by
+//    len = 31, which makes len0 + len1 >= 32; those pairs take a wave-uniform
+//    branch that reads the 8-bit literal;
 //  * a second 256-entry table maps an escaped table index to its exponent
-//    field under the tensor's center.
+//    field under the tensor's center;
+//  * side bytes are fetched with 16-byte buffer loads one 32-step chunk ahead
+//    of use and handed to the lanes through a wave-private LDS slice, so HBM
+//    latency overlaps a whole chunk of decoding; outputs go out through raw
+//    buffer stores (SGPR base, 32-bit lane offset).
 #pragma once
 
 #include "lct_device.h"
 
 namespace lct {
 
+// Buffer resource word 3 for gfx9-family raw buffers.
+constexpr int32_t kBufferConfig = 0x00020000;
+constexpr int kChunkSteps = 32;   // steps per prefetched side-byte chunk
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes),
+                                             kBufferConfig);
+}
+
 struct DecodeTables {
-    uint32_t entry[256];
+    uint16_t entry[256];
     uint32_t escape[256];
 };
 
@@ -36,8 +51,9 @@ __device__ __forceinline__ void build_decode_tables(DecodeTables &tb,
     const int32_t packed = shifted_decode[t];
     const int32_t length = packed & 255;
     const uint32_t field = static_cast<uint32_t>(((packed >> 8) + 127) & 255) << 7;
-    tb.entry[t] = (length >= 1 && length <= 8) ? (static_cast<uint32_t>(length) | field)
-                                               : static_cast<uint32_t>(kEscapeLength);
+    tb.entry[t] = static_cast<uint16_t>((length >= 1 && length <= 8)
+                                            ? (static_cast<uint32_t>(length) | field)
+                                            : static_cast<uint32_t>(kEscapeLength));
     tb.escape[t] = static_cast<uint32_t>((index_to_exponent(t, center) + 127) & 255) << 7;
 }
 
@@ -66,9 +82,9 @@ struct LaneOverlay {
 };
 
 // Expand the block's compact overflow list into per-lane (start, offset), as
-// decode.py:195-240 does.  `ov` may be null.  Contains barriers; every thread
-// of the block must call it.  A buffered tensor whose allocation failed
-// (descriptor status != 0) has no tails and is decoded without overlay.
+// decode.py:195-240 does.  Contains barriers; every thread of the block must
+// call it.  A buffered tensor whose allocation failed (descriptor status != 0)
+// has no tails and is decoded without overlay.
 __device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, bool present,
                                                      int64_t block, int64_t n_blocks, int S,
                                                      int32_t *map_start, int32_t *map_offset,
@@ -155,6 +171,57 @@ struct StreamCursor {
 // Exponent field of an overflow tail byte int8(e - 127).
 __device__ __forceinline__ uint32_t tail_field(uint32_t byte) {
     return ((byte + 127u) & 255u) << 7;
+}
+
+// Overlay one lane's pair if it is at/after its overflow start: exponents come
+// from the tail bytes and the pair consumes no payload bits.
+__device__ __forceinline__ void overlay_pair(const LaneOverlay &lane, int step, uint32_t &f0,
+                                             uint32_t &len0, uint32_t &f1, uint32_t &len1) {
+    if (step >= lane.start) {
+        const uint8_t *src = lane.tail + lane.offset + (step - lane.start);
+        f0 = tail_field(src[0]);
+        f1 = tail_field(src[1]);
+        len0 = 0;
+        len1 = 0;
+    }
+}
+
+// Side bytes reach the lanes through a wave-private LDS slice: each lane
+// fetches 16 contiguous bytes of its wave's 64-byte row segments (one
+// 16-byte buffer load covers 16 steps x 64 lanes per wave instruction), the
+// wave stores them to its slice and each lane then reads its own byte per step
+// (64 consecutive bytes per step: conflict-free).  A chunk is 32 steps, so one
+// chunk is 2 KiB per wave and two 16-byte loads per lane.
+struct SideChunk {
+    uint4 q0, q1;
+};
+
+// Buffer offset of this lane's 16 bytes within a 16-step group.
+__device__ __forceinline__ uint32_t side_fetch_offset() {
+    const uint32_t j = threadIdx.x & (kWave - 1);
+    const uint32_t wave = threadIdx.x / kWave;
+    return (j >> 2) * kLanes + wave * kWave + (j & 3) * 16;
+}
+
+__device__ __forceinline__ SideChunk fetch_side_chunk(__amdgpu_buffer_rsrc_t side,
+                                                      uint32_t voffset, int first_step) {
+    SideChunk c;
+    c.q0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         side, voffset, first_step * kLanes, 0));
+    c.q1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         side, voffset, (first_step + 16) * kLanes, 0));
+    return c;
+}
+
+// slice: this wave's 2 KiB; byte s*64 + lane holds step s of the chunk.
+__device__ __forceinline__ void store_side_chunk(uint8_t *slice, const SideChunk &c) {
+    const uint32_t j = threadIdx.x & (kWave - 1);
+    reinterpret_cast<uint4 *>(slice)[j] = c.q0;
+    reinterpret_cast<uint4 *>(slice + 1024)[j] = c.q1;
+}
+
+__device__ __forceinline__ uint32_t side_byte(const uint8_t *slice, int step_in_chunk) {
+    return slice[step_in_chunk * kWave + (threadIdx.x & (kWave - 1))];
 }
 
 }  // namespace lct

@@ -62,20 +62,6 @@ __device__ __forceinline__ void store_result(uint32_t bits, bool logical_valid, 
     }
 }
 
-// Overlay one lane's pair if it is at/after its overflow start.
-__device__ __forceinline__ void overlay_pair(const LaneOverlay &lane, int step, uint32_t &f0,
-                                             uint32_t &len0, uint32_t &f1, uint32_t &len1) {
-    if (step >= lane.wave_start) {
-        if (step >= lane.start) {
-            const uint8_t *src = lane.tail + lane.offset + (step - lane.start);
-            f0 = tail_field(src[0]);
-            f1 = tail_field(src[1]);
-            len0 = 0;
-            len1 = 0;
-        }
-    }
-}
-
 template <bool kFull, int S, int kPolicy>
 __device__ __forceinline__ void pointwise_rows(const StreamCursor &cursor_in, const LaneOverlay &lane,
                                                const uint8_t *__restrict__ side_block,

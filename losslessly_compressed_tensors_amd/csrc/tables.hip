@@ -23,14 +23,25 @@ __global__ __launch_bounds__(kLanes) void tables_kernel(
     const int t = threadIdx.x;
     int32_t center;
     if (estimate) {
+        // Region i is [i*n/M, (i+1)*n/M).  M is n itself (one element per
+        // region, jitter 0) or, in every call the codec makes, the power of
+        // two 4096; only other M pay for 64-bit division.
+        const bool every = sample_size == logical_numel;
+        const bool pow2 = (sample_size & (sample_size - 1)) == 0;
+        const int shift = __builtin_ctzll(static_cast<uint64_t>(sample_size));
         int32_t sum = 0, kept = 0;
         for (int64_t i = t; i < sample_size; i += kLanes) {
-            const uint32_t hashed = static_cast<uint32_t>(i) * 0x9E3779B9u;
-            const int64_t start = i * logical_numel / sample_size;
-            const int64_t end = (i + 1) * logical_numel / sample_size;
-            const uint64_t jitter =
-                (static_cast<uint64_t>(hashed) * static_cast<uint64_t>(end - start)) >> 32;
-            const int64_t pos = start + static_cast<int64_t>(jitter);
+            int64_t pos = i;
+            if (!every) {
+                const uint32_t hashed = static_cast<uint32_t>(i) * 0x9E3779B9u;
+                const int64_t start = pow2 ? (i * logical_numel) >> shift
+                                           : i * logical_numel / sample_size;
+                const int64_t end = pow2 ? ((i + 1) * logical_numel) >> shift
+                                         : (i + 1) * logical_numel / sample_size;
+                const uint64_t jitter =
+                    (static_cast<uint64_t>(hashed) * static_cast<uint64_t>(end - start)) >> 32;
+                pos = start + static_cast<int64_t>(jitter);
+            }
             int32_t exp;
             if (precomputed) {
                 exp = static_cast<int32_t>(static_cast<const uint8_t *>(source)[pos]) - 127;

@@ -109,3 +109,16 @@ def test_c1_ratio_and_size():
     assert ct.memory_size() == o.memory_size()
     assert np.array_equal(bits_of(decompress(ct)), bits_of(x))
     assert x.numel() * 2 / ct.memory_size() > 1.42
+
+
+def test_unaligned_view_roundtrip():
+    """A view starting 2 bytes into its storage still compresses bit-exactly."""
+    require_gpu()
+    base = _gaussian((300001,), 5).cuda()
+    x = base[1:]
+    assert x.data_ptr() % 16 != 0
+    dist = Distribution(DistType.GAUSSIAN)
+    ct = compress(x, dist)
+    o = oracle_compress(x.cpu(), dist)
+    assert_matches_oracle(ct, o)
+    assert np.array_equal(bits_of(decompress(ct)), bits_of(x))
