@@ -103,37 +103,43 @@ int32_t lct_shift_decoding_table(const int32_t *base_decode,
  * storage order -- written here unless precomputed (padding is written as 0).
  * encoded: int32[nb*256*W + 4]; every one of the first nb*256*W words is
  * written (words a stream does not use are 0).  extra_starts: uint8[nb*256],
- * the first overflowing (even) step of each stream or 255.  summaries:
- * int32[4*nb] (per-block overflow count and tail bytes in the first 2*nb) when
- * write_summary, else unused.  size = nb*B. */
+ * the first overflowing (even) step of each stream or 255.  summaries: the
+ * per-block overflow count and tail bytes go to its first 2*nb entries when
+ * write_summary, else unused.  size = nb*B.  source, side and encoded must be
+ * 16-byte aligned. */
 int32_t lct_encode(const void *source, uint8_t *side, int32_t *encoded,
                    const int32_t *shifted_encode, uint8_t *extra_starts,
                    int32_t *summaries, int64_t size, int64_t logical_numel,
                    lct_geometry geometry, int32_t precomputed,
                    int32_t write_summary, hipStream_t stream);
 
-/* ---- replaces dispatch.py:70-85 (prefix_allocate): exclusive scans of the
- * per-block overflow counts/bytes into summaries[2nb..4nb), counts[4] =
- * {total_count, total_bytes, 0, 0}; if buffered, reserve
- * align16(total_bytes + 2*total_count) bytes from the TensorBuffer whose
- * metadata starts at buffer_meta (int32 free_starts[R] | free_sizes[R] | count
- * | lock | generation) and write descriptor[4] = {offset, size, status, gen}.
+/* ---- replaces dispatch.py:70-85 (prefix_allocate) and the block-metadata
+ * part of compact_extra: summaries is int32[5*nb + 1] whose first 2*nb
+ * entries the encoder filled; writes the exclusive scans of the per-block
+ * overflow counts/bytes into summaries[2nb..4nb), the list of blocks with
+ * overflow into summaries[4nb..) and its length into summaries[5nb];
+ * blocks[3*nb] = {count, first, byte_base}; counts[4] = {total_count,
+ * total_bytes, 0, 0}; if buffered, reserves align16(total_bytes +
+ * 2*total_count) bytes from the TensorBuffer whose metadata starts at
+ * buffer_meta (int32 free_starts[R] | free_sizes[R] | count | lock |
+ * generation) and writes descriptor[4] = {offset, size, status, gen}.
  * n_blocks <= 8192 (LCT/kernels/autotune.py:54). */
 int32_t lct_prefix_allocate(int32_t *summaries, int32_t *counts,
                             int32_t *descriptor, int32_t *buffer_meta,
-                            int64_t n_blocks, int32_t buffered,
+                            int32_t *blocks, int64_t n_blocks, int32_t buffered,
                             int32_t max_free_regions, hipStream_t stream);
 
-/* ---- replaces dispatch.py:113-130 (compact_extra, summaries path): per block
- * write the overflowing streams' lane and start bytes (ascending lane) and
- * their exponent tails int8(e-127) for steps start..S-1, plus
- * blocks[3*nb] = {count, first, byte_base}.  Private: lanes/starts/tail are
- * exact-size arrays, tails at tail + base.  Buffered: all three point at the
- * arena; offsets from descriptor and count as in lct_overflow.  A buffered
- * allocation whose status is not 0 gets no entries or tails written. */
+/* ---- replaces dispatch.py:113-130 (compact_extra, summaries path): for the
+ * blocks listed by lct_prefix_allocate, write the overflowing streams' lane
+ * and start bytes (ascending lane) at entries blocks[nb+k].. and their
+ * exponent tails int8(e-127) for steps start..S-1 from byte blocks[2nb+k].
+ * Private: lanes/starts/tail are exact-size arrays, tails at tail + base.
+ * Buffered: all three point at the arena; offsets from descriptor and count
+ * as in lct_overflow.  A buffered allocation whose status is not 0 gets no
+ * entries or tails written. */
 int32_t lct_compact_extra(const void *source, uint8_t *lanes, uint8_t *starts,
                           uint8_t *tail, const int32_t *descriptor,
-                          const int32_t *count, int32_t *blocks, int64_t base,
+                          const int32_t *count, const int32_t *blocks, int64_t base,
                           const uint8_t *extra_starts, const int32_t *summaries,
                           int64_t size, int64_t logical_numel,
                           lct_geometry geometry, int32_t precomputed,

@@ -83,8 +83,11 @@ def encode_components(
 
     encoded = torch.empty(streams * fixed_words + 4, dtype=torch.int32, device=device)
     extra_starts = torch.empty(streams, dtype=torch.uint8, device=device)
-    summaries = torch.empty(4 * blocks, dtype=torch.int32, device=device)
+    # Per-block overflow counts/bytes, their scans and the list of blocks
+    # that overflow (int32[5*blocks + 1], see lct_prefix_allocate).
+    summaries = torch.empty(5 * blocks + 1, dtype=torch.int32, device=device)
     counts = torch.empty(4, dtype=torch.int32, device=device)
+    blocks_out = torch.empty(3 * blocks, dtype=torch.int32, device=device)
     buffered = buffer is not None
     descriptor = torch.empty(4, dtype=torch.int32, device=device) if buffered else counts
     if blocks > 0:
@@ -93,8 +96,8 @@ def encode_components(
             size, streams, precomputed=precomputed, logical_numel=logical_numel,
             block_symbols=block_symbols, lanes=lanes, steps=steps, fixed_words=fixed_words,
             write_summary=True)
-        dispatch.prefix_allocate(summaries, counts, descriptor, buffer, blocks, buffered,
-                                 buffer.max_free_regions if buffered else 256)
+        dispatch.prefix_allocate(summaries, counts, descriptor, buffer, blocks_out, blocks,
+                                 buffered, buffer.max_free_regions if buffered else 256)
     else:
         counts.zero_()
         if buffered:
@@ -102,8 +105,8 @@ def encode_components(
             buffer_descriptor = buffer.allocate(counts[1:2])
             descriptor = buffer_descriptor.descriptor
 
-    blocks_out = torch.empty(3 * blocks, dtype=torch.int32, device=device)
     final_count, final_total = counts[:1], counts[1:2]
+    needs_compaction = blocks > 0
     if buffered:
         arena = buffer.data
         storage = FallbackStorage(tail=arena, count=final_count, lanes=arena, starts=arena,
@@ -111,13 +114,14 @@ def encode_components(
                                   allocation=descriptor)
     else:
         count, tail_bytes = (int(v) for v in counts[:2].tolist())
+        needs_compaction = needs_compaction and count > 0
         storage = FallbackStorage(
             tail=torch.empty(tail_bytes, dtype=torch.uint8, device=device),
             count=final_count,
             lanes=torch.empty(count, dtype=torch.uint8, device=device),
             starts=torch.empty(count, dtype=torch.uint8, device=device),
             blocks=blocks_out, allocation=counts[2:3], base=0)
-    if blocks > 0:
+    if needs_compaction:
         dispatch.compact_extra(
             source_values, storage, blocks, size, precomputed=precomputed, buffered=buffered,
             logical_numel=logical_numel, block_symbols=block_symbols, lanes=lanes,

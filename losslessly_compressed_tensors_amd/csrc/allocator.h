@@ -79,29 +79,50 @@ __device__ __forceinline__ int32_t block_min(int32_t v, int32_t *scratch) {
     return m;
 }
 
-// Shift entries [from, to) of both arrays by `delta` (+1 or -1).  All reads
-// finish before any write.  Contains barriers.
-__device__ __forceinline__ void allocator_shift(const AllocatorMeta &m, int32_t from,
-                                                int32_t to, int32_t delta) {
-    constexpr int kPerThread = 16;   // up to 4096 regions
-    int32_t s[kPerThread], z[kPerThread];
+// The free list held in registers: thread t owns entries t + k*256.
+constexpr int kRegionsPerThread = 16;   // up to 4096 regions
+
+struct RegionRegs {
+    int32_t start[kRegionsPerThread];
+    int32_t size[kRegionsPerThread];
+};
+
+// Load every entry below `regions` (the caller masks by the live count).
+__device__ __forceinline__ void load_regions(const AllocatorMeta &m, RegionRegs &r) {
 #pragma unroll
-    for (int j = 0; j < kPerThread; ++j) {
-        const int32_t i = from + static_cast<int32_t>(threadIdx.x) + j * kLanes;
-        if (i < to) {
-            s[j] = m.starts[i];
-            z[j] = m.sizes[i];
+    for (int k = 0; k < kRegionsPerThread; ++k) {
+        const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kLanes;
+        r.start[k] = i < m.regions ? m.starts[i] : 0;
+        r.size[k] = i < m.regions ? m.sizes[i] : 0;
+    }
+}
+
+// Write entries i in [from, to) to index i + delta.
+__device__ __forceinline__ void shift_regions(const AllocatorMeta &m, const RegionRegs &r,
+                                              int32_t from, int32_t to, int32_t delta) {
+#pragma unroll
+    for (int k = 0; k < kRegionsPerThread; ++k) {
+        const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kLanes;
+        if (i >= from && i < to) {
+            m.starts[i + delta] = r.start[k];
+            m.sizes[i + delta] = r.size[k];
+        }
+    }
+}
+
+// Value of entry `index` from whichever thread holds it; contains barriers.
+__device__ __forceinline__ void fetch_region(const RegionRegs &r, int32_t index, int32_t *shared2,
+                                             int32_t &start, int32_t &size) {
+#pragma unroll
+    for (int k = 0; k < kRegionsPerThread; ++k) {
+        if (static_cast<int32_t>(threadIdx.x) + k * kLanes == index) {
+            shared2[0] = r.start[k];
+            shared2[1] = r.size[k];
         }
     }
     __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kPerThread; ++j) {
-        const int32_t i = from + static_cast<int32_t>(threadIdx.x) + j * kLanes;
-        if (i < to) {
-            m.starts[i + delta] = s[j];
-            m.sizes[i + delta] = z[j];
-        }
-    }
+    start = shared2[0];
+    size = shared2[1];
     __syncthreads();
 }
 
@@ -109,6 +130,7 @@ __device__ __forceinline__ void allocator_shift(const AllocatorMeta &m, int32_t 
 __device__ __forceinline__ void allocator_allocate(const AllocatorMeta &m, int32_t request,
                                                    int32_t *descriptor, int32_t *scratch,
                                                    int32_t *flag) {
+    __shared__ int32_t shared2[2];
     if (!allocator_lock(m.lock, flag)) {
         if (threadIdx.x == 0) {
             descriptor[0] = -1;
@@ -120,20 +142,21 @@ __device__ __forceinline__ void allocator_allocate(const AllocatorMeta &m, int32
     }
     const int32_t generation = *m.generation;
     const int32_t count = *m.count;
+    RegionRegs r;
+    load_regions(m, r);
     const int32_t size = ((request + kAlignment - 1) / kAlignment) * kAlignment;
     int32_t candidate = m.regions;
-    for (int32_t i = threadIdx.x; i < count; i += kLanes)
-        if (m.sizes[i] >= size) candidate = min(candidate, i);
+#pragma unroll
+    for (int k = kRegionsPerThread - 1; k >= 0; --k) {
+        const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kLanes;
+        if (i < count && r.size[k] >= size) candidate = i;
+    }
     const int32_t slot = block_min(candidate, scratch);
     const bool success = request > 0 && slot < count;
     int32_t start = 0, region = 0;
-    if (success) {
-        start = m.starts[slot];
-        region = m.sizes[slot];
-    }
-    __syncthreads();
+    if (success) fetch_region(r, slot, shared2, start, region);
     if (success && region == size) {
-        allocator_shift(m, slot + 1, count, -1);
+        shift_regions(m, r, slot + 1, count, -1);
         if (threadIdx.x == 0) *m.count = count - 1;
     } else if (success && threadIdx.x == 0) {
         m.starts[slot] = start + size;
@@ -151,32 +174,42 @@ __device__ __forceinline__ void allocator_allocate(const AllocatorMeta &m, int32
 // tensor_buffer.py:94-179.  Returns the status in every thread.
 __device__ __forceinline__ int32_t allocator_free(const AllocatorMeta &m, int32_t *descriptor,
                                                   int32_t *scratch, int32_t *flag) {
+    __shared__ int32_t shared2[2];
     if (!allocator_lock(m.lock, flag)) return kStatusLock;
     const int32_t offset = descriptor[0];
     const int32_t size = descriptor[1];
     const int32_t status = descriptor[2];
     const int32_t generation = descriptor[3];
     const int32_t count = *m.count;
-    const bool valid = status == kStatusOk && generation == *m.generation && offset >= 0
+    const int32_t current_generation = *m.generation;
+    RegionRegs r;
+    load_regions(m, r);
+    const bool valid = status == kStatusOk && generation == current_generation && offset >= 0
         && size > 0;
     int32_t result = kStatusInvalid;
     if (valid) {
         int32_t below = 0;
-        for (int32_t i = threadIdx.x; i < count; i += kLanes) below += m.starts[i] < offset ? 1 : 0;
+#pragma unroll
+        for (int k = 0; k < kRegionsPerThread; ++k) {
+            const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kLanes;
+            below += (i < count && r.start[k] < offset) ? 1 : 0;
+        }
         const int32_t insert = block_sum(below, scratch);
         const bool has_prev = insert > 0, has_next = insert < count;
-        const int32_t prev_start = has_prev ? m.starts[insert - 1] : 0;
-        const int32_t prev_size = has_prev ? m.sizes[insert - 1] : 0;
-        const int32_t next_start = has_next ? m.starts[insert] : 0;
-        const int32_t next_size = has_next ? m.sizes[insert] : 0;
+        int32_t prev_start = 0, prev_size = 0, next_start = 0, next_size = 0;
+        fetch_region(r, has_prev ? insert - 1 : -1, shared2, prev_start, prev_size);
+        if (!has_prev) prev_start = prev_size = 0;
+        fetch_region(r, has_next ? insert : -1, shared2, next_start, next_size);
+        if (!has_next) next_start = next_size = 0;
         const bool merge_prev = has_prev && prev_start + prev_size == offset;
         const bool merge_next = has_next && offset + size == next_start;
-        __syncthreads();
         result = kStatusOk;
         if (merge_prev && merge_next) {
-            if (threadIdx.x == 0) m.sizes[insert - 1] = prev_size + size + next_size;
-            allocator_shift(m, insert + 1, count, -1);
-            if (threadIdx.x == 0) *m.count = count - 1;
+            if (threadIdx.x == 0) {
+                m.sizes[insert - 1] = prev_size + size + next_size;
+                *m.count = count - 1;
+            }
+            shift_regions(m, r, insert + 1, count, -1);
         } else if (merge_prev) {
             if (threadIdx.x == 0) m.sizes[insert - 1] = prev_size + size;
         } else if (merge_next) {
@@ -185,7 +218,7 @@ __device__ __forceinline__ int32_t allocator_free(const AllocatorMeta &m, int32_
                 m.sizes[insert] = next_size + size;
             }
         } else if (count < m.regions) {
-            allocator_shift(m, insert, count, +1);
+            shift_regions(m, r, insert, count, +1);
             if (threadIdx.x == 0) {
                 m.starts[insert] = offset;
                 m.sizes[insert] = size;

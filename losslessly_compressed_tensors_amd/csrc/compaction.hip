@@ -1,5 +1,6 @@
-// Overflow bookkeeping after the encoder: block prefix scans + arena
-// allocation (one workgroup), then per-block compaction of overflowing streams.
+// Overflow bookkeeping after the encoder: block prefix scans, block metadata
+// and arena allocation (one workgroup), then compaction of the overflowing
+// streams of the blocks that have any.
 //
 // Follows LCT/kernels/generic/metadata.py:13-38 and
 // LCT/kernels/generic/compaction.py:99-235 (summaries path).  The compact list
@@ -12,48 +13,83 @@
 namespace lct {
 namespace {
 
-constexpr int kPrefixPerThread = 32;   // 256 x 32 = 8192 blocks
+constexpr int kPrefixMaxBlocks = 8192;   // 3 x 8192 int32 of LDS
+constexpr int kCompactGrid = 2048;     // workgroups walking the overflow-block list
 
+// summaries layout (int32[5*nb + 1]): per-block overflow counts | tail bytes |
+// exclusive count scan | exclusive byte scan | list of blocks with overflow |
+// list length.  The encoder writes the first two; this kernel the rest.
 __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     int32_t *__restrict__ summaries, int32_t *__restrict__ counts,
     int32_t *__restrict__ descriptor, int32_t *__restrict__ buffer_meta,
-    int32_t n_blocks, int32_t buffered, int32_t max_free_regions) {
+    int32_t *__restrict__ blocks, int32_t n_blocks, int32_t buffered,
+    int32_t max_free_regions) {
+    // LDS: per-block counts | tail bytes (then byte scan) | count scan.
+    extern __shared__ int32_t lds[];
+    int32_t *c_lds = lds;
+    int32_t *v_lds = lds + n_blocks;
+    int32_t *cp_lds = lds + 2 * n_blocks;
     __shared__ int32_t scratch[kWavesPerBlock];
     __shared__ int32_t flag;
     const int t = threadIdx.x;
-    // Thread t owns the contiguous run [t*per, t*per + per) and keeps it in
-    // registers between the load, the block scan and the store.
-    const int per = (n_blocks + kLanes - 1) / kLanes;
-    const int begin = t * per;
-    int32_t counts_local[kPrefixPerThread], bytes_local[kPrefixPerThread];
-    int32_t local_count = 0, local_bytes = 0;
+    // Coalesced loads into LDS, all issued before the first LDS write.
+    constexpr int kRows = kPrefixMaxBlocks / kLanes;
+    int32_t c_reg[kRows], v_reg[kRows];
 #pragma unroll
-    for (int j = 0; j < kPrefixPerThread; ++j) {
-        const int b = begin + j;
-        const bool in = j < per && b < n_blocks;
-        counts_local[j] = in ? summaries[b] : 0;
-        bytes_local[j] = in ? summaries[n_blocks + b] : 0;
-        local_count += counts_local[j];
-        local_bytes += bytes_local[j];
+    for (int j = 0; j < kRows; ++j) {
+        const int b = j * kLanes + t;
+        c_reg[j] = b < n_blocks ? summaries[b] : 0;
+        v_reg[j] = b < n_blocks ? summaries[n_blocks + b] : 0;
     }
-    int32_t total_count, total_bytes;
-    int32_t count_run = block_exclusive_scan(local_count, scratch, &total_count);
-    int32_t byte_run = block_exclusive_scan(local_bytes, scratch, &total_bytes);
 #pragma unroll
-    for (int j = 0; j < kPrefixPerThread; ++j) {
-        const int b = begin + j;
-        if (j < per && b < n_blocks) {
-            summaries[2 * n_blocks + b] = count_run;
-            summaries[3 * n_blocks + b] = byte_run;
+    for (int j = 0; j < kRows; ++j) {
+        const int b = j * kLanes + t;
+        if (b < n_blocks) {
+            c_lds[b] = c_reg[j];
+            v_lds[b] = v_reg[j];
         }
-        count_run += counts_local[j];
-        byte_run += bytes_local[j];
+    }
+    __syncthreads();
+    // Thread t scans the contiguous run [t*per, t*per + per).
+    const int per = (n_blocks + kLanes - 1) / kLanes;
+    const int begin = min(t * per, n_blocks);
+    const int end = min(begin + per, n_blocks);
+    int32_t run_count = 0, run_bytes = 0, run_listed = 0;
+    for (int b = begin; b < end; ++b) {
+        run_count += c_lds[b];
+        run_bytes += v_lds[b];
+        run_listed += c_lds[b] > 0 ? 1 : 0;
+    }
+    int32_t total_count, total_bytes, total_listed;
+    int32_t count_before = block_exclusive_scan(run_count, scratch, &total_count);
+    int32_t byte_before = block_exclusive_scan(run_bytes, scratch, &total_bytes);
+    int32_t list_before = block_exclusive_scan(run_listed, scratch, &total_listed);
+    int32_t *list = summaries + 4 * n_blocks;
+    for (int b = begin; b < end; ++b) {
+        const int32_t count = c_lds[b];
+        const int32_t bytes = v_lds[b];
+        cp_lds[b] = count_before;
+        v_lds[b] = byte_before;
+        if (count > 0) list[list_before++] = b;
+        count_before += count;
+        byte_before += bytes;
+    }
+    __syncthreads();
+    // Coalesced stores of the scans and the block metadata.
+    for (int b = t; b < n_blocks; b += kLanes) {
+        const int32_t count = c_lds[b], first = cp_lds[b], byte_base = v_lds[b];
+        summaries[2 * n_blocks + b] = first;
+        summaries[3 * n_blocks + b] = byte_base;
+        blocks[b] = count;
+        blocks[n_blocks + b] = first;
+        blocks[2 * n_blocks + b] = byte_base;
     }
     if (t == 0) {
         counts[0] = total_count;
         counts[1] = total_bytes;
         counts[2] = 0;
         counts[3] = 0;
+        summaries[5 * n_blocks] = total_listed;
     }
     if (buffered) {
         // Two metadata bytes per overflowing stream: lane, then start step.
@@ -62,47 +98,47 @@ __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     }
 }
 
-__global__ __launch_bounds__(kLanes) void compact_extra_kernel(
-    const void *__restrict__ source, uint8_t *__restrict__ lanes,
-    uint8_t *__restrict__ starts, uint8_t *__restrict__ tail,
-    const int32_t *__restrict__ descriptor, const int32_t *__restrict__ count_total,
-    int32_t *__restrict__ blocks, int64_t base, const uint8_t *__restrict__ extra_starts,
-    const int32_t *__restrict__ summaries, int64_t n_blocks, int64_t logical_numel,
-    int S, int precomputed, int buffered) {
-    __shared__ int32_t scratch[kWavesPerBlock];
+// One codec block's overflow entries and tails (compaction.py:137-228).  The
+// block's tail bytes are produced one per thread: tail byte i belongs to the
+// overflowing lane whose local byte range holds i (binary search over the
+// lanes' offsets in LDS), so every byte is an independent load and the tail
+// stores are contiguous.
+__device__ __forceinline__ void compact_block(
+    const void *__restrict__ source, uint8_t *__restrict__ lanes, uint8_t *__restrict__ starts,
+    uint8_t *__restrict__ tail, int64_t lane_off, int64_t start_off, int64_t tail_off,
+    const int32_t *__restrict__ blocks, const uint8_t *__restrict__ extra_starts,
+    int64_t block, int64_t n_blocks, int64_t logical_numel, int S, int precomputed,
+    int32_t *scratch, int32_t *entry_offset, int32_t *entry_start, int32_t *entry_lane) {
     const int t = threadIdx.x;
-    const int64_t block = blockIdx.x;
-    const int32_t count = summaries[block];
-    const int32_t first = summaries[2 * n_blocks + block];
-    const int32_t byte_base = summaries[3 * n_blocks + block];
-    if (t == 0) {
-        blocks[block] = count;
-        blocks[n_blocks + block] = first;
-        blocks[2 * n_blocks + block] = byte_base;
-    }
-    if (count == 0) return;
-    int64_t lane_off = 0, start_off = 0, tail_off = base;
-    if (buffered) {
-        if (descriptor[2] != kStatusOk) return;   // failed allocation: write nothing
-        const int64_t arena = descriptor[0];
-        const int64_t total = count_total[0];
-        lane_off = arena;
-        start_off = arena + total;
-        tail_off = arena + 2 * total;
-    }
+    const int32_t count = blocks[block];
+    const int32_t first = blocks[n_blocks + block];
+    const int32_t byte_base = blocks[2 * n_blocks + block];
     const int32_t start = extra_starts[block * kLanes + t];
     const bool bad = start != 255;
-    int32_t ignored;
-    const int32_t local = block_exclusive_scan(bad ? S - start : 0, scratch, &ignored);
+    int32_t block_bytes, ignored;
+    const int32_t local = block_exclusive_scan(bad ? S - start : 0, scratch, &block_bytes);
     const int32_t rank = block_exclusive_scan(bad ? 1 : 0, scratch, &ignored);
-    if (!bad) return;
-    lanes[lane_off + first + rank] = static_cast<uint8_t>(t);
-    starts[start_off + first + rank] = static_cast<uint8_t>(start);
-    uint8_t *out = tail + tail_off + byte_base + local;
+    if (bad) {
+        lanes[lane_off + first + rank] = static_cast<uint8_t>(t);
+        starts[start_off + first + rank] = static_cast<uint8_t>(start);
+        entry_offset[rank] = local;
+        entry_start[rank] = start;
+        entry_lane[rank] = t;
+    }
+    __syncthreads();
+    uint8_t *out = tail + tail_off + byte_base;
     const int64_t row_base = block * S;
-    for (int row = start; row < S; ++row) {
+    for (int32_t i = t; i < block_bytes; i += kLanes) {
+        // Last entry whose offset is <= i.
+        int32_t lo = 0, hi = count - 1;
+        while (lo < hi) {
+            const int32_t mid = (lo + hi + 1) >> 1;
+            if (entry_offset[mid] <= i) lo = mid;
+            else hi = mid - 1;
+        }
+        const int32_t row = entry_start[lo] + (i - entry_offset[lo]);
         const int64_t logical = (row_base + row) * kLanes
-            + (t ^ static_cast<int32_t>((row_base + row) & 254));
+            + (entry_lane[lo] ^ static_cast<int32_t>((row_base + row) & 254));
         int32_t e = -127;
         if (logical < logical_numel) {
             if (precomputed) {
@@ -112,8 +148,35 @@ __global__ __launch_bounds__(kLanes) void compact_extra_kernel(
                 e = ((bits >> 7) & 255) - 127;
             }
         }
-        out[row - start] = static_cast<uint8_t>(e);
+        out[i] = static_cast<uint8_t>(e);
     }
+    __syncthreads();   // entry arrays are reused by the next listed block
+}
+
+__global__ __launch_bounds__(kLanes) void compact_extra_kernel(
+    const void *__restrict__ source, uint8_t *__restrict__ lanes,
+    uint8_t *__restrict__ starts, uint8_t *__restrict__ tail,
+    const int32_t *__restrict__ descriptor, const int32_t *__restrict__ count_total,
+    const int32_t *__restrict__ blocks, int64_t base, const uint8_t *__restrict__ extra_starts,
+    const int32_t *__restrict__ summaries, int64_t n_blocks, int64_t logical_numel,
+    int S, int precomputed, int buffered) {
+    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ int32_t entry_offset[kLanes], entry_start[kLanes], entry_lane[kLanes];
+    int64_t lane_off = 0, start_off = 0, tail_off = base;
+    if (buffered) {
+        if (descriptor[2] != kStatusOk) return;   // failed allocation: write nothing
+        const int64_t arena = descriptor[0];
+        const int64_t total = count_total[0];
+        lane_off = arena;
+        start_off = arena + total;
+        tail_off = arena + 2 * total;
+    }
+    const int32_t *list = summaries + 4 * n_blocks;
+    const int32_t listed = summaries[5 * n_blocks];
+    for (int32_t i = blockIdx.x; i < listed; i += gridDim.x)
+        compact_block(source, lanes, starts, tail, lane_off, start_off, tail_off, blocks,
+                      extra_starts, list[i], n_blocks, logical_numel, S, precomputed, scratch,
+                      entry_offset, entry_start, entry_lane);
 }
 
 }  // namespace
@@ -123,23 +186,30 @@ using namespace lct;
 
 extern "C" int32_t lct_prefix_allocate(int32_t *summaries, int32_t *counts,
                                        int32_t *descriptor, int32_t *buffer_meta,
-                                       int64_t n_blocks, int32_t buffered,
+                                       int32_t *blocks, int64_t n_blocks, int32_t buffered,
                                        int32_t max_free_regions, hipStream_t stream) {
-    if (!summaries || !counts) return LCT_E_NULL;
+    if (!summaries || !counts || !blocks) return LCT_E_NULL;
     if (buffered && (!descriptor || !buffer_meta)) return LCT_E_NULL;
-    if (n_blocks <= 0 || n_blocks > kLanes * kPrefixPerThread) return LCT_E_SIZE;
+    if (n_blocks <= 0 || n_blocks > kPrefixMaxBlocks) return LCT_E_SIZE;
     if (buffered && (max_free_regions <= 0 || max_free_regions > 4096
                      || (max_free_regions & (max_free_regions - 1)) != 0))
         return LCT_E_ARG;
-    hipLaunchKernelGGL(prefix_allocate_kernel, dim3(1), dim3(kLanes), 0, stream, summaries,
-                       counts, descriptor, buffer_meta, static_cast<int32_t>(n_blocks),
+    const size_t lds = 3 * static_cast<size_t>(n_blocks) * sizeof(int32_t);
+    if (lds > 64 * 1024) {
+        const hipError_t err = hipFuncSetAttribute(
+            reinterpret_cast<const void *>(prefix_allocate_kernel),
+            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (err != hipSuccess) return static_cast<int32_t>(err);
+    }
+    hipLaunchKernelGGL(prefix_allocate_kernel, dim3(1), dim3(kLanes), lds, stream, summaries,
+                       counts, descriptor, buffer_meta, blocks, static_cast<int32_t>(n_blocks),
                        buffered, max_free_regions);
     return static_cast<int32_t>(hipGetLastError());
 }
 
 extern "C" int32_t lct_compact_extra(const void *source, uint8_t *lanes, uint8_t *starts,
                                      uint8_t *tail, const int32_t *descriptor,
-                                     const int32_t *count, int32_t *blocks, int64_t base,
+                                     const int32_t *count, const int32_t *blocks, int64_t base,
                                      const uint8_t *extra_starts, const int32_t *summaries,
                                      int64_t size, int64_t logical_numel, lct_geometry g,
                                      int32_t precomputed, int32_t buffered,
@@ -151,8 +221,8 @@ extern "C" int32_t lct_compact_extra(const void *source, uint8_t *lanes, uint8_t
         return LCT_E_SIZE;
     const int64_t n_blocks = size / g.block_symbols;
     if (n_blocks > 0x7FFFFFFF) return LCT_E_SIZE;
-    hipLaunchKernelGGL(compact_extra_kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes),
-                       0, stream, source, lanes, starts, tail, descriptor, count, blocks, base,
+    const uint32_t grid = static_cast<uint32_t>(n_blocks < kCompactGrid ? n_blocks : kCompactGrid);
+    hipLaunchKernelGGL(compact_extra_kernel, dim3(grid), dim3(kLanes), 0, stream, source, lanes, starts, tail, descriptor, count, blocks, base,
                        extra_starts, summaries, n_blocks, logical_numel, g.steps, precomputed,
                        buffered);
     return static_cast<int32_t>(hipGetLastError());

@@ -101,6 +101,7 @@ __global__ __launch_bounds__(kLanes) void decode_kernel(
     stage_payload(stage, encoded, n_blocks * kLanes, block, W);
     const LaneOverlay lane = build_overlay(ov, has_overlay != 0, block, n_blocks, S, map_start,
                                            map_offset, scratch);
+    wait_memory();
     __syncthreads();
 
     const StreamCursor cursor{stage + threadIdx.x, &tb, 0u, static_cast<uint32_t>(W), rare};

@@ -58,20 +58,28 @@ __device__ __forceinline__ void build_decode_tables(DecodeTables &tb,
 }
 
 // Copy the W payload rows of `block` into stage rows 0..W-1 and zero the two
-// pad rows W, W+1 that a window at pos <= 32W may touch.
+// pad rows W, W+1 that a window at pos <= 32W may touch.  A payload row of a
+// block is 1 KiB contiguous in HBM; each row moves with one direct
+// global-to-LDS load per wave (64 lanes x 16 bytes), so staging takes no
+// registers.  The caller waits (vmcnt(0)) and synchronises before reading.
 __device__ __forceinline__ void stage_payload(uint32_t *stage, const int32_t *__restrict__ encoded,
                                               int64_t n_streams, int64_t block, int W) {
     const int t = threadIdx.x;
-    const int chunks = W * (kLanes / 4);
-    for (int c = t; c < chunks; c += kLanes) {
-        const int row = c / (kLanes / 4);
-        const int quad = c % (kLanes / 4);
-        const uint4 *src = reinterpret_cast<const uint4 *>(encoded + row * n_streams + block * kLanes);
-        reinterpret_cast<uint4 *>(stage + row * kLanes)[quad] = src[quad];
+    const int wave = t / kWave;
+    const int j = t % kWave;
+    for (int row = wave; row < W; row += kWavesPerBlock) {
+        const int32_t *src = encoded + row * n_streams + block * kLanes + j * 4;
+        __builtin_amdgcn_global_load_lds(
+            src, (__attribute__((address_space(3))) void *)(stage + row * kLanes),
+            16, 0, 0);
     }
     stage[W * kLanes + t] = 0u;
     stage[(W + 1) * kLanes + t] = 0u;
 }
+
+// Wait for this thread's outstanding memory operations (including direct
+// global-to-LDS loads) before a barrier publishes the staged data.
+__device__ __forceinline__ void wait_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Per-lane view of the overflow tails of one block.
 struct LaneOverlay {

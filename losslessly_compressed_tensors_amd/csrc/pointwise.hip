@@ -115,6 +115,7 @@ __global__ __launch_bounds__(kLanes) void pointwise_kernel(
     stage_payload(stage, encoded, n_blocks * kLanes, block, W);
     const LaneOverlay lane = build_overlay(ov, has_overlay != 0, block, n_blocks, S, map_start,
                                            map_offset, scratch);
+    wait_memory();
     __syncthreads();
 
     OpParams p{op, alpha_is_one, beta_is_one, 1.0f, 1.0f};
@@ -221,6 +222,7 @@ __global__ __launch_bounds__(kLanes) void dual_kernel(DualOperand a, DualOperand
     __syncthreads();
     const LaneOverlay b_lane = build_overlay(b.ov, b.has_overlay != 0, block, n_blocks, S,
                                              map_start, map_offset, scratch);
+    wait_memory();
     __syncthreads();
 
     const float alpha_value = alpha[0];

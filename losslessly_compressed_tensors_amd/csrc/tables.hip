@@ -23,32 +23,37 @@ __global__ __launch_bounds__(kLanes) void tables_kernel(
     const int t = threadIdx.x;
     int32_t center;
     if (estimate) {
-        // Region i is [i*n/M, (i+1)*n/M).  M is n itself (one element per
-        // region, jitter 0) or, in every call the codec makes, the power of
-        // two 4096; only other M pay for 64-bit division.
+        // Region i is [i*n/M, (i+1)*n/M).  M = min(n, 4096) is either n
+        // itself (one element per region, jitter 0) or a power of two (the
+        // entry point rejects any other M), so no 64-bit division is needed.
         const bool every = sample_size == logical_numel;
-        const bool pow2 = (sample_size & (sample_size - 1)) == 0;
         const int shift = __builtin_ctzll(static_cast<uint64_t>(sample_size));
+        // All of a thread's (at most 16) samples are loaded before any is used.
+        constexpr int kPerThread = kMaxSamples / kLanes;
+        int32_t raw[kPerThread];
+#pragma unroll
+        for (int k = 0; k < kPerThread; ++k) {
+            const int64_t i = t + k * kLanes;
+            raw[k] = 0x7FFFFFFF;
+            if (i < sample_size) {
+                int64_t pos = i;
+                if (!every) {
+                    const uint32_t hashed = static_cast<uint32_t>(i) * 0x9E3779B9u;
+                    const int64_t start = (i * logical_numel) >> shift;
+                    const int64_t end = ((i + 1) * logical_numel) >> shift;
+                    const uint64_t jitter =
+                        (static_cast<uint64_t>(hashed) * static_cast<uint64_t>(end - start)) >> 32;
+                    pos = start + static_cast<int64_t>(jitter);
+                }
+                raw[k] = precomputed ? static_cast<int32_t>(static_cast<const uint8_t *>(source)[pos])
+                                     : static_cast<int32_t>(static_cast<const int16_t *>(source)[pos]);
+            }
+        }
         int32_t sum = 0, kept = 0;
-        for (int64_t i = t; i < sample_size; i += kLanes) {
-            int64_t pos = i;
-            if (!every) {
-                const uint32_t hashed = static_cast<uint32_t>(i) * 0x9E3779B9u;
-                const int64_t start = pow2 ? (i * logical_numel) >> shift
-                                           : i * logical_numel / sample_size;
-                const int64_t end = pow2 ? ((i + 1) * logical_numel) >> shift
-                                         : (i + 1) * logical_numel / sample_size;
-                const uint64_t jitter =
-                    (static_cast<uint64_t>(hashed) * static_cast<uint64_t>(end - start)) >> 32;
-                pos = start + static_cast<int64_t>(jitter);
-            }
-            int32_t exp;
-            if (precomputed) {
-                exp = static_cast<int32_t>(static_cast<const uint8_t *>(source)[pos]) - 127;
-            } else {
-                const int32_t bits = static_cast<const int16_t *>(source)[pos];
-                exp = ((bits >> 7) & 0xFF) - 127;
-            }
+#pragma unroll
+        for (int k = 0; k < kPerThread; ++k) {
+            if (raw[k] == 0x7FFFFFFF) continue;
+            const int32_t exp = (precomputed ? raw[k] : (raw[k] >> 7) & 0xFF) - 127;
             if (exp >= -120) {
                 sum += exp;
                 kept += 1;
@@ -103,6 +108,8 @@ extern "C" int32_t lct_estimate_and_shift_tables(
     if (logical_numel <= 0 || sample_size <= 0 || sample_size > kMaxSamples
         || sample_size > logical_numel)
         return LCT_E_SIZE;
+    if (sample_size != logical_numel && (sample_size & (sample_size - 1)) != 0)
+        return LCT_E_ARG;
     hipLaunchKernelGGL(tables_kernel, dim3(1), dim3(kLanes), 0, stream, source,
                        precomputed, logical_numel, sample_size, base_encode,
                        base_decode, center, 1, shifted_encode, shifted_decode);

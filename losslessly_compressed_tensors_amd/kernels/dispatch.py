@@ -114,20 +114,23 @@ def encode_kernel(source, side, encoded, encode_table, extra_starts, summaries, 
              _stream(source))
 
 
-def prefix_allocate(summaries, counts, descriptor, buffer, blocks, buffered,
+def prefix_allocate(summaries, counts, descriptor, buffer, blocks_out, blocks, buffered,
                     max_free_regions) -> None:
-    """Block scans + optional arena reservation (``dispatch.py:70-85``)."""
+    """Block scans, block metadata, overflow-block list and optional arena
+    reservation (``dispatch.py:70-85`` plus the metadata half of
+    ``compact_extra``).  ``summaries`` is int32[5*blocks + 1]."""
     _require_device(summaries, counts)
     meta = buffer.storage if buffer is not None else None
     hip.call("lct_prefix_allocate", _ptr(summaries), _ptr(counts),
              _ptr(descriptor) if buffered else None, _ptr(meta) if buffered else None,
-             int(blocks), int(bool(buffered)), int(max_free_regions), _stream(summaries))
+             _ptr(blocks_out), int(blocks), int(bool(buffered)), int(max_free_regions),
+             _stream(summaries))
 
 
 def compact_extra(source, storage: FallbackStorage, n_blocks, n_elements, *, precomputed,
                   buffered, logical_numel, block_symbols, lanes, steps, extra_starts,
                   summaries) -> None:
-    """Per-block overflow entries, tails and block metadata (``dispatch.py:113-130``)."""
+    """Overflow entries and tails of the listed blocks (``dispatch.py:113-130``)."""
     _require_device(source, extra_starts, summaries)
     geometry = hip.Geometry(block_symbols, lanes, steps, 2)
     hip.call("lct_compact_extra", _ptr(source), _ptr(storage.lanes), _ptr(storage.starts),

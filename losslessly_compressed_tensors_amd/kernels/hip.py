@@ -56,7 +56,7 @@ _SIGNATURES = {
     "lct_shift_decoding_table": [_ptr, _ptr, _ptr, _ptr],
     "lct_encode": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64, _c_int64, Geometry, _c_int32,
                    _c_int32, _ptr],
-    "lct_prefix_allocate": [_ptr, _ptr, _ptr, _ptr, _c_int64, _c_int32, _c_int32, _ptr],
+    "lct_prefix_allocate": [_ptr, _ptr, _ptr, _ptr, _ptr, _c_int64, _c_int32, _c_int32, _ptr],
     "lct_compact_extra": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64, _ptr, _ptr,
                           _c_int64, _c_int64, Geometry, _c_int32, _c_int32, _ptr],
     "lct_decode": [_ptr, _ptr, _ptr, _ptr, _ptr, _c_int64, _c_int64, Geometry, _c_int32,

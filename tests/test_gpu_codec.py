@@ -122,3 +122,19 @@ def test_unaligned_view_roundtrip():
     o = oracle_compress(x.cpu(), dist)
     assert_matches_oracle(ct, o)
     assert np.array_equal(bits_of(decompress(ct)), bits_of(x))
+
+
+def test_large_block_count_metadata():
+    """7000 codec blocks (458 MB): the prefix scan's large-LDS configuration."""
+    require_gpu()
+    g = torch.Generator(device="cuda").manual_seed(11)
+    n = 7000 * 32768 - 12345
+    x = torch.randn(n, device="cuda", generator=g).to(torch.bfloat16)
+    dist = Distribution(DistType.GAUSSIAN)
+    ct = compress(x, dist)
+    o = oracle_compress(x.cpu(), dist)
+    assert np.array_equal(ct.fallback_blocks.cpu().numpy(), o.blocks)
+    assert ct.memory_size() == o.memory_size()
+    assert np.array_equal(ct.fallback_lanes.cpu().numpy(), o.lanes)
+    assert np.array_equal(ct.fallback_buffer.cpu().numpy(), o.tail)
+    assert torch.equal(decompress(ct).view(torch.int16), x.view(torch.int16))
