@@ -195,12 +195,9 @@ extern "C" int32_t lct_prefix_allocate(int32_t *summaries, int32_t *counts,
                      || (max_free_regions & (max_free_regions - 1)) != 0))
         return LCT_E_ARG;
     const size_t lds = 3 * static_cast<size_t>(n_blocks) * sizeof(int32_t);
-    if (lds > 64 * 1024) {
-        const hipError_t err = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(prefix_allocate_kernel),
-            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        if (err != hipSuccess) return static_cast<int32_t>(err);
-    }
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(prefix_allocate_kernel),
+                                           lds))
+        return static_cast<int32_t>(e);
     hipLaunchKernelGGL(prefix_allocate_kernel, dim3(1), dim3(kLanes), lds, stream, summaries,
                        counts, descriptor, buffer_meta, blocks, static_cast<int32_t>(n_blocks),
                        buffered, max_free_regions);

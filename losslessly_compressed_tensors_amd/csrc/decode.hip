@@ -8,72 +8,126 @@
 // past a stream's overflow start take their exponent from the tail bytes and
 // consume no payload bits.
 //
-// The step loop runs in 32-step chunks: while a chunk is decoded from the
-// wave's LDS side slice, the next chunk's side bytes are already in flight,
-// and the overflow check is only compiled into chunks that reach the wave's
-// first overflow start.
+// The step loop runs in 16-step chunks, each in two phases.  The decode
+// phase walks the 16 steps using only LDS (payload, tables, overflow tails)
+// and keeps the exponent fields in registers.  The store phase then waits for
+// the chunk's side bytes, which were fetched one chunk earlier, issues the next
+// chunk's fetch and writes the 16 BF16 values.  On gfx9 loads and stores share
+// one counter, so a wait for a load also waits for every older store: with the
+// decode phase between a chunk's stores and the next wait, those stores have
+// drained by the time the wave waits.  The overflow check is only compiled into
+// chunks that reach the wave's first overflow start.
 #include "decode_core.h"
 
 namespace lct {
 namespace {
 
-template <bool kFull, bool kOverlay>
-__device__ __forceinline__ void decode_chunk(StreamCursor &cursor, const LaneOverlay &lane,
-                                             const uint8_t *slice, __amdgpu_buffer_rsrc_t out,
-                                             int first_step, int64_t row_base,
-                                             uint32_t valid_in_block) {
-    const uint32_t t2 = threadIdx.x * 2u;
+// Tail bytes per block that are staged in LDS (larger blocks read HBM).
+constexpr int32_t kTailLds = 1024;
+
+// Byte offset of this lane's logical column within row `step` of the block;
+// rows step and step+1 share the swizzle mask.
+__device__ __forceinline__ uint32_t logical_col2(int64_t row_base, int step) {
+    return (threadIdx.x * 2u) ^ (static_cast<uint32_t>((row_base + step) & 254) * 2u);
+}
+
+// Overlay variants of a chunk: no lane of the wave overflows in it, or the
+// block's tails are read from LDS, or from HBM.
+enum Overlay { kNoOverlay, kLdsOverlay, kHbmOverlay };
+
+template <bool kFull, Overlay kOverlay>
+__device__ __forceinline__ void decode_fields(StreamCursor &cursor, const LaneOverlay &lane,
+                                              const uint8_t *tail_lds, int first_step,
+                                              int64_t row_base, uint32_t valid_in_block,
+                                              uint32_t (&f)[kChunkSteps]) {
+    // Every step of a no-overlay chunk of a full block precedes its lane's
+    // overflow start, so the cursor is inside the encoded bits.
+    constexpr bool kClamp = !kFull || kOverlay != kNoOverlay;
 #pragma unroll
     for (int j = 0; j < kChunkSteps; j += 2) {
         const int step = first_step + j;
-        uint32_t f0, len0, f1, len1;
-        cursor.next_pair(f0, len0, f1, len1);
-        if (kOverlay) overlay_pair(lane, step, f0, len0, f1, len1);
-        // Byte offset of the lane's logical column within its row; rows step
-        // and step+1 share the swizzle mask.
-        const uint32_t col2 = t2 ^ (static_cast<uint32_t>((row_base + step) & 254) * 2u);
-        const uint32_t out0 = join_bf16(f0, side_byte(slice, j));
-        const uint32_t out1 = join_bf16(f1, side_byte(slice, j + 1));
-        const int row_bytes = step * kLanes * 2;
-        if (kFull) {
-            __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(out0), out, col2, row_bytes, 0);
-            __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(out1), out, col2,
-                                                  row_bytes + kLanes * 2, 0);
-        } else {
-            const uint32_t off0 = static_cast<uint32_t>(step) * kLanes + (col2 >> 1);
-            const bool v0 = off0 < valid_in_block;
-            const bool v1 = off0 + kLanes < valid_in_block;
-            if (v0)
-                __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(out0), out, col2,
-                                                      row_bytes, 0);
-            if (v1)
-                __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(out1), out, col2,
-                                                      row_bytes + kLanes * 2, 0);
-            len0 = v0 ? len0 : 0u;
-            len1 = v1 ? len1 : 0u;
+        uint32_t f0, f1;
+        uint32_t sum = cursor.next_fields<kClamp>(f0, f1);
+        if (kOverlay != kNoOverlay)
+            overlay_pair<kOverlay == kLdsOverlay>(lane, tail_lds, step, f0, f1);
+        if (!kFull) {
+            // Padding positions of the last block consume no payload bits.
+            const uint32_t off0 = static_cast<uint32_t>(step) * kLanes
+                + (logical_col2(row_base, step) >> 1);
+            if (off0 >= valid_in_block) f0 &= ~31u;
+            if (off0 + kLanes >= valid_in_block) f1 &= ~31u;
         }
-        cursor.pos += len0 + len1;
+        if (kClamp) sum = (f0 + f1) & 127u;
+        f[j] = f0;
+        f[j + 1] = f1;
+        cursor.pos += sum;
     }
 }
 
-// S is a template parameter so the chunk loop has a fixed trip count.
-// `next` holds the side bytes of chunk 0, fetched by the caller.
-template <bool kFull, int S>
-__device__ __forceinline__ void decode_rows(StreamCursor cursor, const LaneOverlay &lane,
-                                            uint8_t *slice, __amdgpu_buffer_rsrc_t side,
-                                            SideChunk next, __amdgpu_buffer_rsrc_t out,
-                                            int64_t row_base, uint32_t valid_in_block) {
-    static_assert(S % kChunkSteps == 0, "whole chunks");
+// Store phase: each lane writes its two values per step pair with 2-byte
+// non-temporal stores (a wave covers 128 contiguous bytes of a row); the last
+// block masks positions past the tensor's end.  The chunk's first step and the
+// block's first row are multiples of 16, so the column of row first_step + j
+// is the chunk's column XOR 2j.
+template <bool kFull>
+__device__ __forceinline__ void store_fields(const uint32_t (&f)[kChunkSteps], const uint8_t *slice,
+                                             __amdgpu_buffer_rsrc_t out, int first_step,
+                                             int64_t row_base, uint32_t valid_in_block) {
+    const uint32_t chunk_col2 = logical_col2(row_base, first_step);
+#pragma unroll
+    for (int j = 0; j < kChunkSteps; j += 2) {
+        const int step = first_step + j;
+        const uint32_t col2 = chunk_col2 ^ static_cast<uint32_t>(2 * j);
+        const uint16_t out0 = static_cast<uint16_t>(join_entry(f[j], side_byte(slice, j)));
+        const uint16_t out1 = static_cast<uint16_t>(join_entry(f[j + 1], side_byte(slice, j + 1)));
+        const int row_bytes = step * kLanes * 2;
+        const uint32_t off0 = static_cast<uint32_t>(step) * kLanes + (col2 >> 1);
+        if (kFull || off0 < valid_in_block)
+            __builtin_amdgcn_raw_buffer_store_b16(out0, out, col2, row_bytes, kStreaming);
+        if (kFull || off0 + kLanes < valid_in_block)
+            __builtin_amdgcn_raw_buffer_store_b16(out1, out, col2, row_bytes + kLanes * 2,
+                                                  kStreaming);
+    }
+}
+
+// Chunks [c_begin, c_end) with one overlay variant.  `side_next` holds the side
+// bytes of chunk c_begin on entry and of chunk c_end on exit.
+template <bool kFull, Overlay kOverlay, int S>
+__device__ __forceinline__ void decode_chunks(StreamCursor &cursor, const LaneOverlay &lane,
+                                              const uint8_t *tail_lds, uint8_t *slice,
+                                              __amdgpu_buffer_rsrc_t side, SideChunk &side_next,
+                                              __amdgpu_buffer_rsrc_t out, int64_t row_base,
+                                              uint32_t valid_in_block, int c_begin, int c_end) {
     const uint32_t voffset = side_fetch_offset();
 #pragma unroll 1
-    for (int c = 0; c < S; c += kChunkSteps) {
-        store_side_chunk(slice, next);
-        if (c + kChunkSteps < S) next = fetch_side_chunk(side, voffset, c + kChunkSteps);
-        if (c + kChunkSteps > lane.wave_start)
-            decode_chunk<kFull, true>(cursor, lane, slice, out, c, row_base, valid_in_block);
-        else
-            decode_chunk<kFull, false>(cursor, lane, slice, out, c, row_base, valid_in_block);
+    for (int c = c_begin; c < c_end; c += kChunkSteps) {
+        uint32_t f[kChunkSteps];
+        decode_fields<kFull, kOverlay>(cursor, lane, tail_lds, c, row_base, valid_in_block, f);
+        store_side_chunk(slice, side_next);
+        if (c + kChunkSteps < S) side_next = fetch_side_chunk(side, voffset, c + kChunkSteps);
+        store_fields<kFull>(f, slice, out, c, row_base, valid_in_block);
     }
+}
+
+// S is a template parameter so the chunk loops have fixed bounds.  Chunks that
+// end at or before the wave's first overflow start skip the overlay check.
+template <bool kFull, int S>
+__device__ __forceinline__ void decode_rows(StreamCursor cursor, const LaneOverlay &lane,
+                                            const uint8_t *tail_lds, uint8_t *slice,
+                                            __amdgpu_buffer_rsrc_t side, SideChunk side_next,
+                                            __amdgpu_buffer_rsrc_t out, int64_t row_base,
+                                            uint32_t valid_in_block) {
+    static_assert(S % kChunkSteps == 0, "whole chunks");
+    const int split = min(S, lane.wave_start & ~(kChunkSteps - 1));
+    decode_chunks<kFull, kNoOverlay, S>(cursor, lane, tail_lds, slice, side, side_next, out,
+                                        row_base, valid_in_block, 0, split);
+    if (split == S) return;
+    if (lane.lds)
+        decode_chunks<kFull, kLdsOverlay, S>(cursor, lane, tail_lds, slice, side, side_next, out,
+                                             row_base, valid_in_block, split, S);
+    else
+        decode_chunks<kFull, kHbmOverlay, S>(cursor, lane, tail_lds, slice, side, side_next, out,
+                                             row_base, valid_in_block, split, S);
 }
 
 __global__ __launch_bounds__(kLanes) void decode_kernel(
@@ -81,10 +135,15 @@ __global__ __launch_bounds__(kLanes) void decode_kernel(
     uint16_t *__restrict__ output, const int32_t *__restrict__ shifted_decode,
     const int32_t *__restrict__ center_ptr, int64_t n_blocks, int64_t logical_numel, int S,
     int W, int rare, lct_overflow ov, int has_overlay) {
-    extern __shared__ uint32_t stage[];   // (W + 2) rows x 256
+    extern __shared__ uint32_t stage[];   // stage_bytes(W)
     __shared__ DecodeTables tb;
-    __shared__ int32_t map_start[kLanes], map_offset[kLanes], scratch[kWavesPerBlock];
+    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ uint8_t tail_lds[kTailLds];
+    // The overflow maps (2 KiB) are only used before the first side chunk is
+    // stored, so they share the side slices' LDS.
     __shared__ __attribute__((aligned(16))) uint8_t side_slices[kWavesPerBlock][kChunkSteps * kWave];
+    int32_t *map_start = reinterpret_cast<int32_t *>(&side_slices[0][0]);
+    int32_t *map_offset = map_start + kLanes;
     const int64_t block = blockIdx.x;
     const int64_t row_base = block * S;
     const int64_t logical_base = row_base * kLanes;
@@ -100,22 +159,26 @@ __global__ __launch_bounds__(kLanes) void decode_kernel(
     build_decode_tables(tb, shifted_decode, center);
     stage_payload(stage, encoded, n_blocks * kLanes, block, W);
     const LaneOverlay lane = build_overlay(ov, has_overlay != 0, block, n_blocks, S, map_start,
-                                           map_offset, scratch);
+                                           map_offset, scratch, tail_lds, kTailLds);
     wait_memory();
-    __syncthreads();
+    __syncthreads();   // payload and tails visible; overflow maps no longer read
 
-    const StreamCursor cursor{stage + threadIdx.x, &tb, 0u, static_cast<uint32_t>(W), rare};
+    const StreamCursor cursor{stage + threadIdx.x, &tb, 0u, static_cast<uint32_t>(W - 1), rare};
     uint8_t *slice = side_slices[threadIdx.x / kWave];
     if (valid == block_elems) {
         if (S == 128)
-            decode_rows<true, 128>(cursor, lane, slice, side_rsrc, first, out_rsrc, row_base, valid);
+            decode_rows<true, 128>(cursor, lane, tail_lds, slice, side_rsrc, first, out_rsrc,
+                                   row_base, valid);
         else
-            decode_rows<true, 256>(cursor, lane, slice, side_rsrc, first, out_rsrc, row_base, valid);
+            decode_rows<true, 256>(cursor, lane, tail_lds, slice, side_rsrc, first, out_rsrc,
+                                   row_base, valid);
     } else {
         if (S == 128)
-            decode_rows<false, 128>(cursor, lane, slice, side_rsrc, first, out_rsrc, row_base, valid);
+            decode_rows<false, 128>(cursor, lane, tail_lds, slice, side_rsrc, first, out_rsrc,
+                                    row_base, valid);
         else
-            decode_rows<false, 256>(cursor, lane, slice, side_rsrc, first, out_rsrc, row_base, valid);
+            decode_rows<false, 256>(cursor, lane, tail_lds, slice, side_rsrc, first, out_rsrc,
+                                    row_base, valid);
     }
 }
 
@@ -145,7 +208,9 @@ extern "C" int32_t lct_decode(const int32_t *encoded, const uint8_t *side, int16
     }
     const int64_t n_blocks = size / g.block_symbols;
     if (n_blocks > 0x7FFFFFFF) return LCT_E_SIZE;
-    const size_t lds = static_cast<size_t>(g.fixed_words + 2) * kLanes * sizeof(uint32_t);
+    const size_t lds = static_cast<size_t>(stage_bytes(g.fixed_words));
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&decode_kernel), lds))
+        return static_cast<int32_t>(e);
     hipLaunchKernelGGL(decode_kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes), lds,
                        stream, encoded, side, reinterpret_cast<uint16_t *>(output),
                        shifted_decode, center, n_blocks, logical_numel, g.steps, g.fixed_words,

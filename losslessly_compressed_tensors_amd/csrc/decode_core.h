@@ -19,7 +19,7 @@
 //    branch that reads the 8-bit literal;
 //  * a second 256-entry table maps an escaped table index to its exponent
 //    field under the tensor's center;
-//  * side bytes are fetched with 16-byte buffer loads one 32-step chunk ahead
+//  * side bytes are fetched with 16-byte buffer loads one 16-step chunk ahead
 //    of use and handed to the lanes through a wave-private LDS slice, so HBM
 //    latency overlaps a whole chunk of decoding; outputs go out through raw
 //    buffer stores (SGPR base, 32-bit lane offset).
@@ -31,7 +31,10 @@ namespace lct {
 
 // Buffer resource word 3 for gfx9-family raw buffers.
 constexpr int32_t kBufferConfig = 0x00020000;
-constexpr int kChunkSteps = 32;   // steps per prefetched side-byte chunk
+// Cache policy of streamed data (read or written once): non-temporal.  On
+// gfx950 this lifts the decoder's mixed read/write traffic by 6-10%.
+constexpr int kStreaming = 2;
+constexpr int kChunkSteps = 16;   // steps per prefetched side-byte chunk
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes),
@@ -40,7 +43,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
 
 struct DecodeTables {
     uint16_t entry[256];
-    uint32_t escape[256];
+    uint16_t escape[256];
 };
 
 // Build both tables from the 1024-entry shifted decode table (len | exp << 8).
@@ -54,12 +57,12 @@ __device__ __forceinline__ void build_decode_tables(DecodeTables &tb,
     tb.entry[t] = static_cast<uint16_t>((length >= 1 && length <= 8)
                                             ? (static_cast<uint32_t>(length) | field)
                                             : static_cast<uint32_t>(kEscapeLength));
-    tb.escape[t] = static_cast<uint32_t>((index_to_exponent(t, center) + 127) & 255) << 7;
+    tb.escape[t] = static_cast<uint16_t>(((index_to_exponent(t, center) + 127) & 255) << 7);
 }
 
-// Copy the W payload rows of `block` into stage rows 0..W-1 and zero the two
-// pad rows W, W+1 that a window at pos <= 32W may touch.  A payload row of a
-// block is 1 KiB contiguous in HBM; each row moves with one direct
+// Copy the W payload rows of `block` into stage rows 0..W-1 and zero the pad
+// row W that a window starting in row W-1 reads as its high word.  A payload
+// row of a block is 1 KiB contiguous in HBM; each row moves with one direct
 // global-to-LDS load per wave (64 lanes x 16 bytes), so staging takes no
 // registers.  The caller waits (vmcnt(0)) and synchronises before reading.
 __device__ __forceinline__ void stage_payload(uint32_t *stage, const int32_t *__restrict__ encoded,
@@ -74,8 +77,10 @@ __device__ __forceinline__ void stage_payload(uint32_t *stage, const int32_t *__
             16, 0, 0);
     }
     stage[W * kLanes + t] = 0u;
-    stage[(W + 1) * kLanes + t] = 0u;
 }
+
+// LDS bytes of the payload stage for W words per stream (W rows + 1 pad row).
+__host__ __device__ constexpr int32_t stage_bytes(int W) { return (W + 1) * kLanes * 4; }
 
 // Wait for this thread's outstanding memory operations (including direct
 // global-to-LDS loads) before a barrier publishes the staged data.
@@ -83,22 +88,27 @@ __device__ __forceinline__ void wait_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Per-lane view of the overflow tails of one block.
 struct LaneOverlay {
-    const uint8_t *tail;   // tail bytes of this lane start at tail[offset]
+    const uint8_t *tail;   // global tail bytes of this lane start at tail[offset]
     int32_t start;         // first overflow step, S if none
-    int32_t offset;
+    int32_t offset;        // byte offset of this lane's tail (LDS-relative if lds)
     int32_t wave_start;    // minimum `start` over the wave (wave-uniform)
+    int32_t lds;           // block-uniform: the block's tails were staged in LDS
 };
 
 // Expand the block's compact overflow list into per-lane (start, offset), as
-// decode.py:195-240 does.  Contains barriers; every thread of the block must
-// call it.  A buffered tensor whose allocation failed (descriptor status != 0)
-// has no tails and is decoded without overlay.
+// decode.py:195-240 does.  When `tail_lds` is given and the block's tail bytes
+// fit in `tail_cap`, they are copied into tail_lds so the step loop reads its
+// overlay from LDS instead of issuing global loads.  Contains barriers; every
+// thread of the block must call it, and the caller synchronises once more
+// before reading tail_lds.  A buffered tensor whose allocation failed
+// (descriptor status != 0) has no tails and is decoded without overlay.
 __device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, bool present,
                                                      int64_t block, int64_t n_blocks, int S,
                                                      int32_t *map_start, int32_t *map_offset,
-                                                     int32_t *scratch) {
+                                                     int32_t *scratch, uint8_t *tail_lds,
+                                                     int32_t tail_cap) {
     const int t = threadIdx.x;
-    LaneOverlay lane{nullptr, S, 0, S};
+    LaneOverlay lane{nullptr, S, 0, S, 0};
     int32_t count = 0;
     if (present) {
         count = ov.blocks[block];
@@ -123,74 +133,108 @@ __device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, boo
         entry_lane = ov.lanes[lane_off + first + t];
         entry_start = ov.starts[start_off + first + t];
     }
-    int32_t ignored;
-    const int32_t local = block_exclusive_scan(valid ? S - entry_start : 0, scratch, &ignored);
+    int32_t block_bytes;
+    const int32_t local = block_exclusive_scan(valid ? S - entry_start : 0, scratch, &block_bytes);
+    block_bytes = __builtin_amdgcn_readfirstlane(block_bytes);
+    const bool staged = tail_lds != nullptr && block_bytes <= tail_cap;
     if (valid) {
         map_start[entry_lane] = entry_start;
-        map_offset[entry_lane] = byte_base + local;
+        map_offset[entry_lane] = staged ? local : byte_base + local;
+    }
+    lane.tail = ov.tail + tail_base;
+    if (staged) {
+        const uint8_t *src = lane.tail + byte_base;
+        for (int i = t; i < block_bytes; i += kLanes) tail_lds[i] = src[i];
     }
     __syncthreads();
-    lane.tail = ov.tail + tail_base;
     lane.start = map_start[t];
     lane.offset = map_offset[t];
     lane.wave_start = __builtin_amdgcn_readfirstlane(wave_min(lane.start));
+    lane.lds = staged ? 1 : 0;
     return lane;
 }
 
 // One lane's stream cursor.
+//
+// A decoded symbol is carried as its table entry: bits 0..4 hold the code
+// length and bits 7..14 the BF16 exponent field, so two entries' lengths add
+// without masking first: (t0 + t1) & 127 = len0 + len1, since each length is at
+// most 31 and the exponent fields start at bit 7.  Direct codes are 1..8 bits,
+// so the sum reaches 32 only when an entry holds the escape marker.
 struct StreamCursor {
     const uint32_t *stage;    // stage + lane; row r at stage[r * 256]
     const DecodeTables *tb;
     uint32_t pos;
-    uint32_t last_row;        // W: clamp so corrupt payloads stay inside the stage
+    uint32_t last_row;        // W - 1
     int32_t rare;
 
-    // Decode the next two symbols: exponent fields (bits 7..14) and lengths.
-    __device__ __forceinline__ void next_pair(uint32_t &f0, uint32_t &len0, uint32_t &f1,
-                                              uint32_t &len1) const {
-        const uint32_t row = min(pos >> 5, last_row);
+    // Decode the next two symbols into entries f0/f1 (length | field << 7) and
+    // return len0 + len1.  kClamp keeps a position at or past the end of the
+    // payload inside the stage: needed where a lane may already be past its
+    // last encoded symbol (overflowed lanes, padding of the last block).
+    template <bool kClamp>
+    __device__ __forceinline__ uint32_t next_fields(uint32_t &f0, uint32_t &f1) const {
+        // An opaque shift keeps row * 1024 + lane at two instructions (shift,
+        // lshl_add); the compiler rewrites (pos >> 5) << 10 into three.
+        uint32_t row;
+        asm("v_lshrrev_b32 %0, 5, %1" : "=v"(row) : "v"(pos));
+        if (kClamp) row = min(row, last_row);
         const uint32_t lo = stage[row * kLanes];
         const uint32_t hi = stage[(row + 1) * kLanes];
         const uint32_t bits = __builtin_amdgcn_alignbit(hi, lo, pos);
         uint32_t t0 = tb->entry[bits & 255u];
-        uint32_t l0 = t0 & 31u;
-        uint32_t t1 = tb->entry[(bits >> l0) & 255u];
-        uint32_t l1 = t1 & 31u;
-        if (__any(l0 + l1 >= 32u)) {
+        // ubfe reads its offset from t0[4:0], the first code's length.
+        uint32_t t1 = tb->entry[__builtin_amdgcn_ubfe(bits, t0, 8)];
+        uint32_t sum = (t0 + t1) & 127u;
+        if (__any(sum >= 32u)) {
             // ESC + 8-bit literal table index (primitives.py:29-35).
+            const uint32_t escaped = static_cast<uint32_t>(rare) + 8u;
+            uint32_t l0 = t0 & 31u;
             if (l0 == kEscapeLength) {
-                t0 = tb->escape[(bits >> rare) & 255u];
-                l0 = static_cast<uint32_t>(rare) + 8u;
+                l0 = escaped;
+                t0 = tb->escape[(bits >> rare) & 255u] | escaped;
                 t1 = tb->entry[(bits >> l0) & 255u];
-                l1 = t1 & 31u;
             }
-            if (l1 == kEscapeLength) {
-                t1 = tb->escape[(bits >> (l0 + static_cast<uint32_t>(rare))) & 255u];
-                l1 = static_cast<uint32_t>(rare) + 8u;
-            }
+            if ((t1 & 31u) == kEscapeLength)
+                t1 = tb->escape[(bits >> (l0 + static_cast<uint32_t>(rare))) & 255u] | escaped;
+            sum = (t0 + t1) & 127u;
         }
         f0 = t0;
         f1 = t1;
-        len0 = l0;
-        len1 = l1;
+        return sum;
     }
 };
+
+// BF16 bits of a decoded entry (exponent field at bits 7..14, nothing at bit 15
+// or above) and its side byte: one multiply and one bit-field insert
+// (v_bfi_b32 takes bits 0..6 and 15 from the spread side byte and the rest
+// from the entry; the compiler otherwise narrows the masks and emits three
+// instructions).
+__device__ __forceinline__ uint32_t join_entry(uint32_t entry, uint32_t sm) {
+    const uint32_t spread = sm * 257u;   // sign at bit 15, mantissa at bits 0..6
+    uint32_t out;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(out) : "s"(0x807Fu), "v"(spread), "v"(entry));
+    return out;
+}
 
 // Exponent field of an overflow tail byte int8(e - 127).
 __device__ __forceinline__ uint32_t tail_field(uint32_t byte) {
     return ((byte + 127u) & 255u) << 7;
 }
 
-// Overlay one lane's pair if it is at/after its overflow start: exponents come
-// from the tail bytes and the pair consumes no payload bits.
-__device__ __forceinline__ void overlay_pair(const LaneOverlay &lane, int step, uint32_t &f0,
-                                             uint32_t &len0, uint32_t &f1, uint32_t &len1) {
+// Overlay one lane's pair if it is at/after its overflow start: the entries
+// become the tail bytes' exponent fields with length 0, so the pair consumes
+// no payload bits.  kLdsTails picks the block's LDS copy (build_overlay staged
+// it) or the tails in HBM; the two are separate instantiations so LDS reads
+// stay ds_read instructions.
+template <bool kLdsTails>
+__device__ __forceinline__ void overlay_pair(const LaneOverlay &lane, const uint8_t *tail_lds,
+                                             int step, uint32_t &f0, uint32_t &f1) {
     if (step >= lane.start) {
-        const uint8_t *src = lane.tail + lane.offset + (step - lane.start);
-        f0 = tail_field(src[0]);
-        f1 = tail_field(src[1]);
-        len0 = 0;
-        len1 = 0;
+        const int32_t i = lane.offset + (step - lane.start);
+        const uint8_t *src = kLdsTails ? tail_lds : lane.tail;
+        f0 = tail_field(src[i]);
+        f1 = tail_field(src[i + 1]);
     }
 }
 
@@ -198,10 +242,10 @@ __device__ __forceinline__ void overlay_pair(const LaneOverlay &lane, int step, 
 // fetches 16 contiguous bytes of its wave's 64-byte row segments (one
 // 16-byte buffer load covers 16 steps x 64 lanes per wave instruction), the
 // wave stores them to its slice and each lane then reads its own byte per step
-// (64 consecutive bytes per step: conflict-free).  A chunk is 32 steps, so one
-// chunk is 2 KiB per wave and two 16-byte loads per lane.
+// (64 consecutive bytes per step: conflict-free).  A chunk is 16 steps: 1 KiB
+// per wave, one 16-byte load per lane.
 struct SideChunk {
-    uint4 q0, q1;
+    uint4 q0;
 };
 
 // Buffer offset of this lane's 16 bytes within a 16-step group.
@@ -215,17 +259,14 @@ __device__ __forceinline__ SideChunk fetch_side_chunk(__amdgpu_buffer_rsrc_t sid
                                                       uint32_t voffset, int first_step) {
     SideChunk c;
     c.q0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                         side, voffset, first_step * kLanes, 0));
-    c.q1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                         side, voffset, (first_step + 16) * kLanes, 0));
+                                         side, voffset, first_step * kLanes, kStreaming));
     return c;
 }
 
-// slice: this wave's 2 KiB; byte s*64 + lane holds step s of the chunk.
+// slice: this wave's 1 KiB; byte s*64 + lane holds step s of the chunk.
 __device__ __forceinline__ void store_side_chunk(uint8_t *slice, const SideChunk &c) {
     const uint32_t j = threadIdx.x & (kWave - 1);
     reinterpret_cast<uint4 *>(slice)[j] = c.q0;
-    reinterpret_cast<uint4 *>(slice + 1024)[j] = c.q1;
 }
 
 __device__ __forceinline__ uint32_t side_byte(const uint8_t *slice, int step_in_chunk) {

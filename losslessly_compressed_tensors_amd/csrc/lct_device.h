@@ -126,4 +126,12 @@ inline bool geometry_ok(const lct_geometry &g) {
         && g.fixed_words <= kMaxWords;
 }
 
+// Lift a kernel's dynamic LDS limit above the 64 KiB default when a launch
+// needs more (the device allows 160 KiB per workgroup).
+inline hipError_t reserve_dynamic_lds(const void *kernel, size_t bytes) {
+    if (bytes <= 65536) return hipSuccess;
+    return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(bytes));
+}
+
 }  // namespace lct

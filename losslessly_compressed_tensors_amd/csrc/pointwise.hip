@@ -73,12 +73,13 @@ __device__ __forceinline__ void pointwise_rows(const StreamCursor &cursor_in, co
     const uint32_t t = threadIdx.x;
 #pragma unroll 2
     for (int step = 0; step < S; step += 2) {
-        uint32_t f0, len0, f1, len1;
-        cursor.next_pair(f0, len0, f1, len1);
+        uint32_t f0, f1;
+        cursor.next_fields<true>(f0, f1);
         const uint32_t slot = static_cast<uint32_t>(step) * kLanes + t;
         const uint32_t sm0 = side_block[slot];
         const uint32_t sm1 = side_block[slot + kLanes];
-        overlay_pair(lane, step, f0, len0, f1, len1);
+        overlay_pair<false>(lane, nullptr, step, f0, f1);
+        uint32_t len0 = f0 & 31u, len1 = f1 & 31u;
         const uint32_t col = t ^ static_cast<uint32_t>((row_base + step) & 254);
         const uint32_t off0 = static_cast<uint32_t>(step) * kLanes + col;
         const uint32_t off1 = off0 + kLanes;
@@ -114,7 +115,7 @@ __global__ __launch_bounds__(kLanes) void pointwise_kernel(
     build_decode_tables(tb, shifted_decode, center_ptr[0]);
     stage_payload(stage, encoded, n_blocks * kLanes, block, W);
     const LaneOverlay lane = build_overlay(ov, has_overlay != 0, block, n_blocks, S, map_start,
-                                           map_offset, scratch);
+                                           map_offset, scratch, nullptr, 0);
     wait_memory();
     __syncthreads();
 
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(kLanes) void pointwise_kernel(
         if (!alpha_is_one) p.alpha = alpha[0];
         if (!beta_is_one) p.beta = beta[0];
     }
-    const StreamCursor cursor{stage + threadIdx.x, &tb, 0u, static_cast<uint32_t>(W), rare};
+    const StreamCursor cursor{stage + threadIdx.x, &tb, 0u, static_cast<uint32_t>(W - 1), rare};
     const int64_t row_base = block * S;
     const int64_t logical_base = row_base * kLanes;
     const uint8_t *side_block = side + logical_base;
@@ -161,14 +162,15 @@ __device__ __forceinline__ void dual_rows(const StreamCursor &a_in, const LaneOv
     const uint32_t t = threadIdx.x;
 #pragma unroll 2
     for (int step = 0; step < S; step += 2) {
-        uint32_t af0, alen0, af1, alen1, bf0, blen0, bf1, blen1;
-        a.next_pair(af0, alen0, af1, alen1);
-        b.next_pair(bf0, blen0, bf1, blen1);
+        uint32_t af0, af1, bf0, bf1;
+        a.next_fields<true>(af0, af1);
+        b.next_fields<true>(bf0, bf1);
         const uint32_t slot = static_cast<uint32_t>(step) * kLanes + t;
         const uint32_t asm0 = a_side[slot], asm1 = a_side[slot + kLanes];
         const uint32_t bsm0 = b_side[slot], bsm1 = b_side[slot + kLanes];
-        overlay_pair(a_lane, step, af0, alen0, af1, alen1);
-        overlay_pair(b_lane, step, bf0, blen0, bf1, blen1);
+        overlay_pair<false>(a_lane, nullptr, step, af0, af1);
+        overlay_pair<false>(b_lane, nullptr, step, bf0, bf1);
+        uint32_t alen0 = af0 & 31u, alen1 = af1 & 31u, blen0 = bf0 & 31u, blen1 = bf1 & 31u;
         const uint32_t col = t ^ static_cast<uint32_t>((row_base + step) & 254);
         const uint32_t off0 = static_cast<uint32_t>(step) * kLanes + col;
         const uint32_t off1 = off0 + kLanes;
@@ -207,27 +209,27 @@ __global__ __launch_bounds__(kLanes) void dual_kernel(DualOperand a, DualOperand
                                                       void *output, uint8_t *auxiliary,
                                                       int64_t n_blocks, int64_t logical_numel,
                                                       int S, int W, int rare, int policy) {
-    extern __shared__ uint32_t stage[];   // two stages of (W + 2) rows x 256
+    extern __shared__ uint32_t stage[];   // two stages of stage_bytes(W)
     __shared__ DecodeTables tb_a, tb_b;
     __shared__ int32_t map_start[kLanes], map_offset[kLanes], scratch[kWavesPerBlock];
     const int64_t block = blockIdx.x;
     uint32_t *stage_a = stage;
-    uint32_t *stage_b = stage + (W + 2) * kLanes;
+    uint32_t *stage_b = stage + stage_bytes(W) / 4;
     build_decode_tables(tb_a, a.shifted_decode, a.center[0]);
     build_decode_tables(tb_b, b.shifted_decode, b.center[0]);
     stage_payload(stage_a, a.encoded, n_blocks * kLanes, block, W);
     stage_payload(stage_b, b.encoded, n_blocks * kLanes, block, W);
     const LaneOverlay a_lane = build_overlay(a.ov, a.has_overlay != 0, block, n_blocks, S,
-                                             map_start, map_offset, scratch);
+                                             map_start, map_offset, scratch, nullptr, 0);
     __syncthreads();
     const LaneOverlay b_lane = build_overlay(b.ov, b.has_overlay != 0, block, n_blocks, S,
-                                             map_start, map_offset, scratch);
+                                             map_start, map_offset, scratch, nullptr, 0);
     wait_memory();
     __syncthreads();
 
     const float alpha_value = alpha[0];
-    const StreamCursor ca{stage_a + threadIdx.x, &tb_a, 0u, static_cast<uint32_t>(W), rare};
-    const StreamCursor cb{stage_b + threadIdx.x, &tb_b, 0u, static_cast<uint32_t>(W), rare};
+    const StreamCursor ca{stage_a + threadIdx.x, &tb_a, 0u, static_cast<uint32_t>(W - 1), rare};
+    const StreamCursor cb{stage_b + threadIdx.x, &tb_b, 0u, static_cast<uint32_t>(W - 1), rare};
     const int64_t row_base = block * S;
     const int64_t logical_base = row_base * kLanes;
     uint16_t *dense_block = static_cast<uint16_t *>(output) + logical_base;
@@ -296,7 +298,9 @@ extern "C" int32_t lct_pointwise_dense(const int32_t *encoded, const uint8_t *si
     if ((reinterpret_cast<uintptr_t>(encoded) & 15) != 0) return LCT_E_ARG;
     const lct_overflow ov = overflow ? *overflow : lct_overflow{};
     const int64_t n_blocks = size / g.block_symbols;
-    const size_t lds = static_cast<size_t>(g.fixed_words + 2) * kLanes * sizeof(uint32_t);
+    const size_t lds = static_cast<size_t>(stage_bytes(g.fixed_words));
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&pointwise_kernel), lds))
+        return static_cast<int32_t>(e);
     hipLaunchKernelGGL(pointwise_kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes), lds,
                        stream, encoded, side, static_cast<const uint16_t *>(other), output,
                        auxiliary, shifted_decode, center, alpha, beta, n_blocks, logical_numel,
@@ -329,7 +333,9 @@ extern "C" int32_t lct_dual(const int32_t *a_encoded, const uint8_t *a_side,
     const DualOperand b{b_encoded, b_side, b_shifted_decode, b_center,
                         b_overflow ? *b_overflow : lct_overflow{}, b_overflow != nullptr};
     const int64_t n_blocks = size / g.block_symbols;
-    const size_t lds = 2 * static_cast<size_t>(g.fixed_words + 2) * kLanes * sizeof(uint32_t);
+    const size_t lds = 2 * static_cast<size_t>(stage_bytes(g.fixed_words));
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&dual_kernel), lds))
+        return static_cast<int32_t>(e);
     hipLaunchKernelGGL(dual_kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes), lds,
                        stream, a, b, alpha, output, auxiliary, n_blocks, logical_numel, g.steps,
                        g.fixed_words, rare_length, output_policy);
