@@ -1,0 +1,93 @@
+"""The C-ABI boundary (CPU): header, library exports and argument checks.
+
+``include/lct.h`` declares the entry points that replace the reference's
+operator boundary (LCT/kernels/dispatch.py).  The built library must export
+exactly those symbols, the ctypes binding must agree with the declared
+argument counts, and every entry point must reject bad arguments before it
+touches the GPU (these calls launch nothing).
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+from losslessly_compressed_tensors_amd.kernels import hip
+
+HEADER = ROOT / "include" / "lct.h"
+LCT_E_NULL, LCT_E_GEOMETRY, LCT_E_SIZE, LCT_E_ARG = -1, -2, -3, -4
+
+
+def _declarations() -> dict[str, int]:
+    """name -> number of parameters, from the header's prototypes."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for match in re.finditer(r"(?:int32_t|const char \*)\s*(lct_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = match.group(2).strip()
+        out[match.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not hip.LIBRARY_PATH.exists():
+        pytest.skip("liblct_hip.so not built (python -m losslessly_compressed_tensors_amd.build)")
+    return hip.load_library()
+
+
+def test_header_declares_every_binding():
+    declared = _declarations()
+    assert set(declared) == set(hip.EXPORTED)
+    for name, argtypes in hip._SIGNATURES.items():
+        assert declared[name] == len(argtypes), name
+
+
+def test_library_exports_exactly_the_header(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(hip.LIBRARY_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines()
+                if line.split() and line.split()[-1].startswith("lct_")}
+    assert exported == set(_declarations())
+
+
+def test_version_and_error_strings(lib):
+    assert lib.lct_version().decode().startswith("lct-hip-gfx950")
+    for code in (LCT_E_NULL, LCT_E_GEOMETRY, LCT_E_SIZE, LCT_E_ARG):
+        assert lib.lct_error_string(code)
+
+
+def _nulls(name):
+    """Arguments for ``name`` with every pointer NULL and plain scalars."""
+    args = []
+    for argtype in hip._SIGNATURES[name]:
+        if argtype is hip.Geometry:
+            args.append(hip.Geometry(32768, 256, 128, 12))
+        elif argtype in (ctypes.c_int32, ctypes.c_int64):
+            args.append(argtype(1))
+        else:
+            args.append(None)
+    return args
+
+
+@pytest.mark.parametrize("name", sorted(hip._SIGNATURES))
+def test_null_pointers_are_rejected(lib, name):
+    assert getattr(lib, name)(*_nulls(name)) == LCT_E_NULL
+
+
+def test_bad_geometry_is_rejected_before_launch(lib):
+    fake = ctypes.c_void_p(1 << 20)   # never dereferenced: geometry fails first
+    for geometry in [hip.Geometry(32768, 256, 100, 12), hip.Geometry(32768, 128, 256, 12),
+                     hip.Geometry(32768, 256, 128, 1), hip.Geometry(32768, 256, 128, 65)]:
+        code = lib.lct_decode(fake, fake, fake, fake, fake, 32768, 32768, geometry, 8, None, None)
+        assert code == LCT_E_GEOMETRY
+        code = lib.lct_encode(fake, fake, fake, fake, fake, fake, 32768, 32768, geometry, 0, 1,
+                              None)
+        assert code == LCT_E_GEOMETRY
+
+
+def test_call_raises_on_error_code(lib):
+    with pytest.raises(hip.LCTKernelError, match="lct_decode failed with code -1"):
+        hip.call("lct_decode", *_nulls("lct_decode"))

@@ -1,0 +1,179 @@
+"""Host-side logic (CPU): the reference's selectors, geometry, storage record,
+RAW path, module aliases and the loud failure without the GPU library."""
+from __future__ import annotations
+
+import importlib
+
+import pytest
+import torch
+
+from losslessly_compressed_tensors_amd.codec.geometry import geometry
+from losslessly_compressed_tensors_amd.comp_format import (
+    Distribution,
+    DistType,
+    NoiseLevel,
+    StorageLayout,
+)
+from losslessly_compressed_tensors_amd.comp_tensor import CompressedTensor
+from losslessly_compressed_tensors_amd.kernels import hip
+from losslessly_compressed_tensors_amd.operations import (
+    a_compA_add_B,
+    a_compA_add_compB,
+    compress,
+    decompress,
+)
+
+
+# ---- Distribution (comp_format.py:26-74) -------------------------------------
+
+
+@pytest.mark.parametrize("param, expected", [
+    (1.0, 1.0), (0.98, 1.0), (0.1, 0.25), (0.375, 0.5), (0.625, 0.5), (0.875, 1.0),
+    (2.2, 2.25), (1e-9, 0.25),
+])
+def test_param_snaps_to_quarters_with_bankers_rounding(param, expected):
+    assert Distribution(DistType.LAPLACE, param).param == expected
+
+
+@pytest.mark.parametrize("mean, expected", [(0.05, 0.0), (-0.125, 0.0), (0.125, 0.0),
+                                            (0.375, 0.5), (-0.3, -0.25), (50.1, 50.0)])
+def test_mean_snaps_to_quarters(mean, expected):
+    assert Distribution(DistType.GAUSSIAN, 1.0, mean).mean == expected
+
+
+@pytest.mark.parametrize("zero_prob, expected", [(None, 0.0), (0.123, 0.12), (0.125, 0.12),
+                                                 (1.0, 1.0), (0.004, 0.0)])
+def test_zero_prob_rounds_to_hundredths(zero_prob, expected):
+    assert Distribution(zero_prob=zero_prob).zero_prob == expected
+
+
+@pytest.mark.parametrize("kwargs, error", [
+    ({"family": "gaussian"}, TypeError),
+    ({"noise_level": 1}, TypeError),
+    ({"param": 0.0}, ValueError),
+    ({"param": -1.0}, ValueError),
+    ({"param": float("inf")}, ValueError),
+    ({"mean": float("nan")}, ValueError),
+    ({"zero_prob": 1.5}, ValueError),
+    ({"zero_prob": -0.1}, ValueError),
+])
+def test_distribution_validation(kwargs, error):
+    with pytest.raises(error):
+        Distribution(**kwargs)
+
+
+def test_distribution_str():
+    assert str(Distribution(DistType.GAUSSIAN)) == "gaussian/std=1.0/mean=0.0/clean"
+    assert (str(Distribution(DistType.LAPLACE, 2.0, 0.5, NoiseLevel.SPARSE))
+            == "laplace/scale=2.0/mean=0.5/sparse")
+
+
+# ---- geometry (codec/geometry.py:13-39) ----------------------------------------
+
+
+@pytest.mark.parametrize("family, noise, expected", [
+    (DistType.GAUSSIAN, NoiseLevel.CLEAN, (32768, 256, 128, 12)),
+    (DistType.LAPLACE, NoiseLevel.CLEAN, (65536, 256, 256, 25)),
+    (DistType.EMPIRICAL, NoiseLevel.CLEAN, (65536, 256, 256, 25)),
+    (DistType.GAMMA, NoiseLevel.CLEAN, (65536, 256, 256, 25)),
+    (DistType.GAUSSIAN, NoiseLevel.SPARSE, (65536, 256, 256, 20)),
+    (DistType.LAPLACE, NoiseLevel.MEDIUM, (32768, 256, 128, 19)),
+    (DistType.EMPIRICAL, NoiseLevel.HIGH, (32768, 256, 128, 22)),
+])
+def test_geometry_table(family, noise, expected):
+    assert geometry(Distribution(family, noise_level=noise)) == expected
+
+
+def test_codec_geometry_fallbacks():
+    legacy = CompressedTensor(torch.zeros(4, dtype=torch.int32), 65536,
+                              distribution=Distribution(DistType.GAUSSIAN),
+                              layout=StorageLayout.COMPRESSED,
+                              fallback_blocks=torch.zeros(3, dtype=torch.int32))
+    assert legacy.codec_geometry == (65536, 256, 256, 24)   # comp_tensor.py:50-54
+    with pytest.raises(ValueError):
+        CompressedTensor(torch.zeros(4, dtype=torch.int32), 65536,
+                         layout=StorageLayout.COMPRESSED).codec_geometry
+
+
+# ---- memory_size (comp_tensor.py:57-72) ----------------------------------------
+
+
+def _record(buffered: bool):
+    nb, ns, W, N = 2, 512, 12, 65536
+    counts = torch.tensor([3, 40, 0, 0], dtype=torch.int32)
+    common = dict(
+        data=torch.zeros(ns * W + 4, dtype=torch.int32), size=N,
+        sign_mantissa=torch.zeros(N, dtype=torch.uint8),
+        fallback_count=counts[0:1], fallback_used=counts[1:2],
+        fallback_blocks=torch.zeros(3 * nb, dtype=torch.int32),
+        center=torch.zeros(1, dtype=torch.int32),
+        decode_table=torch.zeros(1024, dtype=torch.int32),
+        distribution=Distribution(DistType.GAUSSIAN), shape=(N,),
+        layout=StorageLayout.COMPRESSED, stream_geometry=(32768, 256, 128, W))
+    if buffered:
+        arena = torch.zeros(1 << 16, dtype=torch.uint8)
+        return CompressedTensor(fallback_buffer=arena,
+                                fallback_descriptor=torch.tensor([0, 48, 0, 1],
+                                                                 dtype=torch.int32),
+                                **common)
+    return CompressedTensor(fallback_buffer=torch.zeros(40, dtype=torch.uint8),
+                            fallback_lanes=torch.zeros(3, dtype=torch.uint8),
+                            fallback_starts=torch.zeros(3, dtype=torch.uint8), **common)
+
+
+def test_memory_size_private():
+    fixed = (512 * 12 + 4) * 4 + 65536 + 16 + 24 + 4 + 4096
+    assert _record(False).memory_size() == fixed + 3 + 3 + 40
+
+
+def test_memory_size_buffered_counts_reservation_not_arena():
+    fixed = (512 * 12 + 4) * 4 + 65536 + 16 + 24 + 4 + 4096
+    # the arena (shared by lanes/starts/tails) is excluded; the 16-byte
+    # descriptor and the 48 reserved bytes are counted
+    assert _record(True).memory_size() == fixed + 16 + 48
+
+
+# ---- RAW path and error behaviour ------------------------------------------------
+
+
+def test_raw_layout_for_tiny_tensors_round_trips_on_host():
+    x = torch.randn(3, 5).to(torch.bfloat16)
+    ct = compress(x, Distribution(DistType.GAUSSIAN), allow_raw=True)
+    assert ct.layout == StorageLayout.RAW
+    assert torch.equal(decompress(ct), x)
+
+
+def test_non_16_bit_input_is_rejected():
+    with pytest.raises(TypeError):
+        compress(torch.randn(70000), Distribution(DistType.GAUSSIAN))
+
+
+def test_codec_requires_gpu_tensors():
+    with pytest.raises(ValueError, match="GPU"):
+        compress(torch.randn(70000).to(torch.bfloat16), Distribution(DistType.GAUSSIAN))
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="not found"):
+        hip.load_library(tmp_path / "liblct_hip.so")
+
+
+def test_scalar_arguments_must_be_tensors():
+    ct = _record(False)
+    with pytest.raises(TypeError):
+        a_compA_add_B(ct, 0.5, torch.zeros(1))
+    with pytest.raises(TypeError):
+        a_compA_add_compB(ct, 0.5, ct)
+
+
+# ---- drop-in module paths ------------------------------------------------------------
+
+
+@pytest.mark.parametrize("name", ["operations", "comp_format", "comp_tensor", "tensor_buffer",
+                                  "LCTensor", "codec.encode", "codec.decode",
+                                  "compression.huffman_tables"])
+def test_reference_module_paths_resolve_to_this_package(name):
+    ours = importlib.import_module(f"losslessly_compressed_tensors_amd.{name}")
+    assert importlib.import_module(f"LCT.{name}") is ours
+    from LCT.operations import compress as lct_compress
+    assert lct_compress is compress
