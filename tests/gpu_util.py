@@ -26,6 +26,17 @@ def oracle_compress(x: torch.Tensor, dist, buffer=None, **kw):
                            buffer=buffer, **kw)
 
 
+def oracle_from_components(side: np.ndarray, exponents: np.ndarray, dist, buffer=None):
+    """Oracle compress of precomputed components: side bytes (storage order,
+    uint8[size]) and exponent bytes (logical order, uint8[n]), as the fused
+    pointwise kernels hand them to the encoder."""
+    book = distribution_codebook(dist)
+    geometry = oracle.geometry_of(dist.family.value, dist.noise_level.name)
+    return oracle.compress(np.ascontiguousarray(exponents, dtype=np.uint8), geometry,
+                           book.encode, book.decode, book.rare_length, precomputed=True,
+                           side=side, buffer=buffer)
+
+
 def assert_matches_oracle(ct, o: "oracle.Compressed"):
     """Every written field of a GPU CompressedTensor equals the oracle's."""
     B, L, S, W = ct.codec_geometry
