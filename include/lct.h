@@ -123,7 +123,10 @@ int32_t lct_encode(const void *source, uint8_t *side, int32_t *encoded,
  * 2*total_count) bytes from the TensorBuffer whose metadata starts at
  * buffer_meta (int32 free_starts[R] | free_sizes[R] | count | lock |
  * generation) and writes descriptor[4] = {offset, size, status, gen}.
- * n_blocks <= 8192 (LCT/kernels/autotune.py:54). */
+ * Any n_blocks up to 65535 (fewer than 2^31 storage elements: the format's
+ * offsets are int32); blocks are scanned in chunks of 8192 with running
+ * totals, so entries keep block order at every size (the reference's path
+ * above 8192 blocks, LCT/kernels/autotune.py:54, orders them by atomics). */
 int32_t lct_prefix_allocate(int32_t *summaries, int32_t *counts,
                             int32_t *descriptor, int32_t *buffer_meta,
                             int32_t *blocks, int64_t n_blocks, int32_t buffered,

@@ -22,7 +22,7 @@ from ..comp_format import Distribution, StorageLayout
 from ..comp_tensor import CompressedTensor
 from ..compression.huffman_tables import get_distribution_tables
 from ..kernels import dispatch
-from ..kernels.dispatch import SUMMARY_BLOCK_LIMIT, FallbackStorage
+from ..kernels.dispatch import MAX_CODEC_BLOCKS, FallbackStorage
 from ..tensor_buffer import TensorBuffer
 from .geometry import geometry
 
@@ -59,10 +59,10 @@ def encode_components(
     block_symbols, lanes, steps, fixed_words = stream_geometry
     blocks = _cdiv(size, block_symbols)
     streams = blocks * lanes
-    if blocks > SUMMARY_BLOCK_LIMIT:
-        raise NotImplementedError(
-            f"tensors above {SUMMARY_BLOCK_LIMIT} codec blocks "
-            f"({SUMMARY_BLOCK_LIMIT * block_symbols} elements for this layout) are not supported")
+    if blocks > MAX_CODEC_BLOCKS:
+        raise ValueError(
+            f"tensor too large: {blocks} codec blocks; the storage format's int32 offsets "
+            f"allow {MAX_CODEC_BLOCKS} ({MAX_CODEC_BLOCKS * block_symbols} elements here)")
     encode_table, decode_table, _ = get_distribution_tables(distribution, device)
     shifted_encode = torch.empty(256, dtype=torch.int32, device=device)
     shifted_decode = torch.empty_like(decode_table)

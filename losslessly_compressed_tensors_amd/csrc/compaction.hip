@@ -8,93 +8,109 @@
 // at entries [first, first+count), their exponent tails int8(e-127) for steps
 // start..S-1 concatenated from byte_base, and blocks[3*nb] = {count, first,
 // byte_base} so every reader walks the list one block at a time.
+#include <algorithm>
+
 #include "allocator.h"
 
 namespace lct {
 namespace {
 
-constexpr int kPrefixMaxBlocks = 8192;   // 3 x 8192 int32 of LDS
+constexpr int kPrefixChunk = 8192;      // blocks per LDS pass: 3 x 8192 int32 of LDS
 constexpr int kCompactGrid = 2048;     // workgroups walking the overflow-block list
 
 // summaries layout (int32[5*nb + 1]): per-block overflow counts | tail bytes |
 // exclusive count scan | exclusive byte scan | list of blocks with overflow |
 // list length.  The encoder writes the first two; this kernel the rest.
+// Blocks are scanned in chunks of kPrefixChunk with the running totals carried
+// from chunk to chunk, so any block count gives the same deterministic layout
+// (entries in block order, lanes ascending within a block).
 __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     int32_t *__restrict__ summaries, int32_t *__restrict__ counts,
     int32_t *__restrict__ descriptor, int32_t *__restrict__ buffer_meta,
     int32_t *__restrict__ blocks, int32_t n_blocks, int32_t buffered,
     int32_t max_free_regions) {
-    // LDS: per-block counts | tail bytes (then byte scan) | count scan.
+    // LDS per chunk: counts | tail bytes (then byte scan) | count scan.
     extern __shared__ int32_t lds[];
+    const int chunk_cap = min(n_blocks, kPrefixChunk);
     int32_t *c_lds = lds;
-    int32_t *v_lds = lds + n_blocks;
-    int32_t *cp_lds = lds + 2 * n_blocks;
+    int32_t *v_lds = lds + chunk_cap;
+    int32_t *cp_lds = lds + 2 * chunk_cap;
     __shared__ int32_t scratch[kWavesPerBlock];
     __shared__ int32_t flag;
     const int t = threadIdx.x;
-    // Coalesced loads into LDS, all issued before the first LDS write.
-    constexpr int kRows = kPrefixMaxBlocks / kLanes;
-    int32_t c_reg[kRows], v_reg[kRows];
+    int32_t *list = summaries + 4 * static_cast<int64_t>(n_blocks);
+    int32_t carry_count = 0, carry_bytes = 0, carry_listed = 0;
+    for (int base = 0; base < n_blocks; base += kPrefixChunk) {
+        const int m = min(kPrefixChunk, n_blocks - base);
+        // Coalesced loads into LDS, all issued before the first LDS write.
+        constexpr int kRows = kPrefixChunk / kLanes;
+        int32_t c_reg[kRows], v_reg[kRows];
 #pragma unroll
-    for (int j = 0; j < kRows; ++j) {
-        const int b = j * kLanes + t;
-        c_reg[j] = b < n_blocks ? summaries[b] : 0;
-        v_reg[j] = b < n_blocks ? summaries[n_blocks + b] : 0;
-    }
-#pragma unroll
-    for (int j = 0; j < kRows; ++j) {
-        const int b = j * kLanes + t;
-        if (b < n_blocks) {
-            c_lds[b] = c_reg[j];
-            v_lds[b] = v_reg[j];
+        for (int j = 0; j < kRows; ++j) {
+            const int b = j * kLanes + t;
+            c_reg[j] = b < m ? summaries[base + b] : 0;
+            v_reg[j] = b < m ? summaries[n_blocks + base + b] : 0;
         }
-    }
-    __syncthreads();
-    // Thread t scans the contiguous run [t*per, t*per + per).
-    const int per = (n_blocks + kLanes - 1) / kLanes;
-    const int begin = min(t * per, n_blocks);
-    const int end = min(begin + per, n_blocks);
-    int32_t run_count = 0, run_bytes = 0, run_listed = 0;
-    for (int b = begin; b < end; ++b) {
-        run_count += c_lds[b];
-        run_bytes += v_lds[b];
-        run_listed += c_lds[b] > 0 ? 1 : 0;
-    }
-    int32_t total_count, total_bytes, total_listed;
-    int32_t count_before = block_exclusive_scan(run_count, scratch, &total_count);
-    int32_t byte_before = block_exclusive_scan(run_bytes, scratch, &total_bytes);
-    int32_t list_before = block_exclusive_scan(run_listed, scratch, &total_listed);
-    int32_t *list = summaries + 4 * n_blocks;
-    for (int b = begin; b < end; ++b) {
-        const int32_t count = c_lds[b];
-        const int32_t bytes = v_lds[b];
-        cp_lds[b] = count_before;
-        v_lds[b] = byte_before;
-        if (count > 0) list[list_before++] = b;
-        count_before += count;
-        byte_before += bytes;
-    }
-    __syncthreads();
-    // Coalesced stores of the scans and the block metadata.
-    for (int b = t; b < n_blocks; b += kLanes) {
-        const int32_t count = c_lds[b], first = cp_lds[b], byte_base = v_lds[b];
-        summaries[2 * n_blocks + b] = first;
-        summaries[3 * n_blocks + b] = byte_base;
-        blocks[b] = count;
-        blocks[n_blocks + b] = first;
-        blocks[2 * n_blocks + b] = byte_base;
+#pragma unroll
+        for (int j = 0; j < kRows; ++j) {
+            const int b = j * kLanes + t;
+            if (b < m) {
+                c_lds[b] = c_reg[j];
+                v_lds[b] = v_reg[j];
+            }
+        }
+        __syncthreads();
+        // Thread t scans the contiguous run [t*per, t*per + per) of the chunk.
+        const int per = (m + kLanes - 1) / kLanes;
+        const int begin = min(t * per, m);
+        const int end = min(begin + per, m);
+        int32_t run_count = 0, run_bytes = 0, run_listed = 0;
+        for (int b = begin; b < end; ++b) {
+            run_count += c_lds[b];
+            run_bytes += v_lds[b];
+            run_listed += c_lds[b] > 0 ? 1 : 0;
+        }
+        int32_t chunk_count, chunk_bytes, chunk_listed;
+        int32_t count_before = carry_count + block_exclusive_scan(run_count, scratch, &chunk_count);
+        int32_t byte_before = carry_bytes + block_exclusive_scan(run_bytes, scratch, &chunk_bytes);
+        int32_t list_before =
+            carry_listed + block_exclusive_scan(run_listed, scratch, &chunk_listed);
+        for (int b = begin; b < end; ++b) {
+            const int32_t count = c_lds[b];
+            const int32_t bytes = v_lds[b];
+            cp_lds[b] = count_before;
+            v_lds[b] = byte_before;
+            if (count > 0) list[list_before++] = base + b;
+            count_before += count;
+            byte_before += bytes;
+        }
+        __syncthreads();
+        // Coalesced stores of the scans and the block metadata.
+        for (int b = t; b < m; b += kLanes) {
+            const int32_t count = c_lds[b], first = cp_lds[b], byte_base = v_lds[b];
+            const int64_t k = static_cast<int64_t>(base) + b;
+            summaries[2 * static_cast<int64_t>(n_blocks) + k] = first;
+            summaries[3 * static_cast<int64_t>(n_blocks) + k] = byte_base;
+            blocks[k] = count;
+            blocks[n_blocks + k] = first;
+            blocks[2 * static_cast<int64_t>(n_blocks) + k] = byte_base;
+        }
+        carry_count += chunk_count;
+        carry_bytes += chunk_bytes;
+        carry_listed += chunk_listed;
+        __syncthreads();   // the next chunk overwrites the LDS arrays
     }
     if (t == 0) {
-        counts[0] = total_count;
-        counts[1] = total_bytes;
+        counts[0] = carry_count;
+        counts[1] = carry_bytes;
         counts[2] = 0;
         counts[3] = 0;
-        summaries[5 * n_blocks] = total_listed;
+        summaries[5 * static_cast<int64_t>(n_blocks)] = carry_listed;
     }
     if (buffered) {
         // Two metadata bytes per overflowing stream: lane, then start step.
         const AllocatorMeta meta(buffer_meta, max_free_regions);
-        allocator_allocate(meta, total_bytes + 2 * total_count, descriptor, scratch, &flag);
+        allocator_allocate(meta, carry_bytes + 2 * carry_count, descriptor, scratch, &flag);
     }
 }
 
@@ -190,11 +206,13 @@ extern "C" int32_t lct_prefix_allocate(int32_t *summaries, int32_t *counts,
                                        int32_t max_free_regions, hipStream_t stream) {
     if (!summaries || !counts || !blocks) return LCT_E_NULL;
     if (buffered && (!descriptor || !buffer_meta)) return LCT_E_NULL;
-    if (n_blocks <= 0 || n_blocks > kPrefixMaxBlocks) return LCT_E_SIZE;
+    // 5*nb + 1 summary entries and the int32 tail offsets bound the block count.
+    if (n_blocks <= 0 || n_blocks > kMaxBlocks) return LCT_E_SIZE;
     if (buffered && (max_free_regions <= 0 || max_free_regions > 4096
                      || (max_free_regions & (max_free_regions - 1)) != 0))
         return LCT_E_ARG;
-    const size_t lds = 3 * static_cast<size_t>(n_blocks) * sizeof(int32_t);
+    const size_t lds = 3 * static_cast<size_t>(std::min<int64_t>(n_blocks, kPrefixChunk))
+        * sizeof(int32_t);
     if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(prefix_allocate_kernel),
                                            lds))
         return static_cast<int32_t>(e);

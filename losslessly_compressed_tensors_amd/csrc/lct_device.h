@@ -117,6 +117,11 @@ __device__ __forceinline__ int32_t block_sum(int32_t v, int32_t *scratch) {
     return total;
 }
 
+// Largest codec block count of one tensor: overflow offsets and tail byte
+// counts are int32 in the storage format, so a tensor stays below 2^31 storage
+// elements (65535 blocks of 32768).
+constexpr int64_t kMaxBlocks = 65535;
+
 // Geometry check shared by every entry point.
 inline bool geometry_ok(const lct_geometry &g) {
     // Every geometry of LCT/codec/geometry.py:13-39 (and the legacy layout of

@@ -15,9 +15,11 @@ import torch
 
 from . import hip
 
-# Largest block count the single-workgroup prefix scan handles
-# (LCT/kernels/autotune.py:54).
-SUMMARY_BLOCK_LIMIT = 8192
+# Largest codec block count of one tensor.  The reference switches to an
+# atomic compaction path above 8192 blocks (LCT/kernels/autotune.py:54,
+# LCT/codec/encode.py:80); here one deterministic path serves every size up to
+# the storage format's int32 offsets: fewer than 2^31 storage elements.
+MAX_CODEC_BLOCKS = 65535
 
 
 def _ptr(tensor: torch.Tensor | None):

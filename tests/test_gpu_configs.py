@@ -93,3 +93,33 @@ def test_c4_momentum_50_steps():
         state = oracle_from_components(side, exponents, dist)
         assert_matches_oracle(momentum.x, state)
     assert np.array_equal(bits_of(momentum.decompress()), oracle.decompress(state))
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("buffered", [False, True], ids=["private", "buffered"])
+def test_more_blocks_than_one_scan_chunk(buffered):
+    """9000 Gaussian-CLEAN blocks (295 M elements): the block scan runs in
+    chunks of 8192 with carried totals; random bits in every 97th block put
+    overflow entries on both sides of the chunk boundary."""
+    require_gpu()
+    print(f"case large buffered={buffered}", flush=True)
+    B = 32768
+    nb = 9000
+    x = _randn((nb * B,), 11).to(torch.bfloat16)
+    rng = np.random.default_rng(12)
+    bits = x.view(torch.int16).numpy()
+    for block in range(0, nb, 97):
+        lo = block * B + int(rng.integers(0, B - 4096))
+        bits[lo:lo + 4096] = rng.integers(-32768, 32768, 4096, dtype=np.int16)
+    dist = Distribution(DistType.GAUSSIAN)
+    buffer = TensorBuffer(256 << 20, device="cuda") if buffered else None
+    host = oracle.Buffer(256 << 20, 256) if buffered else None
+    ct = compress(x.cuda(), dist, buffer=buffer)
+    o = oracle_compress(x, dist, buffer=host)
+    listed = np.nonzero(o.blocks[:nb])[0]
+    assert listed.min() < 8192 < listed.max()
+    assert_matches_oracle(ct, o)
+    assert np.array_equal(bits_of(decompress(ct)), bits_of(x))
+    if buffered:
+        ct.free()
+        verify_buffer(buffer)
