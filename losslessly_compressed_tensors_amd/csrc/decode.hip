@@ -35,19 +35,21 @@ __device__ __forceinline__ uint32_t logical_col2(int64_t row_base, int step) {
 // block's tails are read from LDS, or from HBM.
 enum Overlay { kNoOverlay, kLdsOverlay, kHbmOverlay };
 
+// Steps decoded before each store phase: half a side chunk keeps the entries
+// in 8 registers.
+constexpr int kHalfSteps = kChunkSteps / 2;
+
 template <bool kFull, Overlay kOverlay>
 __device__ __forceinline__ void decode_fields(StreamCursor &cursor, const LaneOverlay &lane,
                                               const uint8_t *tail_lds, int first_step,
                                               int64_t row_base, uint32_t valid_in_block,
-                                              uint32_t (&f)[kChunkSteps]) {
-    // Every step of a no-overlay chunk of a full block precedes its lane's
-    // overflow start, so the cursor is inside the encoded bits.
-    constexpr bool kClamp = !kFull || kOverlay != kNoOverlay;
+                                              uint32_t (&f)[kHalfSteps]) {
+    constexpr bool kRecount = !kFull || kOverlay != kNoOverlay;
 #pragma unroll
-    for (int j = 0; j < kChunkSteps; j += 2) {
+    for (int j = 0; j < kHalfSteps; j += 2) {
         const int step = first_step + j;
         uint32_t f0, f1;
-        uint32_t sum = cursor.next_fields<kClamp>(f0, f1);
+        uint32_t sum = cursor.next_fields(f0, f1);
         if (kOverlay != kNoOverlay)
             overlay_pair<kOverlay == kLdsOverlay>(lane, tail_lds, step, f0, f1);
         if (!kFull) {
@@ -57,36 +59,64 @@ __device__ __forceinline__ void decode_fields(StreamCursor &cursor, const LaneOv
             if (off0 >= valid_in_block) f0 &= ~31u;
             if (off0 + kLanes >= valid_in_block) f1 &= ~31u;
         }
-        if (kClamp) sum = (f0 + f1) & 127u;
+        if (kRecount) sum = (f0 + f1) & 127u;
         f[j] = f0;
         f[j + 1] = f1;
-        cursor.pos += sum;
+        cursor.advance(sum);
     }
 }
 
-// Store phase: each lane writes its two values per step pair with 2-byte
-// non-temporal stores (a wave covers 128 contiguous bytes of a row); the last
-// block masks positions past the tensor's end.  The chunk's first step and the
-// block's first row are multiples of 16, so the column of row first_step + j
-// is the chunk's column XOR 2j.
+// Store phase.  Lanes j and j^1 hold adjacent columns (c, c+1) of the same
+// two rows: the swizzle mask is even, so it never changes bit 0 of a column.
+// In a full block the pair swaps one value over DPP so that the even lane
+// stores row `step` and the odd lane row `step + 1`, each as one 4-byte
+// non-temporal store of both columns: a wave writes 2 x 128 contiguous bytes
+// per instruction, which gfx950 streams to HBM markedly faster than 2-byte
+// stores.  The last block masks positions past the tensor's end with 2-byte
+// stores.  `first_step` and the block's first row are multiples of 8, so the
+// column of row first_step + j (j < 8) is the first row's column XOR 2j.
+// `first_step` is the first step of these entries; `slice_step` its index in
+// the side slice (0 or kHalfSteps).
 template <bool kFull>
-__device__ __forceinline__ void store_fields(const uint32_t (&f)[kChunkSteps], const uint8_t *slice,
-                                             __amdgpu_buffer_rsrc_t out, int first_step,
-                                             int64_t row_base, uint32_t valid_in_block) {
+__device__ __forceinline__ void store_fields(const uint32_t (&f)[kHalfSteps], const uint8_t *slice,
+                                             int slice_step, __amdgpu_buffer_rsrc_t out,
+                                             int first_step, int64_t row_base,
+                                             uint32_t valid_in_block) {
     const uint32_t chunk_col2 = logical_col2(row_base, first_step);
+    // Byte form of the swizzle mask of the chunk's first row pair.
+    const uint32_t chunk_mask2 = static_cast<uint32_t>((row_base + first_step) & 254) * 2u;
+    const bool odd = (threadIdx.x & 1u) != 0;
+    // Byte selectors of v_perm_b32(recv, keep, sel): even lanes keep column
+    // c in the low half, odd lanes column c+1 in the high half.
+    const uint32_t select = odd ? 0x01000504u : 0x05040100u;
+    // Even lane: row step, column c; odd lane: row step+1, column c (= its
+    // own column - 1).  The swizzle only touches bits 2..8 of this offset.
+    const uint32_t pair_offset = ((threadIdx.x * 2u) & ~3u) | (odd ? kLanes * 2u : 0u);
 #pragma unroll
-    for (int j = 0; j < kChunkSteps; j += 2) {
+    for (int j = 0; j < kHalfSteps; j += 2) {
         const int step = first_step + j;
-        const uint32_t col2 = chunk_col2 ^ static_cast<uint32_t>(2 * j);
-        const uint16_t out0 = static_cast<uint16_t>(join_entry(f[j], side_byte(slice, j)));
-        const uint16_t out1 = static_cast<uint16_t>(join_entry(f[j + 1], side_byte(slice, j + 1)));
+        const uint32_t out0 = join_entry(f[j], side_byte(slice, slice_step + j));
+        const uint32_t out1 = join_entry(f[j + 1], side_byte(slice, slice_step + j + 1));
         const int row_bytes = step * kLanes * 2;
-        const uint32_t off0 = static_cast<uint32_t>(step) * kLanes + (col2 >> 1);
-        if (kFull || off0 < valid_in_block)
-            __builtin_amdgcn_raw_buffer_store_b16(out0, out, col2, row_bytes, kStreaming);
-        if (kFull || off0 + kLanes < valid_in_block)
-            __builtin_amdgcn_raw_buffer_store_b16(out1, out, col2, row_bytes + kLanes * 2,
-                                                  kStreaming);
+        if (kFull) {
+            const uint32_t send = odd ? out0 : out1;
+            const uint32_t keep = odd ? out1 : out0;
+            // quad_perm [1, 0, 3, 2]: exchange with the neighbouring lane.
+            const uint32_t recv = static_cast<uint32_t>(
+                __builtin_amdgcn_mov_dpp(static_cast<int>(send), 0xB1, 0xF, 0xF, false));
+            const uint32_t word = __builtin_amdgcn_perm(recv, keep, select);
+            const uint32_t offset = pair_offset ^ chunk_mask2 ^ static_cast<uint32_t>(2 * j);
+            __builtin_amdgcn_raw_buffer_store_b32(word, out, offset, row_bytes, kStreaming);
+        } else {
+            const uint32_t col2 = chunk_col2 ^ static_cast<uint32_t>(2 * j);
+            const uint32_t off0 = static_cast<uint32_t>(step) * kLanes + (col2 >> 1);
+            if (off0 < valid_in_block)
+                __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(out0), out, col2,
+                                                      row_bytes, kStreaming);
+            if (off0 + kLanes < valid_in_block)
+                __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(out1), out, col2,
+                                                      row_bytes + kLanes * 2, kStreaming);
+        }
     }
 }
 
@@ -101,11 +131,14 @@ __device__ __forceinline__ void decode_chunks(StreamCursor &cursor, const LaneOv
     const uint32_t voffset = side_fetch_offset();
 #pragma unroll 1
     for (int c = c_begin; c < c_end; c += kChunkSteps) {
-        uint32_t f[kChunkSteps];
+        uint32_t f[kHalfSteps];
         decode_fields<kFull, kOverlay>(cursor, lane, tail_lds, c, row_base, valid_in_block, f);
         store_side_chunk(slice, side_next);
         if (c + kChunkSteps < S) side_next = fetch_side_chunk(side, voffset, c + kChunkSteps);
-        store_fields<kFull>(f, slice, out, c, row_base, valid_in_block);
+        store_fields<kFull>(f, slice, 0, out, c, row_base, valid_in_block);
+        decode_fields<kFull, kOverlay>(cursor, lane, tail_lds, c + kHalfSteps, row_base,
+                                       valid_in_block, f);
+        store_fields<kFull>(f, slice, kHalfSteps, out, c + kHalfSteps, row_base, valid_in_block);
     }
 }
 
@@ -163,7 +196,8 @@ __global__ __launch_bounds__(kLanes) void decode_kernel(
     wait_memory();
     __syncthreads();   // payload and tails visible; overflow maps no longer read
 
-    const StreamCursor cursor{stage + threadIdx.x, &tb, 0u, static_cast<uint32_t>(W - 1), rare};
+    StreamCursor cursor;
+    cursor.init(stage + threadIdx.x, &tb, static_cast<uint32_t>(W), rare);
     uint8_t *slice = side_slices[threadIdx.x / kWave];
     if (valid == block_elems) {
         if (S == 128)

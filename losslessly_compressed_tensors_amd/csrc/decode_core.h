@@ -31,8 +31,9 @@ namespace lct {
 
 // Buffer resource word 3 for gfx9-family raw buffers.
 constexpr int32_t kBufferConfig = 0x00020000;
-// Cache policy of streamed data (read or written once): non-temporal.  On
-// gfx950 this lifts the decoder's mixed read/write traffic by 6-10%.
+// Cache policy of streamed output (written once): non-temporal.  Streamed
+// inputs keep the default policy, which measures faster for the decoder's
+// mix of 16-byte loads and 4-byte non-temporal stores on gfx950.
 constexpr int kStreaming = 2;
 constexpr int kChunkSteps = 16;   // steps per prefetched side-byte chunk
 
@@ -156,6 +157,13 @@ __device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, boo
 
 // One lane's stream cursor.
 //
+// The 64-bit window lives in registers: lo/hi are words w and w+1 of the
+// lane's stream, nx is word w+2, and pos (0..31) is the bit offset in lo.  A
+// pair consumes at most 32 bits, so it crosses at most one word boundary;
+// on a crossing the registers shift down by one word and take the word that
+// was read from LDS at the start of the same pair.  The only LDS accesses on
+// the dependency chain are therefore the two table lookups.
+//
 // A decoded symbol is carried as its table entry: bits 0..4 hold the code
 // length and bits 7..14 the BF16 exponent field, so two entries' lengths add
 // without masking first: (t0 + t1) & 127 = len0 + len1, since each length is at
@@ -164,23 +172,33 @@ __device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, boo
 struct StreamCursor {
     const uint32_t *stage;    // stage + lane; row r at stage[r * 256]
     const DecodeTables *tb;
-    uint32_t pos;
-    uint32_t last_row;        // W - 1
+    uint32_t pos;             // bit offset within lo
+    uint32_t lo, hi, nx;      // stream words w, w+1, w+2
+    uint32_t next_row;        // row of word w+3 (clamped to the pad row)
+    uint32_t pad_row;         // W: the zero row after the payload
+    uint32_t pending;         // word next_row, read at the start of a pair
     int32_t rare;
 
+    __device__ __forceinline__ void init(const uint32_t *stage_lane, const DecodeTables *tables,
+                                         uint32_t words, int32_t rare_length) {
+        stage = stage_lane;
+        tb = tables;
+        pos = 0;
+        pad_row = words;
+        lo = stage[0];
+        hi = stage[kLanes];
+        nx = stage[min(2u, words) * kLanes];
+        next_row = min(3u, words);
+        pending = 0;
+        rare = rare_length;
+    }
+
     // Decode the next two symbols into entries f0/f1 (length | field << 7) and
-    // return len0 + len1.  kClamp keeps a position at or past the end of the
-    // payload inside the stage: needed where a lane may already be past its
-    // last encoded symbol (overflowed lanes, padding of the last block).
-    template <bool kClamp>
-    __device__ __forceinline__ uint32_t next_fields(uint32_t &f0, uint32_t &f1) const {
-        // An opaque shift keeps row * 1024 + lane at two instructions (shift,
-        // lshl_add); the compiler rewrites (pos >> 5) << 10 into three.
-        uint32_t row;
-        asm("v_lshrrev_b32 %0, 5, %1" : "=v"(row) : "v"(pos));
-        if (kClamp) row = min(row, last_row);
-        const uint32_t lo = stage[row * kLanes];
-        const uint32_t hi = stage[(row + 1) * kLanes];
+    // return len0 + len1.  Also starts the read of the word a crossing needs.
+    __device__ __forceinline__ uint32_t next_fields(uint32_t &f0, uint32_t &f1) {
+        pending = stage[next_row * kLanes];
+        // Keep the read ahead of the lookups, so its latency overlaps theirs.
+        __builtin_amdgcn_sched_barrier(0);
         const uint32_t bits = __builtin_amdgcn_alignbit(hi, lo, pos);
         uint32_t t0 = tb->entry[bits & 255u];
         // ubfe reads its offset from t0[4:0], the first code's length.
@@ -202,6 +220,17 @@ struct StreamCursor {
         f0 = t0;
         f1 = t1;
         return sum;
+    }
+
+    // Consume `bits` (at most 32) after next_fields.
+    __device__ __forceinline__ void advance(uint32_t bits) {
+        const uint32_t p = pos + bits;
+        const bool cross = p >= 32u;
+        pos = p & 31u;
+        lo = cross ? hi : lo;
+        hi = cross ? nx : hi;
+        nx = cross ? pending : nx;
+        next_row = cross ? min(next_row + 1u, pad_row) : next_row;
     }
 };
 
@@ -259,7 +288,7 @@ __device__ __forceinline__ SideChunk fetch_side_chunk(__amdgpu_buffer_rsrc_t sid
                                                       uint32_t voffset, int first_step) {
     SideChunk c;
     c.q0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                         side, voffset, first_step * kLanes, kStreaming));
+                                         side, voffset, first_step * kLanes, 0));
     return c;
 }
 

@@ -74,7 +74,7 @@ __device__ __forceinline__ void pointwise_rows(const StreamCursor &cursor_in, co
 #pragma unroll 2
     for (int step = 0; step < S; step += 2) {
         uint32_t f0, f1;
-        cursor.next_fields<true>(f0, f1);
+        cursor.next_fields(f0, f1);
         const uint32_t slot = static_cast<uint32_t>(step) * kLanes + t;
         const uint32_t sm0 = side_block[slot];
         const uint32_t sm1 = side_block[slot + kLanes];
@@ -90,7 +90,7 @@ __device__ __forceinline__ void pointwise_rows(const StreamCursor &cursor_in, co
             len0 = v0 ? len0 : 0u;
             len1 = v1 ? len1 : 0u;
         }
-        cursor.pos += len0 + len1;
+        cursor.advance(len0 + len1);
         const uint32_t b0 = v0 ? other_block[off0] : 0u;
         const uint32_t b1 = v1 ? other_block[off1] : 0u;
         const uint32_t r0 = apply_op(p, join_bf16(f0, sm0), b0);
@@ -124,7 +124,8 @@ __global__ __launch_bounds__(kLanes) void pointwise_kernel(
         if (!alpha_is_one) p.alpha = alpha[0];
         if (!beta_is_one) p.beta = beta[0];
     }
-    const StreamCursor cursor{stage + threadIdx.x, &tb, 0u, static_cast<uint32_t>(W - 1), rare};
+    StreamCursor cursor;
+    cursor.init(stage + threadIdx.x, &tb, static_cast<uint32_t>(W), rare);
     const int64_t row_base = block * S;
     const int64_t logical_base = row_base * kLanes;
     const uint8_t *side_block = side + logical_base;
@@ -163,8 +164,8 @@ __device__ __forceinline__ void dual_rows(const StreamCursor &a_in, const LaneOv
 #pragma unroll 2
     for (int step = 0; step < S; step += 2) {
         uint32_t af0, af1, bf0, bf1;
-        a.next_fields<true>(af0, af1);
-        b.next_fields<true>(bf0, bf1);
+        a.next_fields(af0, af1);
+        b.next_fields(bf0, bf1);
         const uint32_t slot = static_cast<uint32_t>(step) * kLanes + t;
         const uint32_t asm0 = a_side[slot], asm1 = a_side[slot + kLanes];
         const uint32_t bsm0 = b_side[slot], bsm1 = b_side[slot + kLanes];
@@ -183,8 +184,8 @@ __device__ __forceinline__ void dual_rows(const StreamCursor &a_in, const LaneOv
             blen0 = v0 ? blen0 : 0u;
             blen1 = v1 ? blen1 : 0u;
         }
-        a.pos += alen0 + alen1;
-        b.pos += blen0 + blen1;
+        a.advance(alen0 + alen1);
+        b.advance(blen0 + blen1);
         const uint32_t r0 = float_to_bf16(__builtin_fmaf(bf16_to_float(join_bf16(af0, asm0)), alpha,
                                                          bf16_to_float(join_bf16(bf0, bsm0))));
         const uint32_t r1 = float_to_bf16(__builtin_fmaf(bf16_to_float(join_bf16(af1, asm1)), alpha,
@@ -228,8 +229,9 @@ __global__ __launch_bounds__(kLanes) void dual_kernel(DualOperand a, DualOperand
     __syncthreads();
 
     const float alpha_value = alpha[0];
-    const StreamCursor ca{stage_a + threadIdx.x, &tb_a, 0u, static_cast<uint32_t>(W - 1), rare};
-    const StreamCursor cb{stage_b + threadIdx.x, &tb_b, 0u, static_cast<uint32_t>(W - 1), rare};
+    StreamCursor ca, cb;
+    ca.init(stage_a + threadIdx.x, &tb_a, static_cast<uint32_t>(W), rare);
+    cb.init(stage_b + threadIdx.x, &tb_b, static_cast<uint32_t>(W), rare);
     const int64_t row_base = block * S;
     const int64_t logical_base = row_base * kLanes;
     uint16_t *dense_block = static_cast<uint16_t *>(output) + logical_base;
