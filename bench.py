@@ -136,6 +136,46 @@ def cpu_baseline(x_cpu, dist, min_seconds: float):
     }
 
 
+def time_update(args, torch, device):
+    """Config C4: m <- 0.95*m + g on a compressed 4096x11008 momentum
+    (EMPIRICAL CLEAN, buffer-backed so no step syncs), m0 ~ N(0, 1e-3^2) seed 4,
+    g ~ N(0, 1e-2^2) seeds 100, 101 alternating.  Reports the step time, the
+    BF16 throughput 2n/t and the fraction of HBM peak that the single-pass
+    minimum traffic (payload + side + 2n read, side + payload written) would
+    need at that time."""
+    from losslessly_compressed_tensors_amd.comp_format import DistType, Distribution
+    from losslessly_compressed_tensors_amd.LCTensor import LCTTensor
+    from losslessly_compressed_tensors_amd.tensor_buffer import TensorBuffer
+
+    shape = (4096, 11008)
+    gen = torch.Generator().manual_seed(4)
+    m0 = (torch.randn(*shape, generator=gen) * 1e-3).to(torch.bfloat16).to(device)
+    grads = []
+    for seed in (100, 101):
+        gen = torch.Generator().manual_seed(seed)
+        grads.append((torch.randn(*shape, generator=gen) * 1e-2).to(torch.bfloat16).to(device))
+    dist = Distribution(DistType.EMPIRICAL)
+    buffer = TensorBuffer(64 << 20, device=device)
+    momentum = LCTTensor(m0, buffer, dist)
+    alpha = torch.tensor([0.95], dtype=torch.float32, device=device)
+    steps = max(10, args.steps // 2)
+    ms = _time_events(lambda i: momentum.mul_add_(alpha, grads[i % 2]), steps, args.warmup,
+                      torch)
+    ct = momentum.x
+    B, L, S, W = ct.codec_geometry
+    nb = ct.size // B
+    n = ct.logical_numel
+    minimum = 2 * (nb * L * W * 4 + ct.size) + 2 * n
+    return {
+        "workload": "C4: 4096x11008, EMPIRICAL CLEAN, LCTTensor.mul_add_(0.95, g), buffered",
+        "steps": steps,
+        "ms_per_step": round(ms, 5),
+        "gbps": round(2 * n / (ms * 1e-3) / 1e9, 2),
+        "single_pass_bytes": minimum,
+        "single_pass_hbm_frac": round(minimum / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+    }
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -216,6 +256,9 @@ def main() -> int:
                                   2, torch)
     enc_alg = encode_bytes(cts[0])
 
+    _log("timing fused update (C4)")
+    update = time_update(args, torch, device)
+
     # Reference traffic for counter calibration: a plain 256 MiB device copy
     # (reads and writes exactly 2n bytes each).
     copy_out = torch.empty_like(xs[0])
@@ -262,6 +305,7 @@ def main() -> int:
             "kernel_us": round(kernel_ms * 1e3, 2),
         },
     }
+    result["update"] = update
     if not args.skip_cpu:
         _log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(host_inputs[0], dist, args.cpu_seconds)

@@ -22,50 +22,6 @@
 namespace lct {
 namespace {
 
-// Tail bytes per block that are staged in LDS (larger blocks read HBM).
-constexpr int32_t kTailLds = 1024;
-
-// Byte offset of this lane's logical column within row `step` of the block;
-// rows step and step+1 share the swizzle mask.
-__device__ __forceinline__ uint32_t logical_col2(int64_t row_base, int step) {
-    return (threadIdx.x * 2u) ^ (static_cast<uint32_t>((row_base + step) & 254) * 2u);
-}
-
-// Overlay variants of a chunk: no lane of the wave overflows in it, or the
-// block's tails are read from LDS, or from HBM.
-enum Overlay { kNoOverlay, kLdsOverlay, kHbmOverlay };
-
-// Steps decoded before each store phase: half a side chunk keeps the entries
-// in 8 registers.
-constexpr int kHalfSteps = kChunkSteps / 2;
-
-template <bool kFull, Overlay kOverlay>
-__device__ __forceinline__ void decode_fields(StreamCursor &cursor, const LaneOverlay &lane,
-                                              const uint8_t *tail_lds, int first_step,
-                                              int64_t row_base, uint32_t valid_in_block,
-                                              uint32_t (&f)[kHalfSteps]) {
-    constexpr bool kRecount = !kFull || kOverlay != kNoOverlay;
-#pragma unroll
-    for (int j = 0; j < kHalfSteps; j += 2) {
-        const int step = first_step + j;
-        uint32_t f0, f1;
-        uint32_t sum = cursor.next_fields(f0, f1);
-        if (kOverlay != kNoOverlay)
-            overlay_pair<kOverlay == kLdsOverlay>(lane, tail_lds, step, f0, f1);
-        if (!kFull) {
-            // Padding positions of the last block consume no payload bits.
-            const uint32_t off0 = static_cast<uint32_t>(step) * kLanes
-                + (logical_col2(row_base, step) >> 1);
-            if (off0 >= valid_in_block) f0 &= ~31u;
-            if (off0 + kLanes >= valid_in_block) f1 &= ~31u;
-        }
-        if (kRecount) sum = (f0 + f1) & 127u;
-        f[j] = f0;
-        f[j + 1] = f1;
-        cursor.advance(sum);
-    }
-}
-
 // Store phase.  Lanes j and j^1 hold adjacent columns (c, c+1) of the same
 // two rows: the swizzle mask is even, so it never changes bit 0 of a column.
 // In a full block the pair swaps one value over DPP so that the even lane

@@ -302,4 +302,107 @@ __device__ __forceinline__ uint32_t side_byte(const uint8_t *slice, int step_in_
     return slice[step_in_chunk * kWave + (threadIdx.x & (kWave - 1))];
 }
 
+// ---- chunked stream walking shared by the decoder and the pointwise kernels
+
+// Tail bytes per block that are staged in LDS (larger blocks read HBM).
+constexpr int32_t kTailLds = 1024;
+
+// Byte offset of this lane's logical column within row `step` of the block;
+// rows step and step+1 share the swizzle mask.
+__device__ __forceinline__ uint32_t logical_col2(int64_t row_base, int step) {
+    return (threadIdx.x * 2u) ^ (static_cast<uint32_t>((row_base + step) & 254) * 2u);
+}
+
+// Overlay variants of a chunk: no lane of the wave overflows in it, or the
+// block's tails are read from LDS, or from HBM.
+enum Overlay { kNoOverlay, kLdsOverlay, kHbmOverlay };
+
+// Steps decoded before each store phase: half a side chunk keeps the entries
+// in 8 registers.
+constexpr int kHalfSteps = kChunkSteps / 2;
+
+template <bool kFull, Overlay kOverlay>
+__device__ __forceinline__ void decode_fields(StreamCursor &cursor, const LaneOverlay &lane,
+                                              const uint8_t *tail_lds, int first_step,
+                                              int64_t row_base, uint32_t valid_in_block,
+                                              uint32_t (&f)[kHalfSteps]) {
+    constexpr bool kRecount = !kFull || kOverlay != kNoOverlay;
+#pragma unroll
+    for (int j = 0; j < kHalfSteps; j += 2) {
+        const int step = first_step + j;
+        uint32_t f0, f1;
+        uint32_t sum = cursor.next_fields(f0, f1);
+        if (kOverlay != kNoOverlay)
+            overlay_pair<kOverlay == kLdsOverlay>(lane, tail_lds, step, f0, f1);
+        if (!kFull) {
+            // Padding positions of the last block consume no payload bits.
+            const uint32_t off0 = static_cast<uint32_t>(step) * kLanes
+                + (logical_col2(row_base, step) >> 1);
+            if (off0 >= valid_in_block) f0 &= ~31u;
+            if (off0 + kLanes >= valid_in_block) f1 &= ~31u;
+        }
+        if (kRecount) sum = (f0 + f1) & 127u;
+        f[j] = f0;
+        f[j + 1] = f1;
+        cursor.advance(sum);
+    }
+}
+
+// ---- lane pairs
+//
+// Lanes j and j^1 hold adjacent columns (c, c+1), c even, of the same two rows
+// (step, step+1): the swizzle mask is even, so it never changes bit 0 of a
+// column.  Exchanging one value over DPP (quad_perm [1, 0, 3, 2]) lets the
+// even lane handle both columns of row `step` and the odd lane both columns of
+// row `step + 1` with one 4-byte access (2 bytes for byte data).
+struct LanePair {
+    bool odd;
+    uint32_t pack16;      // v_perm selector: two 16-bit values, own column's in place
+    uint32_t pack8;       // v_perm selector: two bytes, own column's in place
+    uint32_t low16;       // v_perm selector: row `step` value of own column into bits 16..31
+    uint32_t high16;      // v_perm selector: row `step+1` value of own column into bits 16..31
+    uint32_t offset2;     // byte offset of the pair's word (16-bit data), before the swizzle
+    uint32_t offset1;     // byte offset of the pair's 2 bytes (byte data), before the swizzle
+
+    __device__ __forceinline__ LanePair() {
+        const uint32_t t = threadIdx.x;
+        odd = (t & 1u) != 0;
+        pack16 = odd ? 0x01000504u : 0x05040100u;
+        pack8 = odd ? 0x0C0C0004u : 0x0C0C0400u;
+        // v_perm_b32(recv, own, sel): bytes 0..3 select own, 4..7 recv, 12 = 0.
+        low16 = odd ? 0x07060C0Cu : 0x01000C0Cu;
+        high16 = odd ? 0x03020C0Cu : 0x05040C0Cu;
+        offset2 = ((t * 2u) & ~3u) | (odd ? kLanes * 2u : 0u);
+        offset1 = (t & ~1u) | (odd ? static_cast<uint32_t>(kLanes) : 0u);
+    }
+};
+
+__device__ __forceinline__ uint32_t swap_pair(uint32_t value) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_mov_dpp(static_cast<int>(value), 0xB1, 0xF, 0xF, false));
+}
+
+// The word to store for 16-bit results v0 (row step) and v1 (row step+1) of
+// this lane's column.
+__device__ __forceinline__ uint32_t pair_word16(const LanePair &lp, uint32_t v0, uint32_t v1) {
+    const uint32_t recv = swap_pair(lp.odd ? v0 : v1);
+    return __builtin_amdgcn_perm(recv, lp.odd ? v1 : v0, lp.pack16);
+}
+
+// The 2 bytes to store for byte results v0 (row step) and v1 (row step+1).
+__device__ __forceinline__ uint32_t pair_word8(const LanePair &lp, uint32_t v0, uint32_t v1) {
+    const uint32_t recv = swap_pair(lp.odd ? v0 : v1);
+    return __builtin_amdgcn_perm(recv, lp.odd ? v1 : v0, lp.pack8);
+}
+
+// From the pair's loaded words (own: this lane's load, row step + odd) give
+// this lane's column of rows step and step+1 as FP32 bit patterns (BF16 in
+// the high half).
+__device__ __forceinline__ void pair_unpack16(const LanePair &lp, uint32_t own, float &v0,
+                                              float &v1) {
+    const uint32_t recv = swap_pair(own);
+    v0 = __builtin_bit_cast(float, __builtin_amdgcn_perm(recv, own, lp.low16));
+    v1 = __builtin_bit_cast(float, __builtin_amdgcn_perm(recv, own, lp.high16));
+}
+
 }  // namespace lct

@@ -29,9 +29,7 @@ struct OpParams {
     float beta;
 };
 
-__device__ __forceinline__ uint32_t apply_op(const OpParams &p, uint32_t left, uint32_t right) {
-    const float a = bf16_to_float(left);
-    float b = bf16_to_float(right);
+__device__ __forceinline__ uint32_t apply_op_f(const OpParams &p, float a, float b) {
     float r;
     if (p.op == LCT_OP_ADD) {
         r = a + b;
@@ -44,6 +42,10 @@ __device__ __forceinline__ uint32_t apply_op(const OpParams &p, uint32_t left, u
         r = __builtin_fmaf(a, p.alpha, b);
     }
     return float_to_bf16(r);
+}
+
+__device__ __forceinline__ uint32_t apply_op(const OpParams &p, uint32_t left, uint32_t right) {
+    return apply_op_f(p, bf16_to_float(left), bf16_to_float(right));
 }
 
 // Emits one result.  Dense: bf16 at the logical offset.  Compressed: side byte
@@ -62,43 +64,151 @@ __device__ __forceinline__ void store_result(uint32_t bits, bool logical_valid, 
     }
 }
 
-template <bool kFull, int S, int kPolicy>
-__device__ __forceinline__ void pointwise_rows(const StreamCursor &cursor_in, const LaneOverlay &lane,
-                                               const uint8_t *__restrict__ side_block,
-                                               const uint16_t *__restrict__ other_block,
-                                               uint16_t *dense_block, uint8_t *side_out_block,
-                                               uint8_t *exp_out_block, int64_t row_base,
-                                               int64_t valid_in_block, const OpParams &p) {
-    StreamCursor cursor = cursor_in;
-    const uint32_t t = threadIdx.x;
-#pragma unroll 2
-    for (int step = 0; step < S; step += 2) {
-        uint32_t f0, f1;
-        cursor.next_fields(f0, f1);
-        const uint32_t slot = static_cast<uint32_t>(step) * kLanes + t;
-        const uint32_t sm0 = side_block[slot];
-        const uint32_t sm1 = side_block[slot + kLanes];
-        overlay_pair<false>(lane, nullptr, step, f0, f1);
-        uint32_t len0 = f0 & 31u, len1 = f1 & 31u;
-        const uint32_t col = t ^ static_cast<uint32_t>((row_base + step) & 254);
-        const uint32_t off0 = static_cast<uint32_t>(step) * kLanes + col;
-        const uint32_t off1 = off0 + kLanes;
-        bool v0 = true, v1 = true;
-        if (!kFull) {
-            v0 = off0 < valid_in_block;
-            v1 = off1 < valid_in_block;
-            len0 = v0 ? len0 : 0u;
-            len1 = v1 ? len1 : 0u;
+// Per-workgroup view of the pointwise operands and outputs of one block.
+struct PointwiseIo {
+    __amdgpu_buffer_rsrc_t side;       // A's side bytes (storage order)
+    __amdgpu_buffer_rsrc_t other;      // B, BF16 in logical order
+    __amdgpu_buffer_rsrc_t dense;      // dense output (policy 0)
+    __amdgpu_buffer_rsrc_t side_out;   // result side bytes (policy 1, storage order)
+    __amdgpu_buffer_rsrc_t exp_out;    // result exponent bytes (policy 1, logical order)
+};
+
+// One half chunk (8 steps from first_step, entries f) of a full block: B is
+// read as one 4-byte word per lane per step pair (lane pairs), the results
+// go out as one 4-byte word (dense) or 2 exponent bytes (compressed) per lane
+// per pair; compressed side bytes replace A's side bytes in the wave's slice.
+template <int kPolicy>
+__device__ __forceinline__ void pointwise_half_full(const uint32_t (&f)[kHalfSteps],
+                                                    const uint32_t (&bw)[kHalfSteps / 2],
+                                                    uint8_t *slice, int slice_step,
+                                                    const PointwiseIo &io, const LanePair &lp,
+                                                    int first_step, int64_t row_base,
+                                                    const OpParams &p) {
+    const uint32_t mask = static_cast<uint32_t>((row_base + first_step) & 254);
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (int j = 0; j < kHalfSteps; j += 2) {
+        const int step = first_step + j;
+        const int s0 = slice_step + j;
+        float b0, b1;
+        pair_unpack16(lp, bw[j / 2], b0, b1);
+        const uint32_t a0 = join_entry(f[j], side_byte(slice, s0));
+        const uint32_t a1 = join_entry(f[j + 1], side_byte(slice, s0 + 1));
+        const uint32_t r0 = apply_op_f(p, bf16_to_float(a0), b0);
+        const uint32_t r1 = apply_op_f(p, bf16_to_float(a1), b1);
+        if (kPolicy == LCT_DENSE_OUTPUT) {
+            __builtin_amdgcn_raw_buffer_store_b32(pair_word16(lp, r0, r1), io.dense,
+                                                  lp.offset2 ^ (mask * 2u) ^ static_cast<uint32_t>(2 * j),
+                                                  step * kLanes * 2, kStreaming);
+        } else {
+            slice[s0 * kWave + lane] = static_cast<uint8_t>(side_byte_of(r0));
+            slice[(s0 + 1) * kWave + lane] = static_cast<uint8_t>(side_byte_of(r1));
+            const uint32_t e = pair_word8(lp, (r0 >> 7) & 0xFFu, (r1 >> 7) & 0xFFu);
+            __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(e), io.exp_out,
+                                                  lp.offset1 ^ mask ^ static_cast<uint32_t>(j),
+                                                  step * kLanes, kStreaming);
         }
-        cursor.advance(len0 + len1);
-        const uint32_t b0 = v0 ? other_block[off0] : 0u;
-        const uint32_t b1 = v1 ? other_block[off1] : 0u;
-        const uint32_t r0 = apply_op(p, join_bf16(f0, sm0), b0);
-        const uint32_t r1 = apply_op(p, join_bf16(f1, sm1), b1);
-        store_result<kPolicy>(r0, v0, slot, off0, dense_block, side_out_block, exp_out_block);
-        store_result<kPolicy>(r1, v1, slot + kLanes, off1, dense_block, side_out_block,
-                              exp_out_block);
     }
+}
+
+// The same for the last (partial) block: per element, masked.
+template <int kPolicy>
+__device__ __forceinline__ void pointwise_half_partial(const uint32_t (&f)[kHalfSteps],
+                                                       uint8_t *slice, int slice_step,
+                                                       const PointwiseIo &io, int first_step,
+                                                       int64_t row_base, uint32_t valid_in_block,
+                                                       const OpParams &p) {
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (int j = 0; j < kHalfSteps; ++j) {
+        const int step = first_step + j;
+        const uint32_t col = threadIdx.x ^ static_cast<uint32_t>((row_base + step) & 254);
+        const uint32_t off = static_cast<uint32_t>(step) * kLanes + col;
+        const bool valid = off < valid_in_block;
+        const uint32_t b = valid ? __builtin_amdgcn_raw_buffer_load_b16(io.other, off * 2, 0, 0) : 0u;
+        const uint32_t a = join_entry(f[j], side_byte(slice, slice_step + j));
+        const uint32_t r = valid ? apply_op(p, a, b) : 0u;
+        if (kPolicy == LCT_DENSE_OUTPUT) {
+            if (valid)
+                __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(r), io.dense, off * 2,
+                                                      0, kStreaming);
+        } else {
+            slice[(slice_step + j) * kWave + lane] = static_cast<uint8_t>(side_byte_of(r));
+            if (valid)
+                __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>((r >> 7) & 0xFFu),
+                                                     io.exp_out, off, 0, kStreaming);
+        }
+    }
+}
+
+// Chunks [c_begin, c_end) with one overlay variant; `side_next` holds A's
+// side bytes of chunk c_begin on entry.
+template <bool kFull, Overlay kOverlay, int S, int kPolicy>
+__device__ __forceinline__ void pointwise_chunks(StreamCursor &cursor, const LaneOverlay &lane,
+                                                 const uint8_t *tail_lds, uint8_t *slice,
+                                                 SideChunk &side_next, const PointwiseIo &io,
+                                                 const LanePair &lp, int64_t row_base,
+                                                 uint32_t valid_in_block, int c_begin, int c_end,
+                                                 const OpParams &p) {
+    const uint32_t voffset = side_fetch_offset();
+#pragma unroll 1
+    for (int c = c_begin; c < c_end; c += kChunkSteps) {
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int first = c + half * kHalfSteps;
+            uint32_t bw[kHalfSteps / 2];
+            if (kFull) {
+                // B words of this half, in flight while the entries decode.
+                const uint32_t mask2 = static_cast<uint32_t>((row_base + first) & 254) * 2u;
+#pragma unroll
+                for (int j = 0; j < kHalfSteps; j += 2)
+                    bw[j / 2] = __builtin_amdgcn_raw_buffer_load_b32(
+                        io.other, lp.offset2 ^ mask2 ^ static_cast<uint32_t>(2 * j),
+                        (first + j) * kLanes * 2, 0);
+            }
+            uint32_t f[kHalfSteps];
+            decode_fields<kFull, kOverlay>(cursor, lane, tail_lds, first, row_base,
+                                           valid_in_block, f);
+            if (half == 0) {
+                store_side_chunk(slice, side_next);
+                if (c + kChunkSteps < S) side_next = fetch_side_chunk(io.side, voffset, c + kChunkSteps);
+            }
+            if (kFull)
+                pointwise_half_full<kPolicy>(f, bw, slice, half * kHalfSteps, io, lp, first,
+                                             row_base, p);
+            else
+                pointwise_half_partial<kPolicy>(f, slice, half * kHalfSteps, io, first, row_base,
+                                                valid_in_block, p);
+        }
+        if (kPolicy == LCT_COMPRESSED_OUTPUT) {
+            // The slice now holds the chunk's result side bytes.
+            const uint4 q = reinterpret_cast<const uint4 *>(slice)[threadIdx.x & (kWave - 1)];
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, q), io.side_out,
+                voffset, c * kLanes, kStreaming);
+        }
+    }
+}
+
+template <bool kFull, int S, int kPolicy>
+__device__ __forceinline__ void pointwise_rows(StreamCursor cursor, const LaneOverlay &lane,
+                                               const uint8_t *tail_lds, uint8_t *slice,
+                                               SideChunk side_next, const PointwiseIo &io,
+                                               int64_t row_base, uint32_t valid_in_block,
+                                               const OpParams &p) {
+    const LanePair lp;
+    const int split = min(S, lane.wave_start & ~(kChunkSteps - 1));
+    pointwise_chunks<kFull, kNoOverlay, S, kPolicy>(cursor, lane, tail_lds, slice, side_next, io,
+                                                    lp, row_base, valid_in_block, 0, split, p);
+    if (split == S) return;
+    if (lane.lds)
+        pointwise_chunks<kFull, kLdsOverlay, S, kPolicy>(cursor, lane, tail_lds, slice, side_next,
+                                                         io, lp, row_base, valid_in_block, split,
+                                                         S, p);
+    else
+        pointwise_chunks<kFull, kHbmOverlay, S, kPolicy>(cursor, lane, tail_lds, slice, side_next,
+                                                         io, lp, row_base, valid_in_block, split,
+                                                         S, p);
 }
 
 __global__ __launch_bounds__(kLanes) void pointwise_kernel(
@@ -108,40 +218,51 @@ __global__ __launch_bounds__(kLanes) void pointwise_kernel(
     const float *__restrict__ alpha, const float *__restrict__ beta, int64_t n_blocks,
     int64_t logical_numel, int S, int W, int rare, int op, int alpha_is_one, int beta_is_one,
     int policy, lct_overflow ov, int has_overlay) {
-    extern __shared__ uint32_t stage[];
+    extern __shared__ uint32_t stage[];   // stage_bytes(W)
     __shared__ DecodeTables tb;
-    __shared__ int32_t map_start[kLanes], map_offset[kLanes], scratch[kWavesPerBlock];
+    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ uint8_t tail_lds[kTailLds];
+    __shared__ __attribute__((aligned(16))) uint8_t side_slices[kWavesPerBlock][kChunkSteps * kWave];
+    int32_t *map_start = reinterpret_cast<int32_t *>(&side_slices[0][0]);
+    int32_t *map_offset = map_start + kLanes;
     const int64_t block = blockIdx.x;
+    const int64_t row_base = block * S;
+    const int64_t logical_base = row_base * kLanes;
+    const uint32_t block_elems = static_cast<uint32_t>(S) * kLanes;
+    const int64_t remaining = logical_numel - logical_base;
+    const uint32_t valid = remaining < block_elems ? static_cast<uint32_t>(remaining) : block_elems;
+    PointwiseIo io;
+    io.side = make_rsrc(side + logical_base, block_elems);
+    io.other = make_rsrc(other + logical_base, 2u * valid);
+    io.dense = make_rsrc(static_cast<uint16_t *>(output) + logical_base, 2u * valid);
+    io.side_out = make_rsrc(static_cast<uint8_t *>(output) + logical_base, block_elems);
+    io.exp_out = make_rsrc(auxiliary != nullptr ? auxiliary + logical_base : nullptr,
+                           auxiliary != nullptr ? valid : 0u);
+    const SideChunk first = fetch_side_chunk(io.side, side_fetch_offset(), 0);
+
     build_decode_tables(tb, shifted_decode, center_ptr[0]);
     stage_payload(stage, encoded, n_blocks * kLanes, block, W);
     const LaneOverlay lane = build_overlay(ov, has_overlay != 0, block, n_blocks, S, map_start,
-                                           map_offset, scratch, nullptr, 0);
-    wait_memory();
-    __syncthreads();
-
+                                           map_offset, scratch, tail_lds, kTailLds);
     OpParams p{op, alpha_is_one, beta_is_one, 1.0f, 1.0f};
     if (op == LCT_OP_SCALAR_MUL_ADD) {
         if (!alpha_is_one) p.alpha = alpha[0];
         if (!beta_is_one) p.beta = beta[0];
     }
+    wait_memory();
+    __syncthreads();   // payload and tails visible; overflow maps no longer read
+
     StreamCursor cursor;
     cursor.init(stage + threadIdx.x, &tb, static_cast<uint32_t>(W), rare);
-    const int64_t row_base = block * S;
-    const int64_t logical_base = row_base * kLanes;
-    const uint8_t *side_block = side + logical_base;
-    const uint16_t *other_block = other + logical_base;
-    uint16_t *dense_block = static_cast<uint16_t *>(output) + logical_base;
-    uint8_t *side_out_block = static_cast<uint8_t *>(output) + logical_base;
-    uint8_t *exp_out_block = auxiliary + logical_base;
-    const int64_t valid = logical_numel - logical_base;
-    const bool full = valid >= static_cast<int64_t>(S) * kLanes;
+    uint8_t *slice = side_slices[threadIdx.x / kWave];
 #define LCT_POINTWISE_CASE(FULL, POLICY)                                                       \
     if (S == 128)                                                                              \
-        pointwise_rows<FULL, 128, POLICY>(cursor, lane, side_block, other_block, dense_block, \
-                                          side_out_block, exp_out_block, row_base, valid, p);  \
+        pointwise_rows<FULL, 128, POLICY>(cursor, lane, tail_lds, slice, first, io, row_base,   \
+                                          valid, p);                                           \
     else                                                                                       \
-        pointwise_rows<FULL, 256, POLICY>(cursor, lane, side_block, other_block, dense_block, \
-                                          side_out_block, exp_out_block, row_base, valid, p);
+        pointwise_rows<FULL, 256, POLICY>(cursor, lane, tail_lds, slice, first, io, row_base,   \
+                                          valid, p);
+    const bool full = valid == block_elems;
     if (policy == LCT_DENSE_OUTPUT) {
         if (full) { LCT_POINTWISE_CASE(true, LCT_DENSE_OUTPUT) }
         else { LCT_POINTWISE_CASE(false, LCT_DENSE_OUTPUT) }
