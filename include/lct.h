@@ -86,6 +86,18 @@ int32_t lct_estimate_and_shift_tables(const void *source, int32_t precomputed,
                                       int32_t *center, int32_t *shifted_encode,
                                       int32_t *shifted_decode, hipStream_t stream);
 
+/* ---- the sampling half of dispatch.py:33-48 spread over many workgroups:
+ * sample min(logical_numel, 4096) = sample_size exponents of `source` (as
+ * lct_estimate_and_shift_tables) and write each group of 64 samples' kept
+ * exponent sum and count to partials[2*g], partials[2*g+1]
+ * (int32[2*ceil(sample_size/64)]).  sample_values: NULL, or uint16[
+ * sample_size] that receives the sampled BF16 bits (ignored if precomputed).
+ * lct_encode_sampled turns the partials into the center and tables. */
+int32_t lct_sample_center(const void *source, int32_t precomputed,
+                          int64_t logical_numel, int64_t sample_size,
+                          int32_t *partials, uint16_t *sample_values,
+                          hipStream_t stream);
+
 /* ---- replaces dispatch.py:16-30 (shift_encoding_table): same tables for a
  * given device-resident center. */
 int32_t lct_shift_tables(const int32_t *base_encode, const int32_t *center,
@@ -112,6 +124,21 @@ int32_t lct_encode(const void *source, uint8_t *side, int32_t *encoded,
                    int32_t *summaries, int64_t size, int64_t logical_numel,
                    lct_geometry geometry, int32_t precomputed,
                    int32_t write_summary, hipStream_t stream);
+
+/* ---- lct_encode with the table step of dispatch.py:33-48 folded in: every
+ * workgroup reduces `partials` (lct_sample_center, same sample_size) to the
+ * center and shifts base_encode by it; center_out[1] and
+ * shifted_decode_out[1024] receive the center and the shifted decode table
+ * (as lct_estimate_and_shift_tables writes them).  Other arguments and
+ * outputs as lct_encode. */
+int32_t lct_encode_sampled(const void *source, uint8_t *side, int32_t *encoded,
+                           const int32_t *partials, int64_t sample_size,
+                           const int32_t *base_encode, const int32_t *base_decode,
+                           int32_t *center_out, int32_t *shifted_decode_out,
+                           uint8_t *extra_starts, int32_t *summaries, int64_t size,
+                           int64_t logical_numel, lct_geometry geometry,
+                           int32_t precomputed, int32_t write_summary,
+                           hipStream_t stream);
 
 /* ---- replaces dispatch.py:70-85 (prefix_allocate) and the block-metadata
  * part of compact_extra: summaries is int32[5*nb + 1] whose first 2*nb
@@ -188,6 +215,56 @@ int32_t lct_dual(const int32_t *a_encoded, const uint8_t *a_side,
                  int64_t size, int64_t logical_numel, lct_geometry geometry,
                  int32_t rare_length, int32_t output_policy,
                  hipStream_t stream);
+
+/* ---- single-pass compressed-output pointwise, step 1 of 2: replaces the
+ * center estimate that dispatch.py:33-48 (estimate_and_shift_encoding_table)
+ * makes over the exponent bytes written by dispatch.py:168-187
+ * (pointwise_dense, COMPRESSED_OUTPUT), as LCT/codec/pointwise.py:262-278
+ * sequences them.  Computes op(A, other) only at the center's sample
+ * positions (sample_size = min(logical_numel, 4096), a power of two or
+ * logical_numel) and writes each group of 64 samples' exponent sum and count
+ * to partials[2*g], partials[2*g+1] (int32[2*ceil(sample_size/64)]).  A is
+ * given as for lct_pointwise_dense; op/alpha/beta/flags as there.
+ * a_samples: NULL, or A's BF16 values at the sample positions (uint16[
+ * sample_size], as lct_sample_center or this function records them); with it
+ * A's streams are not read.  result_samples: NULL, or uint16[sample_size] that
+ * receives the result's values at the sample positions. */
+int32_t lct_pointwise_sample(const int32_t *encoded, const uint8_t *side,
+                             const int32_t *shifted_decode, const int32_t *center,
+                             const lct_overflow *overflow, const void *a_samples,
+                             const void *other, const float *alpha, const float *beta,
+                             int64_t size, int64_t logical_numel, lct_geometry geometry,
+                             int32_t rare_length, int32_t op, int32_t alpha_is_one,
+                             int32_t beta_is_one, int64_t sample_size,
+                             int32_t *partials, void *result_samples, hipStream_t stream);
+
+/* ---- single-pass compressed-output pointwise, step 2 of 2: replaces
+ * dispatch.py:168-187 (pointwise_dense, COMPRESSED_OUTPUT) followed by the
+ * table shift of dispatch.py:16-30 and dispatch.py:294-316 (encode_kernel,
+ * precomputed) in one pass.  Reduces `partials` (from lct_pointwise_sample,
+ * same sample_size) to the result's center, shifts the result distribution's
+ * base_encode/base_decode by it, decodes A, applies op with `other` and
+ * encodes the result.  Writes center_out[1], shifted_decode_out[1024] (as
+ * lct_estimate_and_shift_tables), and side_out[size], encoded_out,
+ * extra_starts and summaries[0..2nb) exactly as lct_encode does for the
+ * result; for every overflowing stream, the result's exponent bytes of steps
+ * extra_start..S-1 go to exponents (uint8[logical_numel], logical order; no
+ * other byte of it is written), from where lct_compact_extra
+ * (precomputed = 1) reads the tails.  The result geometry is A's.  encoded,
+ * side and side_out must be 16-byte aligned. */
+int32_t lct_pointwise_encode(const int32_t *encoded, const uint8_t *side,
+                             const int32_t *shifted_decode, const int32_t *center,
+                             const lct_overflow *overflow, const void *other,
+                             const float *alpha, const float *beta,
+                             const int32_t *partials, int64_t sample_size,
+                             const int32_t *base_encode, const int32_t *base_decode,
+                             int32_t *center_out, int32_t *shifted_decode_out,
+                             uint8_t *side_out, int32_t *encoded_out,
+                             uint8_t *extra_starts, int32_t *summaries,
+                             uint8_t *exponents, int64_t size, int64_t logical_numel,
+                             lct_geometry geometry, int32_t rare_length, int32_t op,
+                             int32_t alpha_is_one, int32_t beta_is_one,
+                             hipStream_t stream);
 
 /* ---- TensorBuffer allocator kernels: replace LCT/tensor_buffer.py:130-136
  * (_reset_kernel launch), :93-120 (_allocate_kernel launches) and

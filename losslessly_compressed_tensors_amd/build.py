@@ -25,6 +25,7 @@ SOURCES = [
     "tensor_buffer.hip",
     "decode.hip",
     "pointwise.hip",
+    "update.hip",
 ]
 
 # Packed FP32 instructions are kept out of the device code: the feature is

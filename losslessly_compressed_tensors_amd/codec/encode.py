@@ -2,10 +2,12 @@
 
 Host sequencing of ``LCT/codec/encode.py:22-218`` on the gfx950 library:
 
-1. ``lct_estimate_and_shift_tables`` samples the center and builds the
-   center-shifted encode/decode tables (or shifts them for a given center);
-2. ``lct_encode`` splits fields and writes the fixed payload, per-stream
-   overflow starts and per-block overflow summaries;
+1. ``lct_sample_center`` samples the center's positions over many
+   workgroups (the sampling half of the reference's table kernel);
+2. ``lct_encode_sampled`` derives the center and the center-shifted tables
+   in every workgroup, then splits fields and writes the fixed payload,
+   per-stream overflow starts and per-block overflow summaries (with a given
+   center: ``lct_shift_tables`` then ``lct_encode``);
 3. ``lct_prefix_allocate`` scans the summaries and, for a shared
    ``TensorBuffer``, reserves the overflow region on the device;
 4. private storage only: one device->host sync reads the overflow totals so
@@ -64,38 +66,77 @@ def encode_components(
             f"tensor too large: {blocks} codec blocks; the storage format's int32 offsets "
             f"allow {MAX_CODEC_BLOCKS} ({MAX_CODEC_BLOCKS * block_symbols} elements here)")
     encode_table, decode_table, _ = get_distribution_tables(distribution, device)
-    shifted_encode = torch.empty(256, dtype=torch.int32, device=device)
     shifted_decode = torch.empty_like(decode_table)
-    if center is None:
-        center = torch.empty(1, dtype=torch.int32, device=device)
-        if logical_numel > 0:
-            dispatch.estimate_and_shift_encoding_table(
-                source_values, center, logical_numel, encode_table, shifted_encode,
-                decode_table, shifted_decode, min(logical_numel, CENTER_SAMPLE_SIZE),
-                precomputed)
-        else:
-            center.zero_()   # an empty sample has center 0 (tables.py:47)
-            dispatch.shift_encoding_table(encode_table, center, shifted_encode, decode_table,
-                                          shifted_decode)
-    else:
-        dispatch.shift_encoding_table(encode_table, center, shifted_encode, decode_table,
-                                      shifted_decode)
-
     encoded = torch.empty(streams * fixed_words + 4, dtype=torch.int32, device=device)
     extra_starts = torch.empty(streams, dtype=torch.uint8, device=device)
     # Per-block overflow counts/bytes, their scans and the list of blocks
     # that overflow (int32[5*blocks + 1], see lct_prefix_allocate).
     summaries = torch.empty(5 * blocks + 1, dtype=torch.int32, device=device)
+    launch = dict(precomputed=precomputed, logical_numel=logical_numel,
+                  block_symbols=block_symbols, lanes=lanes, steps=steps, fixed_words=fixed_words)
+    sample_values = None
+    if center is None and logical_numel > 0:
+        # The center's samples are taken by many workgroups; the encoder
+        # reduces their partial sums and shifts the tables itself.  A BF16
+        # source's sampled values are kept for later fused updates.
+        center = torch.empty(1, dtype=torch.int32, device=device)
+        sample_size = min(logical_numel, CENTER_SAMPLE_SIZE)
+        partials = torch.empty(2 * _cdiv(sample_size, 64), dtype=torch.int32, device=device)
+        if not precomputed:
+            sample_values = torch.empty(sample_size, dtype=torch.int16, device=device)
+        dispatch.sample_center(source_values, logical_numel, sample_size, precomputed, partials,
+                               sample_values)
+        dispatch.encode_sampled(source_values, sign_mantissa, encoded, partials, sample_size,
+                                encode_table, decode_table, center, shifted_decode, extra_starts,
+                                summaries, size, **launch)
+    else:
+        if center is None:
+            center = torch.zeros(1, dtype=torch.int32, device=device)   # empty: tables.py:47
+        shifted_encode = torch.empty(256, dtype=torch.int32, device=device)
+        dispatch.shift_encoding_table(encode_table, center, shifted_encode, decode_table,
+                                      shifted_decode)
+        if blocks > 0:
+            dispatch.encode_kernel(source_values, sign_mantissa, encoded, shifted_encode,
+                                   extra_starts, summaries, size, streams, write_summary=True,
+                                   **launch)
+    return finish_encode(source_values, sign_mantissa, encoded, extra_starts, summaries, size,
+                         distribution, buffer, shape, precomputed=precomputed, center=center,
+                         shifted_decode=shifted_decode, logical_numel=logical_numel,
+                         sample_values=sample_values)
+
+
+def finish_encode(
+    tail_source: torch.Tensor,
+    sign_mantissa: torch.Tensor,
+    encoded: torch.Tensor,
+    extra_starts: torch.Tensor,
+    summaries: torch.Tensor,
+    size: int,
+    distribution: Distribution,
+    buffer: TensorBuffer | None,
+    shape: tuple[int, ...],
+    *,
+    precomputed: bool,
+    center: torch.Tensor,
+    shifted_decode: torch.Tensor,
+    logical_numel: int,
+    sample_values: torch.Tensor | None = None,
+) -> CompressedTensor:
+    """Overflow bookkeeping after an encoder pass and the CompressedTensor
+    (``LCT/codec/encode.py:77-186``): block scans and, for a shared buffer, the
+    arena reservation; for private storage one device->host sync that sizes
+    the exact lane/start/tail arrays; then the compaction, which reads the
+    tails' exponents from ``tail_source`` (BF16 bits, or exponent bytes in
+    logical order when ``precomputed``)."""
+    device = encoded.device
+    stream_geometry = geometry(distribution)
+    block_symbols, lanes, steps, _ = stream_geometry
+    blocks = _cdiv(size, block_symbols)
     counts = torch.empty(4, dtype=torch.int32, device=device)
     blocks_out = torch.empty(3 * blocks, dtype=torch.int32, device=device)
     buffered = buffer is not None
     descriptor = torch.empty(4, dtype=torch.int32, device=device) if buffered else counts
     if blocks > 0:
-        dispatch.encode_kernel(
-            source_values, sign_mantissa, encoded, shifted_encode, extra_starts, summaries,
-            size, streams, precomputed=precomputed, logical_numel=logical_numel,
-            block_symbols=block_symbols, lanes=lanes, steps=steps, fixed_words=fixed_words,
-            write_summary=True)
         dispatch.prefix_allocate(summaries, counts, descriptor, buffer, blocks_out, blocks,
                                  buffered, buffer.max_free_regions if buffered else 256)
     else:
@@ -123,7 +164,7 @@ def encode_components(
             blocks=blocks_out, allocation=counts[2:3], base=0)
     if needs_compaction:
         dispatch.compact_extra(
-            source_values, storage, blocks, size, precomputed=precomputed, buffered=buffered,
+            tail_source, storage, blocks, size, precomputed=precomputed, buffered=buffered,
             logical_numel=logical_numel, block_symbols=block_symbols, lanes=lanes,
             steps=steps, extra_starts=extra_starts, summaries=summaries)
     return CompressedTensor(
@@ -138,6 +179,7 @@ def encode_components(
         fallback_used=final_total,
         distribution=distribution, center=center, decode_table=shifted_decode,
         shape=shape, layout=StorageLayout.COMPRESSED, stream_geometry=stream_geometry,
+        sample_values=sample_values,
     )
 
 

@@ -8,9 +8,12 @@ Host logic of ``LCT/codec/pointwise.py:28-304``:
   compressed (one fused launch when geometries and buffering modes agree,
   else decode B and use the dense path).
 
-Dense output is BF16.  Compressed output re-encodes the fused kernel's split
-components (side bytes in storage order + exponent bytes in logical order)
-with a freshly sampled center, so it equals ``compress(result)``.
+Dense output is BF16.  Compressed output equals ``compress(result)`` with a
+freshly sampled center.  With a dense operand it is produced in a single pass
+over the compressed operand (decode, operate, re-encode; see
+``_fused_compressed_output``); the two-compressed form re-encodes the fused
+kernel's split components (side bytes in storage order + exponent bytes in
+logical order), as the reference does for both.
 """
 from __future__ import annotations
 
@@ -26,6 +29,7 @@ from ..kernels import dispatch, hip
 from ..tensor_buffer import TensorBuffer
 from .decode import decode as decode_dense
 from .decode import overlay_of, shifted_decode_table, storage_of
+from .encode import CENTER_SAMPLE_SIZE, finish_encode
 from .encode import encode as compress_dense
 from .encode import encode_components as compress_components
 from .geometry import geometry
@@ -85,6 +89,70 @@ def _launch_pointwise_compressed_dense(data: CompressedTensor, other: torch.Tens
             alpha_is_one=(not scaled) or alpha_is_one, beta_is_one=(not scaled) or beta is None,
             overflow=overlay_of(data))
     return output, auxiliary
+
+
+def _fused_compressed_output(data: CompressedTensor, other: torch.Tensor,
+                             operation: PointwiseOp, result_distribution: Distribution,
+                             buffer: TensorBuffer | None, *, alpha: torch.Tensor | None,
+                             beta: torch.Tensor | None, alpha_is_one: bool) -> CompressedTensor:
+    """``operation(compA, B)`` re-encoded in one pass over A's payload, A's side
+    bytes and B.
+
+    The reference writes the result's side and exponent bytes, then encodes
+    them (``LCT/codec/pointwise.py:262-278`` -> ``LCT/codec/encode.py:22-186``).
+    Here ``lct_pointwise_sample`` computes the result at the center's sample
+    positions (from A's recorded sample values when A has them, else by
+    decoding the sampled streams' prefixes), ``lct_pointwise_encode`` derives
+    the center and encodes the result as it is computed, and only the exponent
+    bytes of overflow rows reach HBM (for the compaction's tails).  The stored
+    tensor is identical.
+    """
+    device = data.data.device
+    scaled = operation is SCALAR_MUL_ADD
+    alpha_is_one = (not scaled) or alpha_is_one
+    beta_is_one = (not scaled) or beta is None
+    other = other.contiguous().view(-1)
+    block_symbols, lanes, steps, fixed_words = data.codec_geometry
+    blocks = data.size // block_symbols
+    streams = blocks * lanes
+    n = data.logical_numel
+    _, _, rare_length = get_distribution_tables(data.distribution, device)
+    base_encode, base_decode, _ = get_distribution_tables(result_distribution, device)
+    sample_size = min(n, CENTER_SAMPLE_SIZE)
+    launch = dict(rare_length=rare_length, logical_numel=n, block_symbols=block_symbols,
+                  lanes=lanes, steps=steps, fixed_words=fixed_words, op=operation.code,
+                  alpha_is_one=alpha_is_one, beta_is_one=beta_is_one, sample_size=sample_size,
+                  overflow=overlay_of(data))
+    alpha_arg = None if alpha_is_one else alpha
+    beta_arg = None if beta_is_one else beta
+    decode_table = shifted_decode_table(data)
+    partials = torch.empty(2 * -(-sample_size // 64), dtype=torch.int32, device=device)
+    # A's recorded values at the sample positions spare the sampler a walk
+    # through A's streams; the result's are recorded for the next update.
+    a_samples = data.sample_values
+    if a_samples is not None and a_samples.numel() != sample_size:
+        a_samples = None
+    result_samples = torch.empty(sample_size, dtype=torch.int16, device=device)
+    dispatch.pointwise_sample(data.data, data.sign_mantissa, decode_table, data.center, other,
+                              alpha_arg, beta_arg, partials, data.size, a_samples=a_samples,
+                              result_samples=result_samples, **launch)
+    center = torch.empty(1, dtype=torch.int32, device=device)
+    shifted_decode = torch.empty(1024, dtype=torch.int32, device=device)
+    side = torch.empty(data.size, dtype=torch.uint8, device=device)
+    encoded = torch.empty(streams * fixed_words + 4, dtype=torch.int32, device=device)
+    extra_starts = torch.empty(streams, dtype=torch.uint8, device=device)
+    summaries = torch.empty(5 * blocks + 1, dtype=torch.int32, device=device)
+    # Only the rows of overflowing streams are written (and read back by the
+    # compaction); the rest stays unwritten.
+    exponents = torch.empty(n, dtype=torch.uint8, device=device)
+    dispatch.pointwise_encode(data.data, data.sign_mantissa, decode_table, data.center, other,
+                              alpha_arg, beta_arg, partials, base_encode,
+                              base_decode, center, shifted_decode, side, encoded, extra_starts,
+                              summaries, exponents, data.size, **launch)
+    return finish_encode(exponents, side, encoded, extra_starts, summaries, data.size,
+                         result_distribution, buffer, data.shape, precomputed=True,
+                         center=center, shifted_decode=shifted_decode, logical_numel=n,
+                         sample_values=result_samples)
 
 
 def _launch_scalar_mul_add_compressed_compressed(data: CompressedTensor,
@@ -178,6 +246,11 @@ def pointwise_compressed_dense(data: CompressedTensor, other: torch.Tensor,
             return result
         return compress_dense(result, result_distribution, buffer)
 
+    if not dense_output and data.logical_numel > 0:
+        if buffer is not None and buffer.capacity_bytes % 4:
+            raise ValueError("TensorBuffer capacity must be divisible by 4")
+        return _fused_compressed_output(data, other, operation, result_distribution, buffer,
+                                        alpha=alpha, beta=beta, alpha_is_one=alpha_is_one)
     policy = DENSE_OUTPUT if dense_output else COMPRESSED_OUTPUT
     values, auxiliary = _launch_pointwise_compressed_dense(
         data, other, operation, policy, alpha=alpha, beta=beta, alpha_is_one=alpha_is_one)

@@ -43,6 +43,11 @@ class CompressedTensor:
     fallback_lanes: Optional[torch.Tensor] = None  # overflow lane per entry (private)
     fallback_blocks: Optional[torch.Tensor] = None  # int32[3*nb] count/first/byte_base
     decode_table: Optional[torch.Tensor] = None  # center-shifted decode table
+    # The tensor's BF16 values at the center's sample positions (uint16[min(n,
+    # 4096)]), recorded when the tensor is made so that a fused update can
+    # sample its result without decoding streams.  An acceleration record, not
+    # part of the reference's storage record: memory_size() does not count it.
+    sample_values: Optional[torch.Tensor] = None
 
     @property
     def codec_geometry(self) -> tuple[int, int, int, int]:
@@ -67,6 +72,8 @@ class CompressedTensor:
             if not isinstance(value, torch.Tensor):
                 continue
             if f.name == "fallback_buffer" and self.fallback_descriptor is not None:
+                continue
+            if f.name == "sample_values":
                 continue
             storage = value.untyped_storage()
             allocations[(value.device, storage.data_ptr())] = storage.nbytes()

@@ -47,18 +47,23 @@ struct DecodeTables {
     uint16_t escape[256];
 };
 
-// Build both tables from the 1024-entry shifted decode table (len | exp << 8).
-__device__ __forceinline__ void build_decode_tables(DecodeTables &tb,
-                                                    const int32_t *__restrict__ shifted_decode,
-                                                    int32_t center) {
-    const int t = threadIdx.x;
-    const int32_t packed = shifted_decode[t];
+// Entry `t` of both tables from entry t of the 1024-entry shifted decode
+// table (len | exp << 8).
+__device__ __forceinline__ void build_decode_entry(DecodeTables &tb, int t, int32_t packed,
+                                                   int32_t center) {
     const int32_t length = packed & 255;
     const uint32_t field = static_cast<uint32_t>(((packed >> 8) + 127) & 255) << 7;
     tb.entry[t] = static_cast<uint16_t>((length >= 1 && length <= 8)
                                             ? (static_cast<uint32_t>(length) | field)
                                             : static_cast<uint32_t>(kEscapeLength));
     tb.escape[t] = static_cast<uint16_t>(((index_to_exponent(t, center) + 127) & 255) << 7);
+}
+
+// Both tables, one entry per thread of a 256-thread block.
+__device__ __forceinline__ void build_decode_tables(DecodeTables &tb,
+                                                    const int32_t *__restrict__ shifted_decode,
+                                                    int32_t center) {
+    build_decode_entry(tb, threadIdx.x, shifted_decode[threadIdx.x], center);
 }
 
 // Copy the W payload rows of `block` into stage rows 0..W-1 and zero the pad
@@ -155,7 +160,7 @@ __device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, boo
     return lane;
 }
 
-// One lane's stream cursor.
+// One lane's stream cursor over payload rows kStride words apart in LDS.
 //
 // The 64-bit window lives in registers: lo/hi are words w and w+1 of the
 // lane's stream, nx is word w+2, and pos (0..31) is the bit offset in lo.  A
@@ -169,8 +174,9 @@ __device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, boo
 // without masking first: (t0 + t1) & 127 = len0 + len1, since each length is at
 // most 31 and the exponent fields start at bit 7.  Direct codes are 1..8 bits,
 // so the sum reaches 32 only when an entry holds the escape marker.
-struct StreamCursor {
-    const uint32_t *stage;    // stage + lane; row r at stage[r * 256]
+template <int kStride>
+struct StreamCursorT {
+    const uint32_t *stage;    // stage + lane; row r at stage[r * kStride]
     const DecodeTables *tb;
     uint32_t pos;             // bit offset within lo
     uint32_t lo, hi, nx;      // stream words w, w+1, w+2
@@ -186,8 +192,8 @@ struct StreamCursor {
         pos = 0;
         pad_row = words;
         lo = stage[0];
-        hi = stage[kLanes];
-        nx = stage[min(2u, words) * kLanes];
+        hi = stage[kStride];
+        nx = stage[min(2u, words) * kStride];
         next_row = min(3u, words);
         pending = 0;
         rare = rare_length;
@@ -196,7 +202,7 @@ struct StreamCursor {
     // Decode the next two symbols into entries f0/f1 (length | field << 7) and
     // return len0 + len1.  Also starts the read of the word a crossing needs.
     __device__ __forceinline__ uint32_t next_fields(uint32_t &f0, uint32_t &f1) {
-        pending = stage[next_row * kLanes];
+        pending = stage[next_row * kStride];
         // Keep the read ahead of the lookups, so its latency overlaps theirs.
         __builtin_amdgcn_sched_barrier(0);
         const uint32_t bits = __builtin_amdgcn_alignbit(hi, lo, pos);
@@ -233,6 +239,9 @@ struct StreamCursor {
         next_row = cross ? min(next_row + 1u, pad_row) : next_row;
     }
 };
+
+// The codec kernels' cursor: one lane per stream of a block, rows of 256 words.
+using StreamCursor = StreamCursorT<kLanes>;
 
 // BF16 bits of a decoded entry (exponent field at bits 7..14, nothing at bit 15
 // or above) and its side byte: one multiply and one bit-field insert

@@ -202,15 +202,30 @@ __device__ __forceinline__ void encode_dispatch(int S, __amdgpu_buffer_rsrc_t sr
                                                row_base, valid, W, first, overflow, extra);
 }
 
+// Where the encoder's table comes from: the center-shifted encode table, or
+// the sampler's partial sums plus the distribution's base tables (the center
+// and shifted tables are then derived in every workgroup; workgroup 0 also
+// stores the center and the shifted decode table).
+struct TableSource {
+    const int32_t *shifted_encode;
+    const int32_t *partials;
+    int32_t n_groups;
+    const int32_t *base_encode;
+    const int32_t *base_decode;
+    int32_t *center_out;
+    int32_t *shifted_decode_out;
+};
+
 __global__ __launch_bounds__(kLanes) void encode_kernel(
     const void *__restrict__ source, uint8_t *__restrict__ side,
-    int32_t *__restrict__ encoded, const int32_t *__restrict__ shifted_encode,
+    int32_t *__restrict__ encoded, TableSource tables,
     uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
     int64_t n_blocks, int64_t logical_numel, int S, int W, int precomputed,
     int write_summary) {
     extern __shared__ uint32_t stage[];   // (W + 1) rows x 256 lanes
     __shared__ uint32_t table[256];
     __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ int32_t shared_center;
     __shared__ __attribute__((aligned(16))) uint8_t in_slices[kWavesPerBlock][2 * kEncChunk * kWave];
     __shared__ __attribute__((aligned(16))) uint8_t side_slices[kWavesPerBlock][kEncChunk * kWave];
     const int t = threadIdx.x;
@@ -226,8 +241,24 @@ __global__ __launch_bounds__(kLanes) void encode_kernel(
         static_cast<const uint8_t *>(source) + logical_base * elem_bytes, valid * elem_bytes);
     const __amdgpu_buffer_rsrc_t side_rsrc = make_rsrc(side + logical_base, block_elems);
 
-    table[t] = repack_encode_entry(static_cast<uint32_t>(shifted_encode[t]));
     for (int i = t; i < (W + 1) * kLanes; i += kLanes) stage[i] = 0u;
+    if (tables.partials != nullptr) {
+        // The raw base table waits in the input slices, which the first
+        // chunk overwrites only after encode_dispatch's barrier.
+        int32_t *raw = reinterpret_cast<int32_t *>(&in_slices[0][0]);
+        raw[t] = tables.base_encode[t];
+        center_from_partials(tables.partials, tables.n_groups, &shared_center);
+        __syncthreads();
+        const int32_t center = shared_center;
+        table[t] = repack_encode_entry(static_cast<uint32_t>(raw[byte_to_index(t, center)]));
+        if (block == 0) {
+            if (t == 0) tables.center_out[0] = center;
+            for (int i = t; i < 1024; i += kLanes)
+                tables.shifted_decode_out[i] = shifted_decode_entry(tables.base_decode[i], center);
+        }
+    } else {
+        table[t] = repack_encode_entry(static_cast<uint32_t>(tables.shifted_encode[t]));
+    }
 
     uint8_t *in_slice = in_slices[t / kWave];
     uint8_t *side_slice = side_slices[t / kWave];
@@ -274,12 +305,13 @@ __global__ __launch_bounds__(kLanes) void encode_kernel(
 
 using namespace lct;
 
-extern "C" int32_t lct_encode(const void *source, uint8_t *side, int32_t *encoded,
-                              const int32_t *shifted_encode, uint8_t *extra_starts,
-                              int32_t *summaries, int64_t size, int64_t logical_numel,
-                              lct_geometry g, int32_t precomputed,
-                              int32_t write_summary, hipStream_t stream) {
-    if (!source || !side || !encoded || !shifted_encode || !extra_starts) return LCT_E_NULL;
+namespace {
+
+int32_t launch_encode(const void *source, uint8_t *side, int32_t *encoded,
+                      const TableSource &tables, uint8_t *extra_starts, int32_t *summaries,
+                      int64_t size, int64_t logical_numel, const lct_geometry &g,
+                      int32_t precomputed, int32_t write_summary, hipStream_t stream) {
+    if (!source || !side || !encoded || !extra_starts) return LCT_E_NULL;
     if (write_summary && !summaries) return LCT_E_NULL;
     if (!geometry_ok(g)) return LCT_E_GEOMETRY;
     if (logical_numel <= 0 || size <= 0 || size % g.block_symbols != 0
@@ -293,8 +325,39 @@ extern "C" int32_t lct_encode(const void *source, uint8_t *side, int32_t *encode
         return LCT_E_ARG;
     const size_t lds = static_cast<size_t>(g.fixed_words + 1) * kLanes * sizeof(uint32_t);
     hipLaunchKernelGGL(encode_kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes),
-                       lds, stream, source, side, encoded, shifted_encode,
+                       lds, stream, source, side, encoded, tables,
                        extra_starts, summaries, n_blocks, logical_numel, g.steps,
                        g.fixed_words, precomputed, write_summary);
     return static_cast<int32_t>(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" int32_t lct_encode(const void *source, uint8_t *side, int32_t *encoded,
+                              const int32_t *shifted_encode, uint8_t *extra_starts,
+                              int32_t *summaries, int64_t size, int64_t logical_numel,
+                              lct_geometry g, int32_t precomputed,
+                              int32_t write_summary, hipStream_t stream) {
+    if (!shifted_encode) return LCT_E_NULL;
+    const TableSource tables{shifted_encode, nullptr, 0, nullptr, nullptr, nullptr, nullptr};
+    return launch_encode(source, side, encoded, tables, extra_starts, summaries, size,
+                         logical_numel, g, precomputed, write_summary, stream);
+}
+
+extern "C" int32_t lct_encode_sampled(const void *source, uint8_t *side, int32_t *encoded,
+                                      const int32_t *partials, int64_t sample_size,
+                                      const int32_t *base_encode, const int32_t *base_decode,
+                                      int32_t *center_out, int32_t *shifted_decode_out,
+                                      uint8_t *extra_starts, int32_t *summaries, int64_t size,
+                                      int64_t logical_numel, lct_geometry g,
+                                      int32_t precomputed, int32_t write_summary,
+                                      hipStream_t stream) {
+    if (!partials || !base_encode || !base_decode || !center_out || !shifted_decode_out)
+        return LCT_E_NULL;
+    if (sample_size <= 0 || sample_size > kMaxSamples || sample_size > logical_numel)
+        return LCT_E_SIZE;
+    const TableSource tables{nullptr, partials, sample_groups(sample_size), base_encode,
+                             base_decode, center_out, shifted_decode_out};
+    return launch_encode(source, side, encoded, tables, extra_starts, summaries, size,
+                         logical_numel, g, precomputed, write_summary, stream);
 }

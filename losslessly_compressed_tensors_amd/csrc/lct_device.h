@@ -40,6 +40,16 @@ __device__ __forceinline__ int32_t byte_to_index(int32_t raw, int32_t center) {
     return exp == -127 ? 0 : delta + (delta < zero_delta ? 1 : 0);
 }
 
+// Entry of the center-shifted decode table: len | exponent << 8, or 0 for a
+// continuation entry (tables.py:102-118).
+__device__ __forceinline__ int32_t shifted_decode_entry(int32_t packed, int32_t center) {
+    const int32_t length = packed & 255;
+    const int32_t exponent = index_to_exponent((packed >> 8) & 255, center);
+    return length == 0 ? 0
+                       : static_cast<int32_t>(static_cast<uint32_t>(length)
+                                              | (static_cast<uint32_t>(exponent) << 8));
+}
+
 // Side byte -> its bits in BF16 position: sign to bit 15, mantissa to 0..6.
 // sm * 257 copies the byte into bits 8..15; the mask keeps bit 15 and 0..6.
 __device__ __forceinline__ uint32_t side_bits(uint32_t sm) {
@@ -65,6 +75,31 @@ __device__ __forceinline__ uint32_t float_to_bf16(float value) {
     const bool nan = (u & 0x7FFFFFFFu) > 0x7F800000u;
     u += 0x7FFFu + ((u >> 16) & 1u);
     return nan ? 0x7FFFu : (u >> 16);
+}
+
+// Center sampling (tables.py:15-49): sample i of M = min(n, 4096) lies in
+// region [i*n/M, (i+1)*n/M) at a hashed offset.  M is either n itself (one
+// element per region, offset 0) or a power of two (the entry points reject any
+// other M), so no 64-bit division is needed; `shift` = log2(M).
+constexpr int kMaxSamples = 4096;
+
+__device__ __forceinline__ int64_t sample_position(int64_t i, int64_t n, int64_t m, int shift) {
+    if (m == n) return i;
+    const uint32_t hashed = static_cast<uint32_t>(i) * 0x9E3779B9u;
+    const int64_t start = (i * n) >> shift;
+    const int64_t end = ((i + 1) * n) >> shift;
+    const uint64_t jitter =
+        (static_cast<uint64_t>(hashed) * static_cast<uint64_t>(end - start)) >> 32;
+    return start + static_cast<int64_t>(jitter);
+}
+
+// The center from the kept samples' exponent sum and count: the mean rounded
+// half away from zero, clamped to [-128, 127]; 0 without samples
+// (tables.py:40-49).
+__device__ __forceinline__ int32_t center_of(int32_t total, int32_t count) {
+    if (count <= 0) return 0;
+    const int32_t c = total >= 0 ? (total + count / 2) / count : -((-total + count / 2) / count);
+    return min(max(c, -128), 127);
 }
 
 __device__ __forceinline__ int wave_lane() { return threadIdx.x & (kWave - 1); }
@@ -115,6 +150,28 @@ __device__ __forceinline__ int32_t block_sum(int32_t v, int32_t *scratch) {
     int32_t total;
     block_exclusive_scan(v, scratch, &total);
     return total;
+}
+
+// The center's samples are taken by workgroups of one wave, one sample per
+// lane; each group writes its kept exponents' sum and count to partials[2g],
+// partials[2g + 1] (at most kMaxSamples / kSampleGroup = 64 groups).
+constexpr int kSampleGroup = 64;
+
+// The center from those partial sums, computed by wave 0 of the block into
+// *shared (visible to the block after its next barrier).
+__device__ __forceinline__ void center_from_partials(const int32_t *__restrict__ partials,
+                                                     int32_t n_groups, int32_t *shared) {
+    if (threadIdx.x < kWave) {
+        const int t = threadIdx.x;
+        const int32_t sum = wave_sum(t < n_groups ? partials[2 * t] : 0);
+        const int32_t kept = wave_sum(t < n_groups ? partials[2 * t + 1] : 0);
+        if (t == 0) *shared = center_of(sum, kept);
+    }
+}
+
+// Number of sampling groups for sample_size samples.
+__host__ __device__ constexpr int32_t sample_groups(int64_t sample_size) {
+    return static_cast<int32_t>((sample_size + kSampleGroup - 1) / kSampleGroup);
 }
 
 // Largest codec block count of one tensor: overflow offsets and tail byte

@@ -16,37 +16,10 @@
 // fma(b, beta, a) when alpha is one); the result is rounded to BF16 to
 // nearest-even.  Compressed output: side byte at the storage offset (0 for
 // padding), exponent byte at the logical offset.
-#include "decode_core.h"
+#include "pointwise_ops.h"
 
 namespace lct {
 namespace {
-
-struct OpParams {
-    int32_t op;
-    int32_t alpha_is_one;
-    int32_t beta_is_one;
-    float alpha;
-    float beta;
-};
-
-__device__ __forceinline__ uint32_t apply_op_f(const OpParams &p, float a, float b) {
-    float r;
-    if (p.op == LCT_OP_ADD) {
-        r = a + b;
-    } else if (p.op == LCT_OP_MULTIPLY) {
-        r = a * b;
-    } else if (p.alpha_is_one) {
-        r = p.beta_is_one ? a + b : __builtin_fmaf(b, p.beta, a);
-    } else {
-        if (!p.beta_is_one) b = b * p.beta;
-        r = __builtin_fmaf(a, p.alpha, b);
-    }
-    return float_to_bf16(r);
-}
-
-__device__ __forceinline__ uint32_t apply_op(const OpParams &p, uint32_t left, uint32_t right) {
-    return apply_op_f(p, bf16_to_float(left), bf16_to_float(right));
-}
 
 // Emits one result.  Dense: bf16 at the logical offset.  Compressed: side byte
 // at the storage slot (0 when the position is padding) and exponent byte at
@@ -244,11 +217,7 @@ __global__ __launch_bounds__(kLanes) void pointwise_kernel(
     stage_payload(stage, encoded, n_blocks * kLanes, block, W);
     const LaneOverlay lane = build_overlay(ov, has_overlay != 0, block, n_blocks, S, map_start,
                                            map_offset, scratch, tail_lds, kTailLds);
-    OpParams p{op, alpha_is_one, beta_is_one, 1.0f, 1.0f};
-    if (op == LCT_OP_SCALAR_MUL_ADD) {
-        if (!alpha_is_one) p.alpha = alpha[0];
-        if (!beta_is_one) p.beta = beta[0];
-    }
+    const OpParams p = load_op_params(op, alpha_is_one, beta_is_one, alpha, beta);
     wait_memory();
     __syncthreads();   // payload and tails visible; overflow maps no longer read
 

@@ -10,8 +10,6 @@
 namespace lct {
 namespace {
 
-constexpr int kMaxSamples = 4096;
-
 __global__ __launch_bounds__(kLanes) void tables_kernel(
     const void *__restrict__ source, int32_t precomputed, int64_t logical_numel,
     int64_t sample_size, const int32_t *__restrict__ base_encode,
@@ -23,10 +21,6 @@ __global__ __launch_bounds__(kLanes) void tables_kernel(
     const int t = threadIdx.x;
     int32_t center;
     if (estimate) {
-        // Region i is [i*n/M, (i+1)*n/M).  M = min(n, 4096) is either n
-        // itself (one element per region, jitter 0) or a power of two (the
-        // entry point rejects any other M), so no 64-bit division is needed.
-        const bool every = sample_size == logical_numel;
         const int shift = __builtin_ctzll(static_cast<uint64_t>(sample_size));
         // All of a thread's (at most 16) samples are loaded before any is used.
         constexpr int kPerThread = kMaxSamples / kLanes;
@@ -36,15 +30,7 @@ __global__ __launch_bounds__(kLanes) void tables_kernel(
             const int64_t i = t + k * kLanes;
             raw[k] = 0x7FFFFFFF;
             if (i < sample_size) {
-                int64_t pos = i;
-                if (!every) {
-                    const uint32_t hashed = static_cast<uint32_t>(i) * 0x9E3779B9u;
-                    const int64_t start = (i * logical_numel) >> shift;
-                    const int64_t end = ((i + 1) * logical_numel) >> shift;
-                    const uint64_t jitter =
-                        (static_cast<uint64_t>(hashed) * static_cast<uint64_t>(end - start)) >> 32;
-                    pos = start + static_cast<int64_t>(jitter);
-                }
+                const int64_t pos = sample_position(i, logical_numel, sample_size, shift);
                 raw[k] = precomputed ? static_cast<int32_t>(static_cast<const uint8_t *>(source)[pos])
                                      : static_cast<int32_t>(static_cast<const int16_t *>(source)[pos]);
             }
@@ -62,12 +48,7 @@ __global__ __launch_bounds__(kLanes) void tables_kernel(
         const int32_t total = block_sum(sum, scratch);
         const int32_t count = block_sum(kept, scratch);
         if (t == 0) {
-            int32_t c = 0;
-            if (count > 0) {
-                c = total >= 0 ? (total + count / 2) / count
-                               : -((-total + count / 2) / count);
-                c = min(max(c, -128), 127);
-            }
+            const int32_t c = center_of(total, count);
             center_io[0] = c;
             shared_center = c;
         }
@@ -82,14 +63,38 @@ __global__ __launch_bounds__(kLanes) void tables_kernel(
     }
     if (shifted_decode != nullptr) {
 #pragma unroll
-        for (int i = t; i < 1024; i += kLanes) {
-            const int32_t packed = base_decode[i];
-            const int32_t length = packed & 255;
-            const int32_t exponent = index_to_exponent((packed >> 8) & 255, center);
-            shifted_decode[i] = length == 0
-                ? 0 : static_cast<int32_t>(static_cast<uint32_t>(length)
-                                           | (static_cast<uint32_t>(exponent) << 8));
+        for (int i = t; i < 1024; i += kLanes)
+            shifted_decode[i] = shifted_decode_entry(base_decode[i], center);
+    }
+}
+
+// One sample per lane (tables.py:15-49 split over 64-sample groups): the
+// group's kept exponent sum and count go to partials; the sampled BF16 bits
+// also go to sample_values[i] when given (never for exponent-byte sources).
+__global__ __launch_bounds__(kSampleGroup) void sample_center_kernel(
+    const void *__restrict__ source, int32_t precomputed, int64_t logical_numel,
+    int64_t sample_size, int32_t *__restrict__ partials, uint16_t *__restrict__ sample_values) {
+    const int t = threadIdx.x;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kSampleGroup + t;
+    const bool active = i < sample_size;
+    const int shift = __builtin_ctzll(static_cast<uint64_t>(sample_size));
+    int32_t exp = -127;
+    if (active) {
+        const int64_t pos = sample_position(i, logical_numel, sample_size, shift);
+        if (precomputed) {
+            exp = static_cast<int32_t>(static_cast<const uint8_t *>(source)[pos]) - 127;
+        } else {
+            const uint32_t bits = static_cast<const uint16_t *>(source)[pos];
+            exp = static_cast<int32_t>((bits >> 7) & 0xFFu) - 127;
+            if (sample_values != nullptr) sample_values[i] = static_cast<uint16_t>(bits);
         }
+    }
+    const bool keep = active && exp >= -120;
+    const int32_t sum = wave_sum(keep ? exp : 0);
+    const int32_t kept = wave_sum(keep ? 1 : 0);
+    if (t == 0) {
+        partials[2 * blockIdx.x] = sum;
+        partials[2 * blockIdx.x + 1] = kept;
     }
 }
 
@@ -97,6 +102,22 @@ __global__ __launch_bounds__(kLanes) void tables_kernel(
 }  // namespace lct
 
 using namespace lct;
+
+extern "C" int32_t lct_sample_center(const void *source, int32_t precomputed,
+                                     int64_t logical_numel, int64_t sample_size,
+                                     int32_t *partials, uint16_t *sample_values,
+                                     hipStream_t stream) {
+    if (!source || !partials) return LCT_E_NULL;
+    if (logical_numel <= 0 || sample_size <= 0 || sample_size > kMaxSamples
+        || sample_size > logical_numel)
+        return LCT_E_SIZE;
+    if (sample_size != logical_numel && (sample_size & (sample_size - 1)) != 0)
+        return LCT_E_ARG;
+    hipLaunchKernelGGL(sample_center_kernel, dim3(sample_groups(sample_size)), dim3(kSampleGroup),
+                       0, stream, source, precomputed, logical_numel, sample_size, partials,
+                       precomputed ? nullptr : sample_values);
+    return static_cast<int32_t>(hipGetLastError());
+}
 
 extern "C" int32_t lct_estimate_and_shift_tables(
     const void *source, int32_t precomputed, int64_t logical_numel,

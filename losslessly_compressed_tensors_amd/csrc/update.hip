@@ -1,0 +1,618 @@
+// Single-pass pointwise update with compressed output (gfx950).
+//
+// The reference's compressed-output path (LCT/codec/pointwise.py:262-278)
+// runs the fused pointwise kernel with COMPRESSED_OUTPUT, which writes the
+// result's side bytes and exponent bytes to HBM
+// (LCT/kernels/generic/pointwise.py:43-65), and then re-encodes them through
+// encode_components(precomputed=True) (LCT/codec/encode.py:22-186): a center
+// estimated from up to 4096 sampled exponent bytes of the result
+// (LCT/kernels/common/tables.py:9-49), the encoder kernel
+// (LCT/kernels/generic/encode.py:10-169), the block scan and the compaction.
+// The result's exponent and side bytes make a round trip through HBM between
+// the two passes.  Here they never leave the chip:
+//
+//  * pointwise_sample_kernel computes the operation's result only at the
+//    sampled positions, decoding each sampled stream's prefix from its payload
+//    words, and writes the exponent sum and count of each group of 64 samples;
+//  * pointwise_encode_kernel reduces those sums to the result's center in
+//    every workgroup, shifts the result distribution's encode table by it, and
+//    then, per codec block, decodes A, applies the operation with the dense
+//    operand B and encodes the result in the same pass.  Its outputs are the
+//    encoder's: side bytes, every payload word, extra starts and the block
+//    summaries.  Rows that an overflowing stream cannot hold also get the
+//    result's exponent bytes written (logical order, those rows only), which
+//    is where the compaction reads their tails, as in the precomputed path.
+//
+// The encoder side writes each payload word straight to HBM when the word
+// completes (one 4-byte store by the lanes whose word completed in a pair,
+// merged in L2), so the workgroup's LDS holds only A's payload: at W = 25,
+// four blocks fit per CU.
+#include "pointwise_ops.h"
+
+namespace lct {
+namespace {
+
+struct OperandA {
+    const int32_t *encoded;
+    const uint8_t *side;
+    const int32_t *shifted_decode;
+    const int32_t *center;
+    lct_overflow ov;
+    int32_t has_overlay;
+};
+
+struct OpArgs {
+    const float *alpha;
+    const float *beta;
+    int32_t op;
+    int32_t alpha_is_one;
+    int32_t beta_is_one;
+};
+
+// Overflow start and tail byte index of one stream (block, lane) of A, from
+// the block's entry list (ascending lanes, tails concatenated in entry order:
+// LCT/kernels/generic/compaction.py:137-228, decode.py:195-240).  `start` is S
+// when the stream does not overflow.
+__device__ __forceinline__ void stream_overlay(const lct_overflow &ov, bool present, int64_t block,
+                                               int64_t n_blocks, int32_t lane, int S,
+                                               int32_t &start, int64_t &tail_index) {
+    start = S;
+    tail_index = 0;
+    if (!present) return;
+    int32_t count = ov.blocks[block];
+    if (ov.descriptor != nullptr && ov.descriptor[2] != 0) count = 0;
+    if (count <= 0) return;
+    int64_t lane_off = 0, start_off = 0, tail_base = ov.base;
+    if (ov.descriptor != nullptr) {
+        const int64_t arena = ov.descriptor[0];
+        const int64_t total = ov.count[0];
+        lane_off = arena;
+        start_off = arena + total;
+        tail_base = arena + 2 * total;
+    }
+    const int32_t first = ov.blocks[n_blocks + block];
+    int64_t offset = tail_base + ov.blocks[2 * n_blocks + block];
+    for (int32_t e = 0; e < count; ++e) {
+        const int32_t entry_lane = ov.lanes[lane_off + first + e];
+        const int32_t entry_start = ov.starts[start_off + first + e];
+        if (entry_lane == lane) {
+            start = entry_start;
+            tail_index = offset;
+            return;
+        }
+        offset += S - entry_start;
+    }
+}
+
+// One sample per thread: the result's exponent at sample position i.  A's
+// value there comes from a_samples (A's values at the same positions, recorded
+// when A was made) or, without it, from A's streams: the sampled stream's W
+// words are staged in this thread's LDS column and its pairs decoded up to the
+// sample's step.  The result's values go to result_samples when given.
+__global__ __launch_bounds__(kSampleGroup) void pointwise_sample_kernel(
+    OperandA a, const uint16_t *__restrict__ a_samples, const uint16_t *__restrict__ other,
+    OpArgs args, int64_t n_blocks, int64_t logical_numel, int64_t sample_size, int S, int W,
+    int rare, int32_t *__restrict__ partials, uint16_t *__restrict__ result_samples) {
+    extern __shared__ uint32_t words[];   // (W + 1) rows x kSampleGroup
+    __shared__ DecodeTables tb;
+    const int t = threadIdx.x;
+    if (a_samples != nullptr) {
+        const int64_t i = static_cast<int64_t>(blockIdx.x) * kSampleGroup + t;
+        const bool active = i < sample_size;
+        const int shift = __builtin_ctzll(static_cast<uint64_t>(sample_size));
+        uint32_t result = 0;
+        if (active) {
+            const int64_t pos = sample_position(i, logical_numel, sample_size, shift);
+            const OpParams p = load_op_params(args.op, args.alpha_is_one, args.beta_is_one,
+                                              args.alpha, args.beta);
+            result = apply_op(p, a_samples[i], other[pos]);
+            if (result_samples != nullptr) result_samples[i] = static_cast<uint16_t>(result);
+        }
+        const int32_t exp = static_cast<int32_t>((result >> 7) & 255u) - 127;
+        const bool keep = active && exp >= -120;
+        const int32_t sum = wave_sum(keep ? exp : 0);
+        const int32_t kept = wave_sum(keep ? 1 : 0);
+        if (t == 0) {
+            partials[2 * blockIdx.x] = sum;
+            partials[2 * blockIdx.x + 1] = kept;
+        }
+        return;
+    }
+    int32_t packed[256 / kSampleGroup];
+#pragma unroll
+    for (int k = 0; k < 256 / kSampleGroup; ++k) packed[k] = a.shifted_decode[t + k * kSampleGroup];
+    const int32_t center = a.center[0];
+    const OpParams p = load_op_params(args.op, args.alpha_is_one, args.beta_is_one, args.alpha,
+                                      args.beta);
+
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kSampleGroup + t;
+    const bool active = i < sample_size;
+    const int shift = __builtin_ctzll(static_cast<uint64_t>(sample_size));
+    const int64_t pos = active ? sample_position(i, logical_numel, sample_size, shift) : 0;
+    const int64_t row = pos / kLanes;                 // storage row of the sample
+    const int32_t lane = static_cast<int32_t>((pos % kLanes) ^ (row & 254));
+    const int64_t block = row >> (S == 128 ? 7 : 8);   // S is 128 or 256
+    const int32_t step = static_cast<int32_t>(row & (S - 1));
+    const int64_t n_streams = n_blocks * kLanes;
+    // The stream's words go straight to this thread's LDS column (row w at
+    // words[w * 64 + t]); all W loads are in flight at once.  Inactive lanes
+    // read stream 0.
+    const int32_t *column = a.encoded + (active ? block * kLanes + lane : 0);
+    for (int w = 0; w < W; ++w)
+        __builtin_amdgcn_global_load_lds(
+            column + w * n_streams,
+            (__attribute__((address_space(3))) void *)(words + w * kSampleGroup), 4, 0, 0);
+    words[W * kSampleGroup + t] = 0u;
+    const uint32_t sm = active ? a.side[row * kLanes + lane] : 0u;
+    const uint32_t b = active ? other[pos] : 0u;
+#pragma unroll
+    for (int k = 0; k < 256 / kSampleGroup; ++k)
+        build_decode_entry(tb, t + k * kSampleGroup, packed[k], center);
+    int32_t start;
+    int64_t tail_index;
+    stream_overlay(a.ov, active && a.has_overlay != 0, block, n_blocks, lane, S, start, tail_index);
+    wait_memory();
+    __syncthreads();   // decode tables and staged words
+
+    uint32_t field = 0;
+    if (step >= start) {
+        field = tail_field(a.ov.tail[tail_index + (step - start)]);
+    } else if (active) {
+        // Steps before `start` hold payload codes; so do all earlier steps of
+        // the stream, none of which is padding (their logical offsets are
+        // below this sample's).
+        StreamCursorT<kSampleGroup> cursor;
+        cursor.init(words + t, &tb, static_cast<uint32_t>(W), rare);
+        for (int pair = 0; pair < step / 2; ++pair) {
+            uint32_t f0, f1;
+            cursor.advance(cursor.next_fields(f0, f1));
+        }
+        uint32_t f0, f1;
+        cursor.next_fields(f0, f1);
+        field = (step & 1) ? f1 : f0;
+    }
+    const uint32_t result = apply_op(p, join_entry(field, sm), b);
+    if (active && result_samples != nullptr) result_samples[i] = static_cast<uint16_t>(result);
+    const int32_t exp = static_cast<int32_t>((result >> 7) & 255u) - 127;
+    const bool keep = active && exp >= -120;
+    const int32_t sum = wave_sum(keep ? exp : 0);
+    const int32_t kept = wave_sum(keep ? 1 : 0);
+    if (t == 0) {
+        partials[2 * blockIdx.x] = sum;
+        partials[2 * blockIdx.x + 1] = kept;
+    }
+}
+
+// ---- the fused decode -> operation -> encode kernel
+//
+// Memory operations are arranged for gfx9's single load/store counter
+// (vmcnt): a chunk's A side bytes and B words are fetched one chunk ahead,
+// before the previous chunk's stores are issued, and every store is
+// unconditional -- lanes that must not write get an out-of-range buffer offset,
+// which the hardware drops.  The compiler can then wait for exactly the loads
+// it needs without also waiting for recent stores.
+
+// Buffer offset rejected by the range check of every resource used here
+// (num_records < 2^31): loads return 0, stores are dropped.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+// Encoder state of one lane's output stream.  Word r of the stream is at byte
+// r * row_bytes + 4 * lane of the block's payload resource.  Once a pair does
+// not fit, pos is parked at limit + 1: every later pair then overflows too and
+// stores nothing (encode.py:73-90: only the first overflowing pair matters).
+struct StreamWriter {
+    __amdgpu_buffer_rsrc_t out;
+    uint32_t row_bytes;   // 4 * n_streams
+    uint32_t row_off;     // byte offset of the word at row pos / 32
+    uint32_t limit;       // 32 W
+    uint32_t pos;         // bits emitted; limit + 1 after an overflow
+    uint32_t word;        // bits of the word at row pos / 32 so far
+    int32_t extra;        // the first pair that did not fit (its even step)
+
+    __device__ __forceinline__ bool overflowed() const { return pos > limit; }
+
+    // Append the pair code of encode entries e0/e1 (reversed code in bits
+    // 0..15, length in 16..20; 0 = no code) for the pair at `step`, following
+    // encode.py:66-90.  Returns whether the pair (and so every later one)
+    // overflows.  One store per pair: the word this pair completes, or, at the
+    // stream's first pair that does not fit, the bits before it (unless the
+    // stream is exactly full).
+    __device__ __forceinline__ bool put(uint32_t e0, uint32_t e1, int step) {
+        const uint32_t len0 = e0 >> 16;
+        const uint32_t code = (e0 & 0xFFFFu) | ((e1 & 0xFFFFu) << len0);
+        const uint32_t len = len0 + (e1 >> 16);
+        const uint32_t shift = pos & 31u;
+        const uint64_t placed = static_cast<uint64_t>(code) << shift;
+        const uint32_t new_word = word | static_cast<uint32_t>(placed);
+        const uint32_t after = pos + len;
+        const bool over = after > limit;
+        const bool completes = shift + len >= 32u;
+        const bool write = over ? pos < limit : completes;
+        __builtin_amdgcn_raw_buffer_store_b32(over ? word : new_word, out,
+                                              write ? row_off : kOutOfRange, 0, 0);
+        extra = over && pos <= limit ? step : extra;
+        row_off += completes ? row_bytes : 0u;
+        word = completes ? static_cast<uint32_t>(placed >> 32) : new_word;
+        pos = over ? limit + 1u : after;
+        return over;
+    }
+
+    // After the last pair: the partial word, then zero words up to row W-1.
+    __device__ __forceinline__ void finish() {
+        for (uint32_t r = pos; r < limit; r += 32u) {
+            __builtin_amdgcn_raw_buffer_store_b32(word, out, row_off, 0, 0);
+            word = 0u;
+            row_off += row_bytes;
+        }
+    }
+};
+
+// Encode-table entry repacked for the kernel: reversed code (<= 16 bits) in
+// bits 0..15, code length in bits 16..20 (shifted tables: tables.py:53-67).
+__device__ __forceinline__ uint32_t repack_encode_entry(uint32_t packed) {
+    return (packed & 0xFFFFu) | ((packed >> 20) << 16);
+}
+
+struct UpdateIo {
+    __amdgpu_buffer_rsrc_t side;       // A's side bytes (storage order)
+    __amdgpu_buffer_rsrc_t other;      // B, BF16 in logical order
+    __amdgpu_buffer_rsrc_t side_out;   // result side bytes (storage order)
+    __amdgpu_buffer_rsrc_t exponents;  // result exponent bytes of overflow rows (logical order)
+};
+
+// B words of the 16-step chunk at `first` (one 4-byte word per lane per step
+// pair, lane-pair layout), or zeros without memory traffic when !fetch.
+__device__ __forceinline__ void fetch_b_chunk(uint32_t (&bw)[kChunkSteps / 2],
+                                              const UpdateIo &io, const LanePair &lp,
+                                              int64_t row_base, int first, bool fetch) {
+    const uint32_t mask2 = static_cast<uint32_t>((row_base + first) & 254) * 2u;
+#pragma unroll
+    for (int j = 0; j < kChunkSteps; j += 2)
+        bw[j / 2] = __builtin_amdgcn_raw_buffer_load_b32(
+            io.other, fetch ? (lp.offset2 ^ mask2 ^ static_cast<uint32_t>(2 * j)) : kOutOfRange,
+            (first + j) * kLanes * 2, 0);
+}
+
+// Results r0/r1 (BF16 in the high halves) of this lane's pair at `step`: side
+// bytes replace A's in the wave's slice, the exponent bytes are encoded, and
+// an overflowing pair's exponent bytes go to the exponent array (positions
+// past the tensor's end are outside its resource and are dropped).
+__device__ __forceinline__ void emit_pair(StreamWriter &writer, const uint32_t *enc,
+                                          uint8_t *slice, int s0, uint32_t h0, uint32_t h1,
+                                          bool v0, bool v1, uint32_t off0, int step,
+                                          const UpdateIo &io) {
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    slice[s0 * kWave + lane] = static_cast<uint8_t>(high_side_byte(h0));
+    slice[(s0 + 1) * kWave + lane] = static_cast<uint8_t>(high_side_byte(h1));
+    const uint32_t x0 = high_exponent_byte(h0);
+    const uint32_t x1 = high_exponent_byte(h1);
+    // Positions past the logical end carry no code (encode.py:255-256).
+    const uint32_t e0 = v0 ? enc[x0] : 0u;
+    const uint32_t e1 = v1 ? enc[x1] : 0u;
+    const bool over = writer.put(e0, e1, step);
+    const uint32_t exp_off = over ? off0 : kOutOfRange;
+    __builtin_amdgcn_raw_buffer_store_b8(x0, io.exponents, exp_off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b8(x1, io.exponents, exp_off + kLanes, 0, 0);
+}
+
+// Chunks [c_begin, c_end) with one overlay variant of A.  On entry side_next
+// and b_next hold chunk c_begin's A side bytes and B words (B only for full
+// blocks); on exit those of chunk c_end.  kForm < 0: the operation is chosen at
+// run time (the last, partial block).
+template <bool kFull, Overlay kOverlay, int S, int kForm>
+__device__ __forceinline__ void update_chunks(StreamCursor &cursor, const LaneOverlay &lane,
+                                              const uint8_t *tail_lds, uint8_t *slice,
+                                              SideChunk &side_next,
+                                              uint32_t (&b_next)[kChunkSteps / 2],
+                                              StreamWriter &writer, const uint32_t *enc,
+                                              const UpdateIo &io, const LanePair &lp,
+                                              int64_t row_base, uint32_t valid_in_block,
+                                              int c_begin, int c_end, const OpParams &p) {
+    const uint32_t voffset = side_fetch_offset();
+#pragma unroll 1
+    for (int c = c_begin; c < c_end; c += kChunkSteps) {
+        store_side_chunk(slice, side_next);
+        uint32_t b_cur[kChunkSteps / 2];
+#pragma unroll
+        for (int k = 0; k < kChunkSteps / 2; ++k) b_cur[k] = b_next[k];
+        const bool more = c + kChunkSteps < S;
+        side_next = fetch_side_chunk(io.side, more ? voffset : kOutOfRange, c + kChunkSteps);
+        if (kFull) fetch_b_chunk(b_next, io, lp, row_base, c + kChunkSteps, more);
+        const uint32_t mask = static_cast<uint32_t>((row_base + c) & 254);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int first = c + half * kHalfSteps;
+            uint32_t f[kHalfSteps];
+            decode_fields<kFull, kOverlay>(cursor, lane, tail_lds, first, row_base,
+                                           valid_in_block, f);
+#pragma unroll
+            for (int j = 0; j < kHalfSteps; j += 2) {
+                const int s0 = half * kHalfSteps + j;   // step within the chunk
+                const int step = c + s0;
+                // Logical offset (in the block) of this lane's element of row
+                // `step`; row step+1 shares the swizzle mask, and the chunk's
+                // first row is a multiple of 16, so the mask of row c+s0 is
+                // mask ^ s0.
+                const uint32_t off0 = static_cast<uint32_t>(step) * kLanes
+                    + (threadIdx.x ^ mask ^ static_cast<uint32_t>(s0));
+                const uint32_t a0 = join_entry(f[j], side_byte(slice, s0));
+                const uint32_t a1 = join_entry(f[j + 1], side_byte(slice, s0 + 1));
+                uint32_t h0, h1;
+                bool v0 = true, v1 = true;
+                if (kFull) {
+                    float b0, b1;
+                    pair_unpack16(lp, b_cur[s0 / 2], b0, b1);
+                    h0 = round_bf16_high(apply_form<kForm>(p, bf16_to_float(a0), b0));
+                    h1 = round_bf16_high(apply_form<kForm>(p, bf16_to_float(a1), b1));
+                } else {
+                    v0 = off0 < valid_in_block;
+                    v1 = off0 + kLanes < valid_in_block;
+                    // Outside the tensor the resource returns 0.
+                    const uint32_t b0 = __builtin_amdgcn_raw_buffer_load_b16(io.other, off0 * 2, 0, 0);
+                    const uint32_t b1 = __builtin_amdgcn_raw_buffer_load_b16(
+                        io.other, (off0 + kLanes) * 2, 0, 0);
+                    // Padding positions hold 0 (side byte 0, no code).
+                    h0 = v0 ? apply_op(p, a0, b0) << 16 : 0u;
+                    h1 = v1 ? apply_op(p, a1, b1) << 16 : 0u;
+                }
+                emit_pair(writer, enc, slice, s0, h0, h1, v0, v1, off0, step, io);
+            }
+        }
+        // The slice now holds the chunk's result side bytes.
+        const uint4 q = reinterpret_cast<const uint4 *>(slice)[threadIdx.x & (kWave - 1)];
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, q), io.side_out,
+            voffset, c * kLanes, kStreaming);
+    }
+}
+
+template <bool kFull, int S, int kForm>
+__device__ __forceinline__ void update_rows(StreamCursor cursor, const LaneOverlay &lane,
+                                            const uint8_t *tail_lds, uint8_t *slice,
+                                            SideChunk side_next, StreamWriter &writer,
+                                            const uint32_t *enc, const UpdateIo &io,
+                                            int64_t row_base, uint32_t valid_in_block,
+                                            const OpParams &p) {
+    const LanePair lp;
+    uint32_t b_next[kChunkSteps / 2];
+    if (kFull) fetch_b_chunk(b_next, io, lp, row_base, 0, true);
+    const int split = min(S, lane.wave_start & ~(kChunkSteps - 1));
+    update_chunks<kFull, kNoOverlay, S, kForm>(cursor, lane, tail_lds, slice, side_next, b_next,
+                                               writer, enc, io, lp, row_base, valid_in_block, 0,
+                                               split, p);
+    if (split == S) return;
+    if (lane.lds)
+        update_chunks<kFull, kLdsOverlay, S, kForm>(cursor, lane, tail_lds, slice, side_next,
+                                                    b_next, writer, enc, io, lp, row_base,
+                                                    valid_in_block, split, S, p);
+    else
+        update_chunks<kFull, kHbmOverlay, S, kForm>(cursor, lane, tail_lds, slice, side_next,
+                                                    b_next, writer, enc, io, lp, row_base,
+                                                    valid_in_block, split, S, p);
+}
+
+// Full blocks take the operation's form as a template parameter; the last,
+// partial block decides at run time.
+template <int S>
+__device__ __forceinline__ void update_block(int32_t form, bool full, const StreamCursor &cursor,
+                                             const LaneOverlay &lane, const uint8_t *tail_lds,
+                                             uint8_t *slice, const SideChunk &side_next,
+                                             StreamWriter &writer, const uint32_t *enc,
+                                             const UpdateIo &io, int64_t row_base,
+                                             uint32_t valid_in_block, const OpParams &p) {
+    if (!full) {
+        update_rows<false, S, -1>(cursor, lane, tail_lds, slice, side_next, writer, enc, io,
+                                  row_base, valid_in_block, p);
+        return;
+    }
+    switch (form) {
+    case kFormAxpy:
+        update_rows<true, S, kFormAxpy>(cursor, lane, tail_lds, slice, side_next, writer, enc, io,
+                                        row_base, valid_in_block, p);
+        break;
+    case kFormAxpby:
+        update_rows<true, S, kFormAxpby>(cursor, lane, tail_lds, slice, side_next, writer, enc,
+                                         io, row_base, valid_in_block, p);
+        break;
+    case kFormBxpa:
+        update_rows<true, S, kFormBxpa>(cursor, lane, tail_lds, slice, side_next, writer, enc, io,
+                                        row_base, valid_in_block, p);
+        break;
+    default:
+        update_rows<true, S, kFormMul>(cursor, lane, tail_lds, slice, side_next, writer, enc, io,
+                                       row_base, valid_in_block, p);
+        break;
+    }
+}
+
+__global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
+    OperandA a, const uint16_t *__restrict__ other, OpArgs args,
+    const int32_t *__restrict__ partials, int32_t n_groups,
+    const int32_t *__restrict__ base_encode, const int32_t *__restrict__ base_decode,
+    int32_t *__restrict__ center_out, int32_t *__restrict__ shifted_decode_out,
+    uint8_t *__restrict__ side_out, int32_t *__restrict__ encoded_out,
+    uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
+    uint8_t *__restrict__ exponents, int64_t n_blocks, int64_t logical_numel, int S, int W,
+    int rare) {
+    extern __shared__ uint32_t stage[];   // A's payload: stage_bytes(W)
+    __shared__ DecodeTables tb;
+    __shared__ uint32_t enc[256];
+    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ int32_t shared_center;
+    __shared__ uint8_t tail_lds[kTailLds];
+    // The overflow maps (2 KiB) and the raw encode table (1 KiB) are only used
+    // before the first side chunk is stored, so they share the side slices.
+    __shared__ __attribute__((aligned(16))) uint8_t side_slices[kWavesPerBlock][kChunkSteps * kWave];
+    int32_t *map_start = reinterpret_cast<int32_t *>(&side_slices[0][0]);
+    int32_t *map_offset = map_start + kLanes;
+    int32_t *raw_encode = map_offset + kLanes;
+    const int t = threadIdx.x;
+    const int64_t block = blockIdx.x;
+    const int64_t row_base = block * S;
+    const int64_t logical_base = row_base * kLanes;
+    const uint32_t block_elems = static_cast<uint32_t>(S) * kLanes;
+    const int64_t remaining = logical_numel - logical_base;
+    const uint32_t valid = remaining < block_elems ? static_cast<uint32_t>(remaining) : block_elems;
+    UpdateIo io;
+    io.side = make_rsrc(a.side + logical_base, block_elems);
+    io.other = make_rsrc(other + logical_base, 2u * valid);
+    io.side_out = make_rsrc(side_out + logical_base, block_elems);
+    io.exponents = make_rsrc(exponents + logical_base, valid);
+    const SideChunk first = fetch_side_chunk(io.side, side_fetch_offset(), 0);
+
+    // The result's center from the sampler's partial sums.
+    raw_encode[t] = base_encode[t];
+    center_from_partials(partials, n_groups, &shared_center);
+    build_decode_tables(tb, a.shifted_decode, a.center[0]);
+    stage_payload(stage, a.encoded, n_blocks * kLanes, block, W);
+    __syncthreads();   // center and raw encode table
+    const int32_t center = shared_center;
+    enc[t] = repack_encode_entry(static_cast<uint32_t>(raw_encode[byte_to_index(t, center)]));
+    if (block == 0) {
+        if (t == 0) center_out[0] = center;
+        for (int i = t; i < 1024; i += kLanes)
+            shifted_decode_out[i] = shifted_decode_entry(base_decode[i], center);
+    }
+    __syncthreads();   // raw_encode is no longer read (it shares the maps' LDS)
+    const LaneOverlay lane = build_overlay(a.ov, a.has_overlay != 0, block, n_blocks, S, map_start,
+                                           map_offset, scratch, tail_lds, kTailLds);
+    const OpParams p = load_op_params(args.op, args.alpha_is_one, args.beta_is_one, args.alpha,
+                                      args.beta);
+    wait_memory();
+    __syncthreads();   // payload, tails and encode table visible; maps no longer read
+
+    StreamCursor cursor;
+    cursor.init(stage + t, &tb, static_cast<uint32_t>(W), rare);
+    const uint32_t row_bytes = static_cast<uint32_t>(n_blocks * kLanes * 4);
+    StreamWriter writer{make_rsrc(encoded_out + block * kLanes,
+                                  static_cast<uint32_t>(W - 1) * row_bytes + kLanes * 4),
+                        row_bytes, static_cast<uint32_t>(t) * 4u,
+                        static_cast<uint32_t>(W) * 32u, 0u, 0u, S};
+    uint8_t *slice = side_slices[t / kWave];
+    const bool full = valid == block_elems;
+    const int32_t form = form_of(args.op, args.alpha_is_one, args.beta_is_one);
+    if (S == 128)
+        update_block<128>(form, full, cursor, lane, tail_lds, slice, first, writer, enc, io,
+                          row_base, valid, p);
+    else
+        update_block<256>(form, full, cursor, lane, tail_lds, slice, first, writer, enc, io,
+                          row_base, valid, p);
+    writer.finish();
+    const bool overflow = writer.overflowed();
+    extra_starts[block * kLanes + t] = static_cast<uint8_t>(overflow ? writer.extra : 255);
+    const int32_t count = block_sum(overflow ? 1 : 0, scratch);
+    const int32_t bytes = block_sum(overflow ? S - writer.extra : 0, scratch);
+    if (t == 0) {
+        summaries[block] = count;
+        summaries[n_blocks + block] = bytes;
+    }
+}
+
+int32_t check_operand(const int32_t *encoded, const uint8_t *side, const int32_t *shifted_decode,
+                      const int32_t *center, const lct_overflow *overflow) {
+    if (!encoded || !side || !shifted_decode || !center) return LCT_E_NULL;
+    if (overflow != nullptr) {
+        if (!overflow->lanes || !overflow->starts || !overflow->tail || !overflow->blocks)
+            return LCT_E_NULL;
+        if (overflow->descriptor != nullptr && overflow->count == nullptr) return LCT_E_NULL;
+    }
+    return LCT_OK;
+}
+
+int32_t check_op(int32_t op, int32_t alpha_is_one, int32_t beta_is_one, const float *alpha,
+                 const float *beta) {
+    if (op < LCT_OP_ADD || op > LCT_OP_SCALAR_MUL_ADD) return LCT_E_ARG;
+    if (op == LCT_OP_SCALAR_MUL_ADD && ((!alpha_is_one && !alpha) || (!beta_is_one && !beta)))
+        return LCT_E_NULL;
+    return LCT_OK;
+}
+
+int32_t check_shape(int64_t size, int64_t logical_numel, const lct_geometry &g,
+                    int32_t rare_length) {
+    if (!geometry_ok(g)) return LCT_E_GEOMETRY;
+    if (logical_numel <= 0 || size <= 0 || size % g.block_symbols != 0 || logical_numel > size
+        || logical_numel <= size - g.block_symbols || size / g.block_symbols > kMaxBlocks)
+        return LCT_E_SIZE;
+    if (rare_length < 0 || rare_length > 8) return LCT_E_ARG;
+    return LCT_OK;
+}
+
+int32_t check_samples(int64_t sample_size, int64_t logical_numel) {
+    if (sample_size <= 0 || sample_size > kMaxSamples || sample_size > logical_numel)
+        return LCT_E_SIZE;
+    if (sample_size != logical_numel && (sample_size & (sample_size - 1)) != 0) return LCT_E_ARG;
+    return LCT_OK;
+}
+
+}  // namespace
+}  // namespace lct
+
+using namespace lct;
+
+extern "C" int32_t lct_pointwise_sample(const int32_t *encoded, const uint8_t *side,
+                                        const int32_t *shifted_decode, const int32_t *center,
+                                        const lct_overflow *overflow, const void *a_samples,
+                                        const void *other, const float *alpha,
+                                        const float *beta, int64_t size,
+                                        int64_t logical_numel, lct_geometry g,
+                                        int32_t rare_length, int32_t op, int32_t alpha_is_one,
+                                        int32_t beta_is_one, int64_t sample_size,
+                                        int32_t *partials, void *result_samples,
+                                        hipStream_t stream) {
+    if (int32_t e = check_operand(encoded, side, shifted_decode, center, overflow)) return e;
+    if (!other || !partials) return LCT_E_NULL;
+    if (int32_t e = check_op(op, alpha_is_one, beta_is_one, alpha, beta)) return e;
+    if (int32_t e = check_shape(size, logical_numel, g, rare_length)) return e;
+    if (int32_t e = check_samples(sample_size, logical_numel)) return e;
+    const OperandA a{encoded, side, shifted_decode, center,
+                     overflow ? *overflow : lct_overflow{}, overflow != nullptr};
+    const OpArgs args{alpha, beta, op, alpha_is_one, beta_is_one};
+    const int64_t n_blocks = size / g.block_symbols;
+    const size_t lds = static_cast<size_t>(g.fixed_words + 1) * kSampleGroup * sizeof(uint32_t);
+    hipLaunchKernelGGL(pointwise_sample_kernel, dim3(sample_groups(sample_size)),
+                       dim3(kSampleGroup), lds, stream, a,
+                       static_cast<const uint16_t *>(a_samples),
+                       static_cast<const uint16_t *>(other), args, n_blocks, logical_numel,
+                       sample_size, g.steps, g.fixed_words, rare_length, partials,
+                       static_cast<uint16_t *>(result_samples));
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_pointwise_encode(
+    const int32_t *encoded, const uint8_t *side, const int32_t *shifted_decode,
+    const int32_t *center, const lct_overflow *overflow, const void *other, const float *alpha,
+    const float *beta, const int32_t *partials, int64_t sample_size, const int32_t *base_encode,
+    const int32_t *base_decode, int32_t *center_out, int32_t *shifted_decode_out,
+    uint8_t *side_out, int32_t *encoded_out, uint8_t *extra_starts, int32_t *summaries,
+    uint8_t *exponents, int64_t size, int64_t logical_numel, lct_geometry g, int32_t rare_length,
+    int32_t op, int32_t alpha_is_one, int32_t beta_is_one, hipStream_t stream) {
+    if (int32_t e = check_operand(encoded, side, shifted_decode, center, overflow)) return e;
+    if (!other || !partials || !base_encode || !base_decode || !center_out || !shifted_decode_out
+        || !side_out || !encoded_out || !extra_starts || !summaries || !exponents)
+        return LCT_E_NULL;
+    if (int32_t e = check_op(op, alpha_is_one, beta_is_one, alpha, beta)) return e;
+    if (int32_t e = check_shape(size, logical_numel, g, rare_length)) return e;
+    if (int32_t e = check_samples(sample_size, logical_numel)) return e;
+    // 16-byte accesses: A's payload staging, A's and the result's side bytes.
+    if (((reinterpret_cast<uintptr_t>(encoded) | reinterpret_cast<uintptr_t>(side)
+          | reinterpret_cast<uintptr_t>(side_out)) & 15) != 0)
+        return LCT_E_ARG;
+    const int64_t n_blocks = size / g.block_symbols;
+    // The result's payload words are addressed with 32-bit buffer offsets.
+    if (static_cast<int64_t>(g.fixed_words) * n_blocks * kLanes * 4 >= (int64_t{1} << 31))
+        return LCT_E_SIZE;
+    const OperandA a{encoded, side, shifted_decode, center,
+                     overflow ? *overflow : lct_overflow{}, overflow != nullptr};
+    const OpArgs args{alpha, beta, op, alpha_is_one, beta_is_one};
+    const int32_t groups = sample_groups(sample_size);
+    const size_t lds = static_cast<size_t>(stage_bytes(g.fixed_words));
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&pointwise_encode_kernel),
+                                           lds))
+        return static_cast<int32_t>(e);
+    hipLaunchKernelGGL(pointwise_encode_kernel, dim3(static_cast<uint32_t>(n_blocks)),
+                       dim3(kLanes), lds, stream, a, static_cast<const uint16_t *>(other), args,
+                       partials, groups, base_encode, base_decode, center_out,
+                       shifted_decode_out, side_out, encoded_out, extra_starts, summaries,
+                       exponents, n_blocks, logical_numel, g.steps, g.fixed_words, rare_length);
+    return static_cast<int32_t>(hipGetLastError());
+}

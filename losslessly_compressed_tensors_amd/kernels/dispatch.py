@@ -90,6 +90,16 @@ def estimate_and_shift_encoding_table(source, center, size, encode_table, shifte
              _ptr(shifted_encode), _ptr(shifted_decode), _stream(source))
 
 
+def sample_center(source, logical_numel, sample_size, precomputed, partials,
+                  sample_values=None) -> None:
+    """Center samples spread over 64-sample workgroups: per-group exponent
+    sums and counts into ``partials`` (the sampling half of ``dispatch.py:33-48``);
+    the sampled BF16 values into ``sample_values`` when given."""
+    _require_device(source, partials)
+    hip.call("lct_sample_center", _ptr(source), int(bool(precomputed)), int(logical_numel),
+             int(sample_size), _ptr(partials), _ptr(sample_values), _stream(source))
+
+
 def shift_decoding_table(decode_table, center) -> torch.Tensor:
     """Return a center-shifted copy of ``decode_table`` (``dispatch.py:51-62``)."""
     _require_device(decode_table, center)
@@ -114,6 +124,20 @@ def encode_kernel(source, side, encoded, encode_table, extra_starts, summaries, 
              _ptr(extra_starts), _ptr(summaries) if write_summary else None, int(size),
              int(logical_numel), geometry, int(bool(precomputed)), int(bool(write_summary)),
              _stream(source))
+
+
+def encode_sampled(source, side, encoded, partials, sample_size, encode_table, decode_table,
+                   center, shifted_decode, extra_starts, summaries, size, *, precomputed,
+                   logical_numel, block_symbols, lanes, steps, fixed_words) -> None:
+    """The encoder with the table step folded in: the center and both shifted
+    tables come from ``sample_center``'s partials (``dispatch.py:33-48`` then
+    ``:294-316``)."""
+    _require_device(source, side, encoded, partials)
+    geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
+    hip.call("lct_encode_sampled", _ptr(source), _ptr(side), _ptr(encoded), _ptr(partials),
+             int(sample_size), _ptr(encode_table), _ptr(decode_table), _ptr(center),
+             _ptr(shifted_decode), _ptr(extra_starts), _ptr(summaries), int(size),
+             int(logical_numel), geometry, int(bool(precomputed)), 1, _stream(source))
 
 
 def prefix_allocate(summaries, counts, descriptor, buffer, blocks_out, blocks, buffered,
@@ -189,6 +213,47 @@ def dual_mapped(a_encoded, a_sign_mantissa, a_shifted_decode, a_center, a_storag
              b_ov if b_ov is None else hip.ctypes.byref(b_ov), _ptr(alpha), _ptr(output),
              _ptr(auxiliary), int(size), int(logical_numel), geometry, int(rare_length),
              int(output_policy), _stream(a_encoded))
+
+
+def pointwise_sample(encoded, sign_mantissa, shifted_decode, center, other, alpha, beta,
+                     partials, size, *, rare_length, logical_numel, block_symbols, lanes, steps,
+                     fixed_words, op, alpha_is_one, beta_is_one, sample_size,
+                     overflow: FallbackStorage | None = None, a_samples=None,
+                     result_samples=None) -> None:
+    """The operation's result at the center sample positions only: exponent
+    sum and count per group of 64 samples into ``partials``
+    (int32[2*ceil(sample_size/64)]).  ``a_samples``: A's recorded values at
+    those positions (then A's streams are not read); ``result_samples``
+    receives the result's."""
+    _require_device(encoded, sign_mantissa, other, partials)
+    geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
+    ov = overflow.as_overflow() if overflow is not None else None
+    hip.call("lct_pointwise_sample", _ptr(encoded), _ptr(sign_mantissa), _ptr(shifted_decode),
+             _ptr(center), ov if ov is None else hip.ctypes.byref(ov), _ptr(a_samples),
+             _ptr(other), _ptr(alpha), _ptr(beta), int(size), int(logical_numel), geometry,
+             int(rare_length), int(op), int(bool(alpha_is_one)), int(bool(beta_is_one)),
+             int(sample_size), _ptr(partials), _ptr(result_samples), _stream(encoded))
+
+
+def pointwise_encode(encoded, sign_mantissa, shifted_decode, center, other, alpha, beta,
+                     partials, base_encode, base_decode, center_out, shifted_decode_out,
+                     side_out, encoded_out, extra_starts, summaries, exponents, size, *,
+                     rare_length, logical_numel, block_symbols, lanes, steps, fixed_words, op,
+                     alpha_is_one, beta_is_one, sample_size,
+                     overflow: FallbackStorage | None = None) -> None:
+    """Decode + op + re-encode in one pass: the single-pass form of the
+    compressed-output ``pointwise_dense`` launch followed by the encoder
+    launch of ``encode_components(precomputed=True)``."""
+    _require_device(encoded, sign_mantissa, other, partials, encoded_out)
+    geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
+    ov = overflow.as_overflow() if overflow is not None else None
+    hip.call("lct_pointwise_encode", _ptr(encoded), _ptr(sign_mantissa), _ptr(shifted_decode),
+             _ptr(center), ov if ov is None else hip.ctypes.byref(ov), _ptr(other), _ptr(alpha),
+             _ptr(beta), _ptr(partials), int(sample_size), _ptr(base_encode), _ptr(base_decode),
+             _ptr(center_out), _ptr(shifted_decode_out), _ptr(side_out), _ptr(encoded_out),
+             _ptr(extra_starts), _ptr(summaries), _ptr(exponents), int(size),
+             int(logical_numel), geometry, int(rare_length), int(op), int(bool(alpha_is_one)),
+             int(bool(beta_is_one)), _stream(encoded))
 
 
 # ---------------------------------------------------------------------------

@@ -67,6 +67,16 @@ _SIGNATURES = {
     "lct_dual": [_ptr, _ptr, _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _ptr, _ptr,
                  ctypes.POINTER(Overflow), _ptr, _ptr, _ptr, _c_int64, _c_int64, Geometry,
                  _c_int32, _c_int32, _ptr],
+    "lct_pointwise_sample": [_ptr, _ptr, _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _ptr,
+                             _ptr, _c_int64, _c_int64, Geometry, _c_int32, _c_int32, _c_int32,
+                             _c_int32, _c_int64, _ptr, _ptr, _ptr],
+    "lct_sample_center": [_ptr, _c_int32, _c_int64, _c_int64, _ptr, _ptr, _ptr],
+    "lct_encode_sampled": [_ptr, _ptr, _ptr, _ptr, _c_int64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
+                           _c_int64, _c_int64, Geometry, _c_int32, _c_int32, _ptr],
+    "lct_pointwise_encode": [_ptr, _ptr, _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _ptr,
+                             _ptr, _c_int64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
+                             _c_int64, _c_int64, Geometry, _c_int32, _c_int32, _c_int32, _c_int32,
+                             _ptr],
     "lct_buffer_reset": [_ptr, _c_int32, _c_int32, _ptr],
     "lct_buffer_allocate": [_ptr, _c_int32, _ptr, _ptr, _c_int32, _ptr, _ptr],
     "lct_buffer_free": [_ptr, _c_int32, _ptr, _ptr, _ptr],

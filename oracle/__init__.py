@@ -173,6 +173,14 @@ def shift_tables(base_encode, base_decode, center: int):
     return enc, dec
 
 
+def sample_positions(n: int) -> np.ndarray:
+    """Logical positions of the center's min(n, 4096) samples."""
+    out = np.zeros(min(n, 4096), dtype=np.int64)
+    if n:
+        lib().lcto_sample_positions(ctypes.c_int64(n), ctypes.c_int64(out.size), _p(out))
+    return out
+
+
 def estimate_center(source: np.ndarray, precomputed: bool = False) -> int:
     n = source.size
     if n == 0:

@@ -46,16 +46,28 @@ static inline int32_t exponent_byte(int32_t value, int precomputed) {
 
 /* ---- center and shifted tables (LCT/kernels/common/tables.py) ---------- */
 
+/* tables.py:24-31: sample i lies in region [i*n/M, (i+1)*n/M) at a hashed
+ * offset. */
+static int64_t sample_position(int64_t i, int64_t logical_numel, int64_t sample_size) {
+    uint32_t hashed = (uint32_t)i * 0x9E3779B9u;
+    int64_t start = i * logical_numel / sample_size;
+    int64_t end = (i + 1) * logical_numel / sample_size;
+    uint64_t jitter = ((uint64_t)hashed * (uint64_t)(end - start)) >> 32;
+    return start + (int64_t)jitter;
+}
+
+void lcto_sample_positions(int64_t logical_numel, int64_t sample_size, int64_t *out) {
+    for (int64_t i = 0; i < sample_size; ++i)
+        out[i] = sample_position(i, logical_numel, sample_size);
+}
+
 int32_t lcto_estimate_center(const void *source, int64_t logical_numel,
                              int64_t sample_size, int precomputed) {
     /* tables.py:15-49: one jittered sample per region, exponent >= -120. */
     int64_t total = 0, kept = 0;
     for (int64_t i = 0; i < sample_size; ++i) {
-        uint32_t hashed = (uint32_t)i * 0x9E3779B9u;
-        int64_t start = i * logical_numel / sample_size;
-        int64_t end = (i + 1) * logical_numel / sample_size;
-        uint64_t jitter = ((uint64_t)hashed * (uint64_t)(end - start)) >> 32;
-        int32_t value = load_source(source, precomputed, start + (int64_t)jitter);
+        int32_t value = load_source(source, precomputed,
+                                    sample_position(i, logical_numel, sample_size));
         int32_t exp = exponent_byte(value, precomputed) - 127;
         if (exp >= -120) {
             total += exp;

@@ -28,6 +28,9 @@ typedef struct {
 
 /* Center of the sampled unbiased exponents (LCT/kernels/common/tables.py:9-49,
  * sample size min(n, 4096) from LCT/codec/encode.py:19,64). */
+/* Positions of the center's samples (tables.py:24-31), out[sample_size]. */
+void lcto_sample_positions(int64_t logical_numel, int64_t sample_size, int64_t *out);
+
 int32_t lcto_estimate_center(const void *source, int64_t logical_numel,
                              int64_t sample_size, int precomputed);
 

@@ -178,17 +178,25 @@ def test_memory_size_closed_form_c1(oracle_lib):
 # ---- center sampler -----------------------------------------------------------
 
 
-def _center_closed_form(exponents: np.ndarray) -> int:
-    """tables.py:15-49 restated: M = min(n, 4096) hashed positions, keep
-    exponents >= -120, mean rounded half away from zero, clamped."""
-    n = exponents.size
+def _positions_closed_form(n: int) -> list[int]:
+    """tables.py:24-31 restated: sample i of M = min(n, 4096) at a hashed
+    offset inside region [i*n/M, (i+1)*n/M)."""
     m = min(n, 4096)
-    total, count = 0, 0
+    out = []
     for i in range(m):
         start = i * n // m
         end = (i + 1) * n // m
         offset = ((i * 0x9E3779B9) & 0xFFFFFFFF) * (end - start) >> 32
-        e = int(exponents[start + offset])
+        out.append(start + offset)
+    return out
+
+
+def _center_closed_form(exponents: np.ndarray) -> int:
+    """tables.py:15-49 restated: M = min(n, 4096) hashed positions, keep
+    exponents >= -120, mean rounded half away from zero, clamped."""
+    total, count = 0, 0
+    for position in _positions_closed_form(exponents.size):
+        e = int(exponents[position])
         if e >= -120:
             total += e
             count += 1
@@ -209,6 +217,18 @@ def test_center_matches_closed_form(oracle_lib, n):
     assert oracle_lib.estimate_center(bits.view(np.int16)) == _center_closed_form(exponents)
     raw = ((bits.astype(np.int64) >> 7) & 0xFF).astype(np.uint8)
     assert oracle_lib.estimate_center(raw, precomputed=True) == _center_closed_form(exponents)
+
+
+@pytest.mark.parametrize("n", [1, 7, 4095, 4096, 4097, 65536 * 3 + 5, 45088768])
+def test_sample_positions_match_closed_form(oracle_lib, n):
+    """The positions the fused pointwise sampler is checked against: one per
+    region, strictly increasing, inside the tensor."""
+    positions = oracle_lib.sample_positions(n)
+    assert positions.tolist() == _positions_closed_form(n)
+    m = positions.size
+    regions = np.arange(m, dtype=np.int64)
+    assert np.all(positions >= regions * n // m)
+    assert np.all(positions < (regions + 1) * n // m)
 
 
 def test_center_special_cases(oracle_lib):
