@@ -8,8 +8,10 @@ alternate so the 256 MB Infinity Cache cannot serve repeats.
 
 Prints one JSON line: ``value`` is decompression throughput in GB/s of
 uncompressed BF16 (2n bytes / time), with compression throughput, the
-compression ratio, the decoder kernel's roofline fraction and a host-core
-CPU baseline (the C oracle, OpenMP over codec blocks) beside it.
+compression ratio, the decoder kernel's roofline fraction (``roofline``), the
+encoder kernel's (``encode_roofline``), the fused momentum update of config
+C4 with its single-pass kernel's roofline (``update``) and a host-core CPU
+baseline (the C oracle, OpenMP over codec blocks) beside them.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -54,18 +56,20 @@ def encode_bytes(ct) -> int:
     return 2 * ct.logical_numel + ct.size + nb * L * W * 4 + nb * L + tails + 2 * count + 12 * nb
 
 
-TRAFFIC_PROFILE = ROOT / "profiles" / "codec_kernels_NS_traffic.md"
+TRAFFIC_PROFILE = ROOT / "profiles" / "codec_kernels_NS_C4_traffic.md"
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of ``kernel`` from the committed rocprofv3
-    FETCH_SIZE/WRITE_SIZE summary (calibrated on a 256 MiB copy), or None."""
+def measured_traffic(kernel: str, workgroups: int):
+    """HBM bytes per launch of ``kernel`` at ``workgroups`` workgroups from the
+    committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary (calibrated on a 256 MiB
+    copy), or None."""
     try:
         for line in TRAFFIC_PROFILE.read_text().splitlines():
             fields = line.split()
-            if len(fields) == 3 and fields[0] == "traffic_bytes_per_launch" and fields[1] == kernel:
-                return int(fields[2])
-    except OSError:
+            if (len(fields) == 4 and fields[0] == "traffic_bytes_per_launch"
+                    and fields[1] == kernel and int(fields[2]) == workgroups):
+                return int(fields[3])
+    except (OSError, ValueError):
         pass
     return None
 
@@ -166,6 +170,43 @@ def time_update(args, torch, device):
     nb = ct.size // B
     n = ct.logical_numel
     minimum = 2 * (nb * L * W * 4 + ct.size) + 2 * n
+
+    # The single-pass kernel alone, launched back to back on the final
+    # momentum with outputs preallocated: reads A's payload and side bytes and
+    # B, writes the result's side bytes, payload, extra starts and summaries.
+    from losslessly_compressed_tensors_amd.codec.decode import overlay_of, shifted_decode_table
+    from losslessly_compressed_tensors_amd.compression.huffman_tables import (
+        get_distribution_tables,
+    )
+    from losslessly_compressed_tensors_amd.kernels import dispatch
+
+    base_encode, base_decode, rare = get_distribution_tables(dist, device)
+    sample_size = min(n, 4096)
+    launch = dict(rare_length=rare, logical_numel=n, block_symbols=B, lanes=L, steps=S,
+                  fixed_words=W, op=2, alpha_is_one=False, beta_is_one=True,
+                  sample_size=sample_size, overflow=overlay_of(ct))
+    table = shifted_decode_table(ct)
+    partials = torch.empty(2 * -(-sample_size // 64), dtype=torch.int32, device=device)
+    dispatch.pointwise_sample(ct.data, ct.sign_mantissa, table, ct.center, grads[0], alpha, None,
+                              partials, ct.size, a_samples=ct.sample_values, **launch)
+    outs = dict(center=torch.empty(1, dtype=torch.int32, device=device),
+                shifted=torch.empty(1024, dtype=torch.int32, device=device),
+                side=torch.empty(ct.size, dtype=torch.uint8, device=device),
+                encoded=torch.empty(nb * L * W + 4, dtype=torch.int32, device=device),
+                extra=torch.empty(nb * L, dtype=torch.uint8, device=device),
+                summaries=torch.empty(5 * nb + 1, dtype=torch.int32, device=device),
+                exponents=torch.empty(n, dtype=torch.uint8, device=device))
+
+    def launch_fused(i):
+        dispatch.pointwise_encode(ct.data, ct.sign_mantissa, table, ct.center, grads[i % 2],
+                                  alpha, None, partials, base_encode, base_decode, outs["center"],
+                                  outs["shifted"], outs["side"], outs["encoded"], outs["extra"],
+                                  outs["summaries"], outs["exponents"], ct.size, **launch)
+
+    for i in range(args.warmup):
+        launch_fused(i)
+    fused_ms = _kernel_ms(launch_fused, steps, torch)
+    fused_alg = minimum + nb * L + 8 * nb
     return {
         "workload": "C4: 4096x11008, EMPIRICAL CLEAN, LCTTensor.mul_add_(0.95, g), buffered",
         "steps": steps,
@@ -173,6 +214,14 @@ def time_update(args, torch, device):
         "gbps": round(2 * n / (ms * 1e-3) / 1e9, 2),
         "single_pass_bytes": minimum,
         "single_pass_hbm_frac": round(minimum / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "kernel_roofline": {
+            "kernel": "pointwise_encode_kernel",
+            "kernel_us": round(fused_ms * 1e3, 2),
+            "algorithmic_bytes": fused_alg,
+            "achieved": round(fused_alg / (fused_ms * 1e-3) / 1e9, 1),
+            "frac": round(fused_alg / (fused_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "traffic": measured_traffic("pointwise_encode_kernel", nb),
+        },
     }
 
 
@@ -256,6 +305,34 @@ def main() -> int:
                                   2, torch)
     enc_alg = encode_bytes(cts[0])
 
+    # Encoder kernel alone (field split + tables from the sampler's partials +
+    # payload), launched back to back into preallocated outputs.
+    encode_table, decode_table, _ = get_distribution_tables(dist, device)
+    nb = n // B
+    partials = []
+    for x in xs:
+        p = torch.empty(2 * 64, dtype=torch.int32, device=device)
+        dispatch.sample_center(x.view(-1).view(torch.int16), n, 4096, False, p)
+        partials.append(p)
+    enc_outs = dict(side=torch.empty(n, dtype=torch.uint8, device=device),
+                    encoded=torch.empty(nb * L * W + 4, dtype=torch.int32, device=device),
+                    center=torch.empty(1, dtype=torch.int32, device=device),
+                    shifted=torch.empty(1024, dtype=torch.int32, device=device),
+                    extra=torch.empty(nb * L, dtype=torch.uint8, device=device),
+                    summaries=torch.empty(5 * nb + 1, dtype=torch.int32, device=device))
+
+    def launch_encode(i):
+        dispatch.encode_sampled(xs[i % 2].view(-1).view(torch.int16), enc_outs["side"],
+                                enc_outs["encoded"], partials[i % 2], 4096, encode_table,
+                                decode_table, enc_outs["center"], enc_outs["shifted"],
+                                enc_outs["extra"], enc_outs["summaries"], n, precomputed=False,
+                                logical_numel=n, block_symbols=B, lanes=L, steps=S,
+                                fixed_words=W)
+
+    for i in range(args.warmup):
+        launch_encode(i)
+    encode_kernel_ms = _kernel_ms(launch_encode, args.steps, torch)
+
     _log("timing fused update (C4)")
     update = time_update(args, torch, device)
 
@@ -299,10 +376,18 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(dec_alg / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-            "traffic": measured_traffic("decode_kernel"),
+            "traffic": measured_traffic("decode_kernel", nb),
             "traffic_source": TRAFFIC_PROFILE.relative_to(ROOT).as_posix(),
             "algorithmic_bytes": dec_alg,
             "kernel_us": round(kernel_ms * 1e3, 2),
+        },
+        "encode_roofline": {
+            "kernel": "encode_kernel",
+            "kernel_us": round(encode_kernel_ms * 1e3, 2),
+            "algorithmic_bytes": enc_alg,
+            "achieved": round(enc_alg / (encode_kernel_ms * 1e-3) / 1e9, 1),
+            "frac": round(enc_alg / (encode_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "traffic": measured_traffic("encode_kernel", nb),
         },
     }
     result["update"] = update

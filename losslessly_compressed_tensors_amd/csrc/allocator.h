@@ -126,12 +126,34 @@ __device__ __forceinline__ void fetch_region(const RegionRegs &r, int32_t index,
     __syncthreads();
 }
 
+// An allocation in two halves, so a caller can take the lock and fetch the
+// free list before it knows the request size (the prefix scan overlaps this
+// latency with its own work).  allocator_begin returns whether the lock was
+// taken; allocator_finish must follow in every case.  Both contain barriers.
+struct AllocatorSnapshot {
+    RegionRegs r;
+    int32_t generation;
+    int32_t count;
+    bool locked;
+};
+
+__device__ __forceinline__ void allocator_begin(const AllocatorMeta &m, AllocatorSnapshot &snap,
+                                                int32_t *flag) {
+    snap.locked = allocator_lock(m.lock, flag);
+    snap.generation = 0;
+    snap.count = 0;
+    if (!snap.locked) return;
+    snap.generation = *m.generation;
+    snap.count = *m.count;
+    load_regions(m, snap.r);
+}
+
 // tensor_buffer.py:37-91.  `request` already includes item bytes.
-__device__ __forceinline__ void allocator_allocate(const AllocatorMeta &m, int32_t request,
-                                                   int32_t *descriptor, int32_t *scratch,
-                                                   int32_t *flag) {
+__device__ __forceinline__ void allocator_finish(const AllocatorMeta &m,
+                                                 const AllocatorSnapshot &snap, int32_t request,
+                                                 int32_t *descriptor, int32_t *scratch) {
     __shared__ int32_t shared2[2];
-    if (!allocator_lock(m.lock, flag)) {
+    if (!snap.locked) {
         if (threadIdx.x == 0) {
             descriptor[0] = -1;
             descriptor[1] = 0;
@@ -140,10 +162,8 @@ __device__ __forceinline__ void allocator_allocate(const AllocatorMeta &m, int32
         }
         return;
     }
-    const int32_t generation = *m.generation;
-    const int32_t count = *m.count;
-    RegionRegs r;
-    load_regions(m, r);
+    const RegionRegs &r = snap.r;
+    const int32_t count = snap.count;
     const int32_t size = ((request + kAlignment - 1) / kAlignment) * kAlignment;
     int32_t candidate = m.regions;
 #pragma unroll
@@ -166,9 +186,17 @@ __device__ __forceinline__ void allocator_allocate(const AllocatorMeta &m, int32
         descriptor[0] = success ? start : -1;
         descriptor[1] = success ? size : 0;
         descriptor[2] = request <= 0 ? kStatusEmpty : (success ? kStatusOk : kStatusNoFit);
-        descriptor[3] = generation;
+        descriptor[3] = snap.generation;
     }
     allocator_unlock(m.lock);
+}
+
+__device__ __forceinline__ void allocator_allocate(const AllocatorMeta &m, int32_t request,
+                                                   int32_t *descriptor, int32_t *scratch,
+                                                   int32_t *flag) {
+    AllocatorSnapshot snap;
+    allocator_begin(m, snap, flag);
+    allocator_finish(m, snap, request, descriptor, scratch);
 }
 
 // tensor_buffer.py:94-179.  Returns the status in every thread.

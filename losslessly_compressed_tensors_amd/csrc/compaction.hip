@@ -8,110 +8,166 @@
 // at entries [first, first+count), their exponent tails int8(e-127) for steps
 // start..S-1 concatenated from byte_base, and blocks[3*nb] = {count, first,
 // byte_base} so every reader walks the list one block at a time.
-#include <algorithm>
-
 #include "allocator.h"
 
 namespace lct {
 namespace {
 
-constexpr int kPrefixChunk = 8192;      // blocks per LDS pass: 3 x 8192 int32 of LDS
-constexpr int kCompactGrid = 2048;     // workgroups walking the overflow-block list
+constexpr int kPrefixPer = 16;                       // blocks per thread per pass
+constexpr int kPrefixPass = kPrefixPer * kLanes;     // 4096 blocks per pass
+constexpr int kCompactGrid = 2048;                   // workgroups walking the overflow-block list
+
+// Exclusive prefix sums of three values over the 256 threads of a block, with
+// their totals; one exchange through `scratch` (3 * kWavesPerBlock ints).
+// Contains barriers.
+__device__ __forceinline__ void block_exclusive_scan3(const int32_t (&v)[3], int32_t *scratch,
+                                                      int32_t (&before)[3],
+                                                      int32_t (&total)[3]) {
+    const int wave = threadIdx.x / kWave;
+    int32_t inclusive[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        inclusive[k] = wave_inclusive_scan(v[k]);
+        if (wave_lane() == kWave - 1) scratch[k * kWavesPerBlock + wave] = inclusive[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        int32_t prior = 0, sum = 0;
+#pragma unroll
+        for (int w = 0; w < kWavesPerBlock; ++w) {
+            const int32_t s = scratch[k * kWavesPerBlock + w];
+            prior += w < wave ? s : 0;
+            sum += s;
+        }
+        before[k] = prior + inclusive[k] - v[k];
+        total[k] = sum;
+    }
+    __syncthreads();
+}
 
 // summaries layout (int32[5*nb + 1]): per-block overflow counts | tail bytes |
 // exclusive count scan | exclusive byte scan | list of blocks with overflow |
 // list length.  The encoder writes the first two; this kernel the rest.
-// Blocks are scanned in chunks of kPrefixChunk with the running totals carried
-// from chunk to chunk, so any block count gives the same deterministic layout
-// (entries in block order, lanes ascending within a block).
+// Each pass covers 4096 blocks, 16 consecutive ones per thread, loaded and
+// stored as four 16-byte buffer accesses per array (blocks past the end read
+// as 0 and are not written); running totals carry from pass to pass, so any
+// block count gives the same deterministic layout (entries in block order,
+// lanes ascending within a block).  A buffered call takes the arena's lock and
+// reads its free list before scanning, so that latency overlaps the scan.
 __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     int32_t *__restrict__ summaries, int32_t *__restrict__ counts,
     int32_t *__restrict__ descriptor, int32_t *__restrict__ buffer_meta,
     int32_t *__restrict__ blocks, int32_t n_blocks, int32_t buffered,
     int32_t max_free_regions) {
-    // LDS per chunk: counts | tail bytes (then byte scan) | count scan.
-    extern __shared__ int32_t lds[];
-    const int chunk_cap = min(n_blocks, kPrefixChunk);
-    int32_t *c_lds = lds;
-    int32_t *v_lds = lds + chunk_cap;
-    int32_t *cp_lds = lds + 2 * chunk_cap;
-    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ int32_t scratch[3 * kWavesPerBlock];
     __shared__ int32_t flag;
     const int t = threadIdx.x;
-    int32_t *list = summaries + 4 * static_cast<int64_t>(n_blocks);
-    int32_t carry_count = 0, carry_bytes = 0, carry_listed = 0;
-    for (int base = 0; base < n_blocks; base += kPrefixChunk) {
-        const int m = min(kPrefixChunk, n_blocks - base);
-        // Coalesced loads into LDS, all issued before the first LDS write.
-        constexpr int kRows = kPrefixChunk / kLanes;
-        int32_t c_reg[kRows], v_reg[kRows];
+    const AllocatorMeta meta(buffer_meta, max_free_regions);
+    AllocatorSnapshot snap;
+    if (buffered) allocator_begin(meta, snap, &flag);
+
+    const int64_t nb = n_blocks;
+    const uint32_t bytes = static_cast<uint32_t>(n_blocks) * 4u;
+    const __amdgpu_buffer_rsrc_t count_in = make_rsrc(summaries, bytes);
+    const __amdgpu_buffer_rsrc_t bytes_in = make_rsrc(summaries + nb, bytes);
+    const __amdgpu_buffer_rsrc_t first_out = make_rsrc(summaries + 2 * nb, bytes);
+    const __amdgpu_buffer_rsrc_t base_out = make_rsrc(summaries + 3 * nb, bytes);
+    const __amdgpu_buffer_rsrc_t meta_count = make_rsrc(blocks, bytes);
+    const __amdgpu_buffer_rsrc_t meta_first = make_rsrc(blocks + nb, bytes);
+    const __amdgpu_buffer_rsrc_t meta_base = make_rsrc(blocks + 2 * nb, bytes);
+    int32_t *list = summaries + 4 * nb;
+    int32_t carry[3] = {0, 0, 0};   // entries, tail bytes, listed blocks
+    for (int base = 0; base < n_blocks; base += kPrefixPass) {
+        const int32_t first_block = base + t * kPrefixPer;
+        const uint32_t off = static_cast<uint32_t>(first_block) * 4u;
+        // A thread whose 16 blocks all exist moves them with 16-byte accesses;
+        // the one that straddles the end (and those past it) use 4-byte
+        // accesses, which the range check reads as 0 or drops one by one.
+        const bool whole = first_block + kPrefixPer <= n_blocks;
+        int32_t c[kPrefixPer], v[kPrefixPer];
+        if (whole) {
 #pragma unroll
-        for (int j = 0; j < kRows; ++j) {
-            const int b = j * kLanes + t;
-            c_reg[j] = b < m ? summaries[base + b] : 0;
-            v_reg[j] = b < m ? summaries[n_blocks + base + b] : 0;
-        }
+            for (int q = 0; q < kPrefixPer / 4; ++q) {
+                const auto cq = __builtin_amdgcn_raw_buffer_load_b128(count_in, off + 16 * q, 0, 0);
+                const auto vq = __builtin_amdgcn_raw_buffer_load_b128(bytes_in, off + 16 * q, 0, 0);
 #pragma unroll
-        for (int j = 0; j < kRows; ++j) {
-            const int b = j * kLanes + t;
-            if (b < m) {
-                c_lds[b] = c_reg[j];
-                v_lds[b] = v_reg[j];
+                for (int k = 0; k < 4; ++k) {
+                    c[4 * q + k] = static_cast<int32_t>(cq[k]);
+                    v[4 * q + k] = static_cast<int32_t>(vq[k]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < kPrefixPer; ++k) {
+                c[k] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(count_in, off + 4 * k, 0, 0));
+                v[k] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(bytes_in, off + 4 * k, 0, 0));
             }
         }
-        __syncthreads();
-        // Thread t scans the contiguous run [t*per, t*per + per) of the chunk.
-        const int per = (m + kLanes - 1) / kLanes;
-        const int begin = min(t * per, m);
-        const int end = min(begin + per, m);
-        int32_t run_count = 0, run_bytes = 0, run_listed = 0;
-        for (int b = begin; b < end; ++b) {
-            run_count += c_lds[b];
-            run_bytes += v_lds[b];
-            run_listed += c_lds[b] > 0 ? 1 : 0;
+        int32_t run[3] = {0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < kPrefixPer; ++k) {
+            run[0] += c[k];
+            run[1] += v[k];
+            run[2] += c[k] > 0 ? 1 : 0;
         }
-        int32_t chunk_count, chunk_bytes, chunk_listed;
-        int32_t count_before = carry_count + block_exclusive_scan(run_count, scratch, &chunk_count);
-        int32_t byte_before = carry_bytes + block_exclusive_scan(run_bytes, scratch, &chunk_bytes);
-        int32_t list_before =
-            carry_listed + block_exclusive_scan(run_listed, scratch, &chunk_listed);
-        for (int b = begin; b < end; ++b) {
-            const int32_t count = c_lds[b];
-            const int32_t bytes = v_lds[b];
-            cp_lds[b] = count_before;
-            v_lds[b] = byte_before;
-            if (count > 0) list[list_before++] = base + b;
-            count_before += count;
-            byte_before += bytes;
+        int32_t before[3], total[3];
+        block_exclusive_scan3(run, scratch, before, total);
+        int32_t count_before = carry[0] + before[0];
+        int32_t byte_before = carry[1] + before[1];
+        int32_t list_before = carry[2] + before[2];
+        int32_t firsts[kPrefixPer], bases[kPrefixPer];
+#pragma unroll
+        for (int k = 0; k < kPrefixPer; ++k) {
+            firsts[k] = count_before;
+            bases[k] = byte_before;
+            if (c[k] > 0) list[list_before++] = first_block + k;
+            count_before += c[k];
+            byte_before += v[k];
         }
-        __syncthreads();
-        // Coalesced stores of the scans and the block metadata.
-        for (int b = t; b < m; b += kLanes) {
-            const int32_t count = c_lds[b], first = cp_lds[b], byte_base = v_lds[b];
-            const int64_t k = static_cast<int64_t>(base) + b;
-            summaries[2 * static_cast<int64_t>(n_blocks) + k] = first;
-            summaries[3 * static_cast<int64_t>(n_blocks) + k] = byte_base;
-            blocks[k] = count;
-            blocks[n_blocks + k] = first;
-            blocks[2 * static_cast<int64_t>(n_blocks) + k] = byte_base;
+        if (!whole) {
+#pragma unroll
+            for (int k = 0; k < kPrefixPer; ++k) {
+                const uint32_t o = off + 4 * k;
+                __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(firsts[k]), first_out, o, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(bases[k]), base_out, o, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(c[k]), meta_count, o, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(firsts[k]), meta_first, o, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(bases[k]), meta_base, o, 0, 0);
+            }
         }
-        carry_count += chunk_count;
-        carry_bytes += chunk_bytes;
-        carry_listed += chunk_listed;
-        __syncthreads();   // the next chunk overwrites the LDS arrays
+#pragma unroll
+        for (int q = 0; whole && q < kPrefixPer / 4; ++q) {
+            using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
+            const u32x4 fq = {static_cast<uint32_t>(firsts[4 * q]),
+                              static_cast<uint32_t>(firsts[4 * q + 1]),
+                              static_cast<uint32_t>(firsts[4 * q + 2]),
+                              static_cast<uint32_t>(firsts[4 * q + 3])};
+            const u32x4 bq = {static_cast<uint32_t>(bases[4 * q]),
+                              static_cast<uint32_t>(bases[4 * q + 1]),
+                              static_cast<uint32_t>(bases[4 * q + 2]),
+                              static_cast<uint32_t>(bases[4 * q + 3])};
+            const u32x4 cq = {static_cast<uint32_t>(c[4 * q]), static_cast<uint32_t>(c[4 * q + 1]),
+                              static_cast<uint32_t>(c[4 * q + 2]),
+                              static_cast<uint32_t>(c[4 * q + 3])};
+            __builtin_amdgcn_raw_buffer_store_b128(fq, first_out, off + 16 * q, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(bq, base_out, off + 16 * q, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(cq, meta_count, off + 16 * q, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(fq, meta_first, off + 16 * q, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(bq, meta_base, off + 16 * q, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k) carry[k] += total[k];
     }
     if (t == 0) {
-        counts[0] = carry_count;
-        counts[1] = carry_bytes;
+        counts[0] = carry[0];
+        counts[1] = carry[1];
         counts[2] = 0;
         counts[3] = 0;
-        summaries[5 * static_cast<int64_t>(n_blocks)] = carry_listed;
+        summaries[5 * nb] = carry[2];
     }
-    if (buffered) {
-        // Two metadata bytes per overflowing stream: lane, then start step.
-        const AllocatorMeta meta(buffer_meta, max_free_regions);
-        allocator_allocate(meta, carry_bytes + 2 * carry_count, descriptor, scratch, &flag);
-    }
+    // Two metadata bytes per overflowing stream: lane, then start step.
+    if (buffered) allocator_finish(meta, snap, carry[1] + 2 * carry[0], descriptor, scratch);
 }
 
 // One codec block's overflow entries and tails (compaction.py:137-228).  The
@@ -211,12 +267,7 @@ extern "C" int32_t lct_prefix_allocate(int32_t *summaries, int32_t *counts,
     if (buffered && (max_free_regions <= 0 || max_free_regions > 4096
                      || (max_free_regions & (max_free_regions - 1)) != 0))
         return LCT_E_ARG;
-    const size_t lds = 3 * static_cast<size_t>(std::min<int64_t>(n_blocks, kPrefixChunk))
-        * sizeof(int32_t);
-    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(prefix_allocate_kernel),
-                                           lds))
-        return static_cast<int32_t>(e);
-    hipLaunchKernelGGL(prefix_allocate_kernel, dim3(1), dim3(kLanes), lds, stream, summaries,
+    hipLaunchKernelGGL(prefix_allocate_kernel, dim3(1), dim3(kLanes), 0, stream, summaries,
                        counts, descriptor, buffer_meta, blocks, static_cast<int32_t>(n_blocks),
                        buffered, max_free_regions);
     return static_cast<int32_t>(hipGetLastError());

@@ -29,18 +29,11 @@
 
 namespace lct {
 
-// Buffer resource word 3 for gfx9-family raw buffers.
-constexpr int32_t kBufferConfig = 0x00020000;
 // Cache policy of streamed output (written once): non-temporal.  Streamed
 // inputs keep the default policy, which measures faster for the decoder's
 // mix of 16-byte loads and 4-byte non-temporal stores on gfx950.
 constexpr int kStreaming = 2;
 constexpr int kChunkSteps = 16;   // steps per prefetched side-byte chunk
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes),
-                                             kBufferConfig);
-}
 
 struct DecodeTables {
     uint16_t entry[256];

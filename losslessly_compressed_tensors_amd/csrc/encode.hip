@@ -185,23 +185,6 @@ __device__ __forceinline__ void encode_block(
     extra_out = extra;
 }
 
-template <bool kFull, bool kPrecomputed>
-__device__ __forceinline__ void encode_dispatch(int S, __amdgpu_buffer_rsrc_t src,
-                                                __amdgpu_buffer_rsrc_t side, const uint32_t *table,
-                                                uint32_t *stage, uint8_t *in_slice,
-                                                uint8_t *side_slice, int64_t row_base,
-                                                uint32_t valid, int W, bool &overflow, int &extra) {
-    const InputChunk first = fetch_input<kFull, kPrecomputed>(
-        src, row_base, 0, valid * (kPrecomputed ? 1u : 2u));
-    __syncthreads();   // encode table and zeroed stage are visible
-    if (S == 128)
-        encode_block<kFull, kPrecomputed, 128>(src, side, table, stage, in_slice, side_slice,
-                                               row_base, valid, W, first, overflow, extra);
-    else
-        encode_block<kFull, kPrecomputed, 256>(src, side, table, stage, in_slice, side_slice,
-                                               row_base, valid, W, first, overflow, extra);
-}
-
 // Where the encoder's table comes from: the center-shifted encode table, or
 // the sampler's partial sums plus the distribution's base tables (the center
 // and shifted tables are then derived in every workgroup; workgroup 0 also
@@ -215,6 +198,52 @@ struct TableSource {
     int32_t *center_out;
     int32_t *shifted_decode_out;
 };
+
+// The workgroup's LDS encode table.  With sampler partials, wave 0 reduces
+// them to the center while the raw base table waits in `raw` (LDS the first
+// input chunk overwrites only later); workgroup 0 stores the center and the
+// shifted decode table.  Contains a barrier when sampled.
+__device__ __forceinline__ void setup_table(const TableSource &tables, uint32_t *table,
+                                            int32_t *raw, int32_t *shared_center,
+                                            int64_t block) {
+    const int t = threadIdx.x;
+    if (tables.partials == nullptr) {
+        table[t] = repack_encode_entry(static_cast<uint32_t>(tables.shifted_encode[t]));
+        return;
+    }
+    raw[t] = tables.base_encode[t];
+    center_from_partials(tables.partials, tables.n_groups, shared_center);
+    __syncthreads();
+    const int32_t center = *shared_center;
+    table[t] = repack_encode_entry(static_cast<uint32_t>(raw[byte_to_index(t, center)]));
+    if (block == 0) {
+        if (t == 0) tables.center_out[0] = center;
+        for (int i = t; i < 1024; i += kLanes)
+            tables.shifted_decode_out[i] = shifted_decode_entry(tables.base_decode[i], center);
+    }
+}
+
+template <bool kFull, bool kPrecomputed>
+__device__ __forceinline__ void encode_dispatch(int S, __amdgpu_buffer_rsrc_t src,
+                                                __amdgpu_buffer_rsrc_t side,
+                                                const TableSource &tables, uint32_t *table,
+                                                int32_t *raw, int32_t *shared_center,
+                                                int64_t block, uint32_t *stage,
+                                                uint8_t *in_slice, uint8_t *side_slice,
+                                                int64_t row_base, uint32_t valid, int W,
+                                                bool &overflow, int &extra) {
+    // The first chunk is in flight while the table is set up.
+    const InputChunk first = fetch_input<kFull, kPrecomputed>(
+        src, row_base, 0, valid * (kPrecomputed ? 1u : 2u));
+    setup_table(tables, table, raw, shared_center, block);
+    __syncthreads();   // encode table and zeroed stage are visible
+    if (S == 128)
+        encode_block<kFull, kPrecomputed, 128>(src, side, table, stage, in_slice, side_slice,
+                                               row_base, valid, W, first, overflow, extra);
+    else
+        encode_block<kFull, kPrecomputed, 256>(src, side, table, stage, in_slice, side_slice,
+                                               row_base, valid, W, first, overflow, extra);
+}
 
 __global__ __launch_bounds__(kLanes) void encode_kernel(
     const void *__restrict__ source, uint8_t *__restrict__ side,
@@ -242,38 +271,26 @@ __global__ __launch_bounds__(kLanes) void encode_kernel(
     const __amdgpu_buffer_rsrc_t side_rsrc = make_rsrc(side + logical_base, block_elems);
 
     for (int i = t; i < (W + 1) * kLanes; i += kLanes) stage[i] = 0u;
-    if (tables.partials != nullptr) {
-        // The raw base table waits in the input slices, which the first
-        // chunk overwrites only after encode_dispatch's barrier.
-        int32_t *raw = reinterpret_cast<int32_t *>(&in_slices[0][0]);
-        raw[t] = tables.base_encode[t];
-        center_from_partials(tables.partials, tables.n_groups, &shared_center);
-        __syncthreads();
-        const int32_t center = shared_center;
-        table[t] = repack_encode_entry(static_cast<uint32_t>(raw[byte_to_index(t, center)]));
-        if (block == 0) {
-            if (t == 0) tables.center_out[0] = center;
-            for (int i = t; i < 1024; i += kLanes)
-                tables.shifted_decode_out[i] = shifted_decode_entry(tables.base_decode[i], center);
-        }
-    } else {
-        table[t] = repack_encode_entry(static_cast<uint32_t>(tables.shifted_encode[t]));
-    }
+    int32_t *raw = reinterpret_cast<int32_t *>(&in_slices[0][0]);
 
     uint8_t *in_slice = in_slices[t / kWave];
     uint8_t *side_slice = side_slices[t / kWave];
     bool overflow;
     int extra;
     if (precomputed) {
-        if (full) encode_dispatch<true, true>(S, src_rsrc, side_rsrc, table, stage, in_slice,
-                                              side_slice, row_base, valid, W, overflow, extra);
-        else encode_dispatch<false, true>(S, src_rsrc, side_rsrc, table, stage, in_slice,
-                                          side_slice, row_base, valid, W, overflow, extra);
+        if (full) encode_dispatch<true, true>(S, src_rsrc, side_rsrc, tables, table, raw,
+                                              &shared_center, block, stage, in_slice, side_slice,
+                                              row_base, valid, W, overflow, extra);
+        else encode_dispatch<false, true>(S, src_rsrc, side_rsrc, tables, table, raw,
+                                          &shared_center, block, stage, in_slice, side_slice,
+                                          row_base, valid, W, overflow, extra);
     } else {
-        if (full) encode_dispatch<true, false>(S, src_rsrc, side_rsrc, table, stage, in_slice,
+        if (full) encode_dispatch<true, false>(S, src_rsrc, side_rsrc, tables, table, raw,
+                                               &shared_center, block, stage, in_slice,
                                                side_slice, row_base, valid, W, overflow, extra);
-        else encode_dispatch<false, false>(S, src_rsrc, side_rsrc, table, stage, in_slice,
-                                           side_slice, row_base, valid, W, overflow, extra);
+        else encode_dispatch<false, false>(S, src_rsrc, side_rsrc, tables, table, raw,
+                                           &shared_center, block, stage, in_slice, side_slice,
+                                           row_base, valid, W, overflow, extra);
     }
 
     const int64_t n_streams = n_blocks * kLanes;

@@ -23,6 +23,16 @@ constexpr int kWavesPerBlock = kLanes / kWave;
 constexpr int kMaxWords = 64;   // largest fixed payload per stream accepted
 constexpr int kEscapeLength = 31;  // decode-table length field marking an escape
 
+// Buffer resource word 3 for gfx9-family raw buffers.
+constexpr int32_t kBufferConfig = 0x00020000;
+
+// A raw buffer resource over `bytes` bytes from `base`: accesses are 32-bit
+// offsets from an SGPR base, and those at or past `bytes` read 0 / are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes),
+                                             kBufferConfig);
+}
+
 // Unbiased exponent of Huffman table index `symbol` under `center`
 // (tables.py:109-116, primitives.py:29-35).
 __device__ __forceinline__ int32_t index_to_exponent(int32_t symbol, int32_t center) {
