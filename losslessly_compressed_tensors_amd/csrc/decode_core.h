@@ -29,9 +29,9 @@
 
 namespace lct {
 
-// Cache policy of streamed output (written once): non-temporal.  Streamed
-// inputs keep the default policy, which measures faster for the decoder's
-// mix of 16-byte loads and 4-byte non-temporal stores on gfx950.
+// Cache policy of data touched once: non-temporal.  The decoder uses it for
+// its payload staging and output stores; its side-byte loads keep the default
+// policy (non-temporal there measures slower in combination on gfx950).
 constexpr int kStreaming = 2;
 constexpr int kChunkSteps = 16;   // steps per prefetched side-byte chunk
 
@@ -63,7 +63,9 @@ __device__ __forceinline__ void build_decode_tables(DecodeTables &tb,
 // row W that a window starting in row W-1 reads as its high word.  A payload
 // row of a block is 1 KiB contiguous in HBM; each row moves with one direct
 // global-to-LDS load per wave (64 lanes x 16 bytes), so staging takes no
-// registers.  The caller waits (vmcnt(0)) and synchronises before reading.
+// registers.  The loads are non-temporal (each payload word is read once):
+// on gfx950 that takes the decoder from 88.5 to 81.8 us at 4096 blocks.  The
+// caller waits (vmcnt(0)) and synchronises before reading.
 __device__ __forceinline__ void stage_payload(uint32_t *stage, const int32_t *__restrict__ encoded,
                                               int64_t n_streams, int64_t block, int W) {
     const int t = threadIdx.x;
@@ -73,7 +75,7 @@ __device__ __forceinline__ void stage_payload(uint32_t *stage, const int32_t *__
         const int32_t *src = encoded + row * n_streams + block * kLanes + j * 4;
         __builtin_amdgcn_global_load_lds(
             src, (__attribute__((address_space(3))) void *)(stage + row * kLanes),
-            16, 0, 0);
+            16, 0, kStreaming);
     }
     stage[W * kLanes + t] = 0u;
 }
