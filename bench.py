@@ -10,8 +10,10 @@ Prints one JSON line: ``value`` is decompression throughput in GB/s of
 uncompressed BF16 (2n bytes / time), with compression throughput, the
 compression ratio, the decoder kernel's roofline fraction (``roofline``), the
 encoder kernel's (``encode_roofline``), the fused momentum update of config
-C4 with its single-pass kernel's roofline (``update``) and a host-core CPU
-baseline (the C oracle, OpenMP over codec blocks) beside them.
+C4 with its single-pass kernel's roofline (``update``), the weight step of
+compressed SGD-momentum with its single-pass kernel's roofline
+(``weight_update``) and a host-core CPU baseline (the C oracle, OpenMP over
+codec blocks) beside them.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -225,6 +227,89 @@ def time_update(args, torch, device):
     }
 
 
+def time_weight_update(args, torch, device):
+    """The weight half of the compressed SGD-momentum step
+    (LCT/components/sparse_utils.py:52-54): p <- p + (-lr) * m with both the
+    weight p and the momentum m compressed, at config C4's shape 4096x11008.
+    p ~ N(0, 0.02^2) seed 5 under the reference's weight distribution (LAPLACE
+    CLEAN), m ~ N(0, 1e-2^2) seed 100 under its momentum distribution
+    (EMPIRICAL CLEAN, zero_prob 0.02), both buffer-backed; lr = 0.01.  Reports
+    the step time and the single-pass kernel's roofline (reads both operands'
+    payload and side bytes, writes the result's)."""
+    from losslessly_compressed_tensors_amd.codec.decode import overlay_of, shifted_decode_table
+    from losslessly_compressed_tensors_amd.comp_format import DistType, Distribution
+    from losslessly_compressed_tensors_amd.compression.huffman_tables import (
+        get_distribution_tables,
+    )
+    from losslessly_compressed_tensors_amd.kernels import dispatch
+    from losslessly_compressed_tensors_amd.LCTensor import LCTTensor
+    from losslessly_compressed_tensors_amd.tensor_buffer import TensorBuffer
+
+    shape = (4096, 11008)
+    gen = torch.Generator().manual_seed(5)
+    p0 = (torch.randn(*shape, generator=gen) * 0.02).to(torch.bfloat16).to(device)
+    gen = torch.Generator().manual_seed(100)
+    m0 = (torch.randn(*shape, generator=gen) * 1e-2).to(torch.bfloat16).to(device)
+    weight_dist = Distribution(DistType.LAPLACE)
+    momentum_dist = Distribution(DistType.EMPIRICAL, zero_prob=0.02)
+    buffer = TensorBuffer(96 << 20, device=device)
+    weight = LCTTensor(p0, buffer, weight_dist)
+    momentum = LCTTensor(m0, buffer, momentum_dist)
+    neg_lr = torch.tensor([-0.01], dtype=torch.float32, device=device)
+    steps = max(10, args.steps // 2)
+    ms = _time_events(lambda i: weight.add_comp_(momentum, neg_lr), steps, args.warmup, torch)
+
+    a, b = momentum.x, weight.x
+    B, L, S, W = b.codec_geometry
+    nb = b.size // B
+    n = b.logical_numel
+    base_encode, base_decode, rare = get_distribution_tables(weight_dist, device)
+    sample_size = min(n, 4096)
+    launch = dict(rare_length=rare, logical_numel=n, block_symbols=B, lanes=L, steps=S,
+                  fixed_words=W, sample_size=sample_size)
+    tables = shifted_decode_table(a), shifted_decode_table(b)
+    storages = overlay_of(a), overlay_of(b)
+    partials = torch.empty(2 * -(-sample_size // 64), dtype=torch.int32, device=device)
+    dispatch.dual_sample(a.data, a.sign_mantissa, tables[0], a.center, storages[0], b.data,
+                         b.sign_mantissa, tables[1], b.center, storages[1], neg_lr, partials,
+                         b.size, a_samples=a.sample_values, b_samples=b.sample_values, **launch)
+    outs = dict(center=torch.empty(1, dtype=torch.int32, device=device),
+                shifted=torch.empty(1024, dtype=torch.int32, device=device),
+                side=torch.empty(b.size, dtype=torch.uint8, device=device),
+                encoded=torch.empty(nb * L * W + 4, dtype=torch.int32, device=device),
+                extra=torch.empty(nb * L, dtype=torch.uint8, device=device),
+                summaries=torch.empty(5 * nb + 1, dtype=torch.int32, device=device),
+                exponents=torch.empty(n, dtype=torch.uint8, device=device))
+
+    def launch_fused(i):
+        dispatch.dual_encode(a.data, a.sign_mantissa, tables[0], a.center, storages[0], b.data,
+                             b.sign_mantissa, tables[1], b.center, storages[1], neg_lr, partials,
+                             base_encode, base_decode, outs["center"], outs["shifted"],
+                             outs["side"], outs["encoded"], outs["extra"], outs["summaries"],
+                             outs["exponents"], b.size, **launch)
+
+    for i in range(args.warmup):
+        launch_fused(i)
+    fused_ms = _kernel_ms(launch_fused, steps, torch)
+    stream_bytes = nb * L * W * 4 + b.size
+    fused_alg = 3 * stream_bytes + nb * L + 8 * nb
+    return {
+        "workload": "SGD-momentum weight step at C4's shape: 4096x11008, weight LAPLACE CLEAN, "
+                    "momentum EMPIRICAL CLEAN, LCTTensor.add_comp_(m, -0.01), buffered",
+        "steps": steps,
+        "ms_per_step": round(ms, 5),
+        "gbps": round(2 * n / (ms * 1e-3) / 1e9, 2),
+        "kernel_roofline": {
+            "kernel": "dual_encode_kernel",
+            "kernel_us": round(fused_ms * 1e3, 2),
+            "algorithmic_bytes": fused_alg,
+            "achieved": round(fused_alg / (fused_ms * 1e-3) / 1e9, 1),
+            "frac": round(fused_alg / (fused_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "traffic": measured_traffic("dual_encode_kernel", nb),
+        },
+    }
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -335,6 +420,8 @@ def main() -> int:
 
     _log("timing fused update (C4)")
     update = time_update(args, torch, device)
+    _log("timing fused weight update")
+    weight_update = time_weight_update(args, torch, device)
 
     # Reference traffic for counter calibration: a plain 256 MiB device copy
     # (reads and writes exactly 2n bytes each).
@@ -391,6 +478,7 @@ def main() -> int:
         },
     }
     result["update"] = update
+    result["weight_update"] = weight_update
     if not args.skip_cpu:
         _log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(host_inputs[0], dist, args.cpu_seconds)

@@ -266,6 +266,43 @@ int32_t lct_pointwise_encode(const int32_t *encoded, const uint8_t *side,
                              int32_t alpha_is_one, int32_t beta_is_one,
                              hipStream_t stream);
 
+/* ---- single-pass compressed-output alpha*A + B over two compressed
+ * operands, step 1 of 2: replaces the center estimate that dispatch.py:33-48
+ * makes over the exponent bytes written by dispatch.py:215-286 (dual_mapped,
+ * COMPRESSED_OUTPUT), as LCT/codec/pointwise.py:159-210 sequences them for
+ * LCT/LCTensor.py:91-99 (add_comp_).  As lct_pointwise_sample, with the
+ * result fma(a, alpha[0], b) rounded to BF16: A and B as for lct_dual;
+ * a_samples / b_samples: NULL, or that operand's values at the sample
+ * positions (then its streams are not read). */
+int32_t lct_dual_sample(const int32_t *a_encoded, const uint8_t *a_side,
+                        const int32_t *a_shifted_decode, const int32_t *a_center,
+                        const lct_overflow *a_overflow, const void *a_samples,
+                        const int32_t *b_encoded, const uint8_t *b_side,
+                        const int32_t *b_shifted_decode, const int32_t *b_center,
+                        const lct_overflow *b_overflow, const void *b_samples,
+                        const float *alpha, int64_t size, int64_t logical_numel,
+                        lct_geometry geometry, int32_t rare_length, int64_t sample_size,
+                        int32_t *partials, void *result_samples, hipStream_t stream);
+
+/* ---- single-pass compressed-output alpha*A + B over two compressed
+ * operands, step 2 of 2: replaces dispatch.py:215-286 (dual_mapped,
+ * COMPRESSED_OUTPUT) followed by the table shift of dispatch.py:16-30 and
+ * dispatch.py:294-316 (encode_kernel, precomputed) in one pass.  Outputs as
+ * lct_pointwise_encode; partials from lct_dual_sample with the same
+ * sample_size.  a_encoded, b_encoded, a_side, b_side and side_out must be
+ * 16-byte aligned. */
+int32_t lct_dual_encode(const int32_t *a_encoded, const uint8_t *a_side,
+                        const int32_t *a_shifted_decode, const int32_t *a_center,
+                        const lct_overflow *a_overflow, const int32_t *b_encoded,
+                        const uint8_t *b_side, const int32_t *b_shifted_decode,
+                        const int32_t *b_center, const lct_overflow *b_overflow,
+                        const float *alpha, const int32_t *partials, int64_t sample_size,
+                        const int32_t *base_encode, const int32_t *base_decode,
+                        int32_t *center_out, int32_t *shifted_decode_out, uint8_t *side_out,
+                        int32_t *encoded_out, uint8_t *extra_starts, int32_t *summaries,
+                        uint8_t *exponents, int64_t size, int64_t logical_numel,
+                        lct_geometry geometry, int32_t rare_length, hipStream_t stream);
+
 /* ---- TensorBuffer allocator kernels: replace LCT/tensor_buffer.py:130-136
  * (_reset_kernel launch), :93-120 (_allocate_kernel launches) and
  * LCT/kernels/tensor_buffer_ops.py:5-15 (_free_storage_kernel launch).

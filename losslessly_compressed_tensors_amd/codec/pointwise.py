@@ -11,9 +11,8 @@ Host logic of ``LCT/codec/pointwise.py:28-304``:
 Dense output is BF16.  Compressed output equals ``compress(result)`` with a
 freshly sampled center.  With a dense operand it is produced in a single pass
 over the compressed operand (decode, operate, re-encode; see
-``_fused_compressed_output``); the two-compressed form re-encodes the fused
-kernel's split components (side bytes in storage order + exponent bytes in
-logical order), as the reference does for both.
+``_fused_compressed_output``), and so with two compressed operands
+(``_fused_dual_compressed_output``).
 """
 from __future__ import annotations
 
@@ -155,6 +154,66 @@ def _fused_compressed_output(data: CompressedTensor, other: torch.Tensor,
                          sample_values=result_samples)
 
 
+def _fused_dual_compressed_output(data: CompressedTensor, other: CompressedTensor,
+                                  alpha: torch.Tensor, result_distribution: Distribution,
+                                  buffer: TensorBuffer | None) -> CompressedTensor:
+    """``alpha * compA + compB`` re-encoded in one pass over both operands'
+    payloads and side bytes.
+
+    The reference runs the dual kernel with compressed output and encodes its
+    side and exponent bytes (``LCT/codec/pointwise.py:191-202`` ->
+    ``LCT/codec/encode.py:22-186``).  Here ``lct_dual_sample`` computes the
+    result at the center's sample positions (from an operand's recorded
+    sample values when it has them, else by decoding the sampled streams'
+    prefixes) and ``lct_dual_encode`` decodes both operands, applies
+    ``fma(a, alpha, b)`` and encodes the result as it is computed.  The stored
+    tensor is identical.
+    """
+    device = data.data.device
+    _, _, rare_a = get_distribution_tables(data.distribution, device)
+    _, _, rare_b = get_distribution_tables(other.distribution, device)
+    if rare_a != rare_b:
+        raise ValueError("two-compressed path requires matching RARE_LENGTH")
+    base_encode, base_decode, _ = get_distribution_tables(result_distribution, device)
+    block_symbols, lanes, steps, fixed_words = data.codec_geometry
+    blocks = data.size // block_symbols
+    streams = blocks * lanes
+    n = data.logical_numel
+    sample_size = min(n, CENTER_SAMPLE_SIZE)
+    launch = dict(rare_length=rare_a, logical_numel=n, block_symbols=block_symbols, lanes=lanes,
+                  steps=steps, fixed_words=fixed_words, sample_size=sample_size)
+    a_table, b_table = shifted_decode_table(data), shifted_decode_table(other)
+    a_storage, b_storage = overlay_of(data), overlay_of(other)
+
+    def recorded(tensor: CompressedTensor):
+        values = tensor.sample_values
+        return values if values is not None and values.numel() == sample_size else None
+
+    partials = torch.empty(2 * -(-sample_size // 64), dtype=torch.int32, device=device)
+    result_samples = torch.empty(sample_size, dtype=torch.int16, device=device)
+    dispatch.dual_sample(data.data, data.sign_mantissa, a_table, data.center, a_storage,
+                         other.data, other.sign_mantissa, b_table, other.center, b_storage,
+                         alpha, partials, data.size, a_samples=recorded(data),
+                         b_samples=recorded(other), result_samples=result_samples, **launch)
+    center = torch.empty(1, dtype=torch.int32, device=device)
+    shifted_decode = torch.empty(1024, dtype=torch.int32, device=device)
+    side = torch.empty(data.size, dtype=torch.uint8, device=device)
+    encoded = torch.empty(streams * fixed_words + 4, dtype=torch.int32, device=device)
+    extra_starts = torch.empty(streams, dtype=torch.uint8, device=device)
+    summaries = torch.empty(5 * blocks + 1, dtype=torch.int32, device=device)
+    # Only the rows of overflowing streams are written (and read back by the
+    # compaction); the rest stays unwritten.
+    exponents = torch.empty(n, dtype=torch.uint8, device=device)
+    dispatch.dual_encode(data.data, data.sign_mantissa, a_table, data.center, a_storage,
+                         other.data, other.sign_mantissa, b_table, other.center, b_storage,
+                         alpha, partials, base_encode, base_decode, center, shifted_decode,
+                         side, encoded, extra_starts, summaries, exponents, data.size, **launch)
+    return finish_encode(exponents, side, encoded, extra_starts, summaries, data.size,
+                         result_distribution, buffer, data.shape, precomputed=True,
+                         center=center, shifted_decode=shifted_decode, logical_numel=n,
+                         sample_values=result_samples)
+
+
 def _launch_scalar_mul_add_compressed_compressed(data: CompressedTensor,
                                                  other: CompressedTensor,
                                                  alpha: torch.Tensor, policy: int):
@@ -189,9 +248,18 @@ def pointwise_scale_add_compressed(data: CompressedTensor, other: CompressedTens
         "pointwise_scale_add_compressed requires both inputs to be buffer-backed "
         "or both to be non-buffer-backed")
     if same_layout and data.codec_geometry == other.codec_geometry:
+        # Both operands' streams are walked with A's size (the reference reads B
+        # out of bounds otherwise).
+        if data.shape != other.shape:
+            raise ValueError(f"{SCALAR_MUL_ADD.name} expects tensors with the same shape")
         result_distribution = distribution or data.distribution
         if not dense_output and geometry(result_distribution) != data.codec_geometry:
             raise ValueError("matrix compressed output must preserve the input stream geometry")
+        if not dense_output and data.logical_numel > 0:
+            if buffer is not None and buffer.capacity_bytes % 4:
+                raise ValueError("TensorBuffer capacity must be divisible by 4")
+            return _fused_dual_compressed_output(data, other, alpha, result_distribution,
+                                                 buffer)
         policy = DENSE_OUTPUT if dense_output else COMPRESSED_OUTPUT
         values, auxiliary = _launch_scalar_mul_add_compressed_compressed(
             data, other, alpha, policy)

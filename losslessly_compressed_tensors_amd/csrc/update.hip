@@ -508,6 +508,293 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     }
 }
 
+// ---- the two-compressed form: alpha * A + B with compressed output
+//
+// The reference's weight update (LCT/LCTensor.py:91-99 -> codec/pointwise.py:
+// 159-210 with dense_output=False) runs the dual kernel with
+// COMPRESSED_OUTPUT (LCT/kernels/generic/pointwise_scalar_dual.py:17-346) and
+// re-encodes its components.  As for one compressed operand, the sampler
+// computes the result at the sample positions and the encode kernel decodes
+// both operands, applies fma(a, alpha, b) (pointwise_scalar_dual.py:226) and
+// encodes the result in one pass.
+
+// One compressed operand of the sampler whose value at the sample has to be
+// decoded from its stream: the state between issuing its loads and walking.
+struct SampleWalk {
+    int32_t start;        // first overflow step of the sampled stream, S if none
+    int64_t tail_index;   // its tail's first byte
+    uint32_t sm;          // side byte at the sample
+};
+
+// Stage the sampled stream's W words into this thread's LDS column of
+// `words`, read the side byte and the stream's overflow entry.
+__device__ __forceinline__ void sample_issue(const OperandA &x, bool active, int64_t row,
+                                             int32_t lane, int64_t block, int64_t n_blocks,
+                                             int S, int W, uint32_t *words, SampleWalk &w) {
+    const int t = threadIdx.x;
+    const int64_t n_streams = n_blocks * kLanes;
+    const int32_t *column = x.encoded + (active ? block * kLanes + lane : 0);
+    for (int r = 0; r < W; ++r)
+        __builtin_amdgcn_global_load_lds(
+            column + r * n_streams,
+            (__attribute__((address_space(3))) void *)(words + r * kSampleGroup), 4, 0, 0);
+    words[W * kSampleGroup + t] = 0u;
+    w.sm = active ? x.side[row * kLanes + lane] : 0u;
+    stream_overlay(x.ov, active && x.has_overlay != 0, block, n_blocks, lane, S, w.start,
+                   w.tail_index);
+}
+
+// The operand's BF16 bits at the sample (after the staged words and tables
+// are visible): the tail byte at or after the stream's overflow start, else
+// the decoded prefix's last symbol.
+__device__ __forceinline__ uint32_t sample_walk(const OperandA &x, const SampleWalk &w,
+                                                bool active, int32_t step, uint32_t *words,
+                                                const DecodeTables *tb, int W, int rare) {
+    uint32_t field = 0;
+    if (step >= w.start) {
+        field = tail_field(x.ov.tail[w.tail_index + (step - w.start)]);
+    } else if (active) {
+        StreamCursorT<kSampleGroup> cursor;
+        cursor.init(words + threadIdx.x, tb, static_cast<uint32_t>(W), rare);
+        for (int pair = 0; pair < step / 2; ++pair) {
+            uint32_t f0, f1;
+            cursor.advance(cursor.next_fields(f0, f1));
+        }
+        uint32_t f0, f1;
+        cursor.next_fields(f0, f1);
+        field = (step & 1) ? f1 : f0;
+    }
+    return join_entry(field, w.sm);
+}
+
+__global__ __launch_bounds__(kSampleGroup) void dual_sample_kernel(
+    OperandA a, const uint16_t *__restrict__ a_samples, OperandA b,
+    const uint16_t *__restrict__ b_samples, const float *__restrict__ alpha, int64_t n_blocks,
+    int64_t logical_numel, int64_t sample_size, int S, int W, int rare,
+    int32_t *__restrict__ partials, uint16_t *__restrict__ result_samples) {
+    extern __shared__ uint32_t words[];   // A's then B's: 2 x (W + 1) rows x kSampleGroup
+    __shared__ DecodeTables tba, tbb;
+    const int t = threadIdx.x;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kSampleGroup + t;
+    const bool active = i < sample_size;
+    const int shift = __builtin_ctzll(static_cast<uint64_t>(sample_size));
+    const int64_t pos = active ? sample_position(i, logical_numel, sample_size, shift) : 0;
+    const int64_t row = pos / kLanes;
+    const int32_t lane = static_cast<int32_t>((pos % kLanes) ^ (row & 254));
+    const int64_t block = row >> (S == 128 ? 7 : 8);   // S is 128 or 256
+    const int32_t step = static_cast<int32_t>(row & (S - 1));
+    const bool walk_a = a_samples == nullptr, walk_b = b_samples == nullptr;
+    uint32_t *words_a = words, *words_b = words + (W + 1) * kSampleGroup;
+    SampleWalk wa{}, wb{};
+    if (walk_a) {
+        int32_t packed[256 / kSampleGroup];
+#pragma unroll
+        for (int k = 0; k < 256 / kSampleGroup; ++k)
+            packed[k] = a.shifted_decode[t + k * kSampleGroup];
+        sample_issue(a, active, row, lane, block, n_blocks, S, W, words_a, wa);
+        const int32_t center = a.center[0];
+#pragma unroll
+        for (int k = 0; k < 256 / kSampleGroup; ++k)
+            build_decode_entry(tba, t + k * kSampleGroup, packed[k], center);
+    }
+    if (walk_b) {
+        int32_t packed[256 / kSampleGroup];
+#pragma unroll
+        for (int k = 0; k < 256 / kSampleGroup; ++k)
+            packed[k] = b.shifted_decode[t + k * kSampleGroup];
+        sample_issue(b, active, row, lane, block, n_blocks, S, W, words_b, wb);
+        const int32_t center = b.center[0];
+#pragma unroll
+        for (int k = 0; k < 256 / kSampleGroup; ++k)
+            build_decode_entry(tbb, t + k * kSampleGroup, packed[k], center);
+    }
+    wait_memory();
+    __syncthreads();   // decode tables and staged words
+    const uint32_t av = walk_a ? sample_walk(a, wa, active, step, words_a, &tba, W, rare)
+                               : (active ? a_samples[i] : 0u);
+    const uint32_t bv = walk_b ? sample_walk(b, wb, active, step, words_b, &tbb, W, rare)
+                               : (active ? b_samples[i] : 0u);
+    const uint32_t result =
+        float_to_bf16(__builtin_fmaf(bf16_to_float(av), alpha[0], bf16_to_float(bv)));
+    if (active && result_samples != nullptr) result_samples[i] = static_cast<uint16_t>(result);
+    const int32_t exp = static_cast<int32_t>((result >> 7) & 255u) - 127;
+    const bool keep = active && exp >= -120;
+    const int32_t sum = wave_sum(keep ? exp : 0);
+    const int32_t kept = wave_sum(keep ? 1 : 0);
+    if (t == 0) {
+        partials[2 * blockIdx.x] = sum;
+        partials[2 * blockIdx.x + 1] = kept;
+    }
+}
+
+// Chunks [c_begin, c_end) of the two-operand pass with one overlay variant for
+// both operands (tails read from HBM).  On entry side_a/side_b hold chunk
+// c_begin's side bytes of A and B.
+template <bool kFull, Overlay kOverlay, int S>
+__device__ __forceinline__ void dual_chunks(StreamCursor &ca, const LaneOverlay &lane_a,
+                                            StreamCursor &cb, const LaneOverlay &lane_b,
+                                            uint8_t *slice_a, uint8_t *slice_b,
+                                            SideChunk &side_a, SideChunk &side_b,
+                                            __amdgpu_buffer_rsrc_t b_side, StreamWriter &writer,
+                                            const uint32_t *enc, const UpdateIo &io,
+                                            int64_t row_base, uint32_t valid_in_block,
+                                            int c_begin, int c_end, float alpha) {
+    const uint32_t voffset = side_fetch_offset();
+#pragma unroll 1
+    for (int c = c_begin; c < c_end; c += kChunkSteps) {
+        store_side_chunk(slice_a, side_a);
+        store_side_chunk(slice_b, side_b);
+        const bool more = c + kChunkSteps < S;
+        side_a = fetch_side_chunk(io.side, more ? voffset : kOutOfRange, c + kChunkSteps);
+        side_b = fetch_side_chunk(b_side, more ? voffset : kOutOfRange, c + kChunkSteps);
+        const uint32_t mask = static_cast<uint32_t>((row_base + c) & 254);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int first = c + half * kHalfSteps;
+            uint32_t fa[kHalfSteps], fb[kHalfSteps];
+            decode_fields<kFull, kOverlay>(ca, lane_a, nullptr, first, row_base, valid_in_block,
+                                           fa);
+            decode_fields<kFull, kOverlay>(cb, lane_b, nullptr, first, row_base, valid_in_block,
+                                           fb);
+#pragma unroll
+            for (int j = 0; j < kHalfSteps; j += 2) {
+                const int s0 = half * kHalfSteps + j;
+                const int step = c + s0;
+                const uint32_t off0 = static_cast<uint32_t>(step) * kLanes
+                    + (threadIdx.x ^ mask ^ static_cast<uint32_t>(s0));
+                const bool v0 = kFull || off0 < valid_in_block;
+                const bool v1 = kFull || off0 + kLanes < valid_in_block;
+                const float a0 = bf16_to_float(join_entry(fa[j], side_byte(slice_a, s0)));
+                const float a1 = bf16_to_float(join_entry(fa[j + 1], side_byte(slice_a, s0 + 1)));
+                const float b0 = bf16_to_float(join_entry(fb[j], side_byte(slice_b, s0)));
+                const float b1 = bf16_to_float(join_entry(fb[j + 1], side_byte(slice_b, s0 + 1)));
+                // Padding positions hold 0 (side byte 0, no code).
+                const uint32_t h0 = v0 ? round_bf16_high(__builtin_fmaf(a0, alpha, b0)) : 0u;
+                const uint32_t h1 = v1 ? round_bf16_high(__builtin_fmaf(a1, alpha, b1)) : 0u;
+                emit_pair(writer, enc, slice_a, s0, h0, h1, v0, v1, off0, step, io);
+            }
+        }
+        const uint4 q = reinterpret_cast<const uint4 *>(slice_a)[threadIdx.x & (kWave - 1)];
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, q), io.side_out,
+            voffset, c * kLanes, kStreaming);
+    }
+}
+
+template <bool kFull, int S>
+__device__ __forceinline__ void dual_rows(StreamCursor ca, const LaneOverlay &lane_a,
+                                          StreamCursor cb, const LaneOverlay &lane_b,
+                                          uint8_t *slice_a, uint8_t *slice_b, SideChunk side_a,
+                                          SideChunk side_b, __amdgpu_buffer_rsrc_t b_side,
+                                          StreamWriter &writer, const uint32_t *enc,
+                                          const UpdateIo &io, int64_t row_base,
+                                          uint32_t valid_in_block, float alpha) {
+    const int split = min(S, min(lane_a.wave_start, lane_b.wave_start) & ~(kChunkSteps - 1));
+    dual_chunks<kFull, kNoOverlay, S>(ca, lane_a, cb, lane_b, slice_a, slice_b, side_a, side_b,
+                                      b_side, writer, enc, io, row_base, valid_in_block, 0, split,
+                                      alpha);
+    if (split < S)
+        dual_chunks<kFull, kHbmOverlay, S>(ca, lane_a, cb, lane_b, slice_a, slice_b, side_a,
+                                           side_b, b_side, writer, enc, io, row_base,
+                                           valid_in_block, split, S, alpha);
+}
+
+__global__ __launch_bounds__(kLanes) void dual_encode_kernel(
+    OperandA a, OperandA b, const float *__restrict__ alpha,
+    const int32_t *__restrict__ partials, int32_t n_groups,
+    const int32_t *__restrict__ base_encode, const int32_t *__restrict__ base_decode,
+    int32_t *__restrict__ center_out, int32_t *__restrict__ shifted_decode_out,
+    uint8_t *__restrict__ side_out, int32_t *__restrict__ encoded_out,
+    uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
+    uint8_t *__restrict__ exponents, int64_t n_blocks, int64_t logical_numel, int S, int W,
+    int rare) {
+    extern __shared__ uint32_t stages[];   // A's payload then B's: 2 x stage_bytes(W)
+    __shared__ DecodeTables tba, tbb;
+    __shared__ uint32_t enc[256];
+    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ int32_t shared_center;
+    // The overflow maps (2 KiB) and the raw encode table (1 KiB) are only used
+    // before the first side chunks are stored, so they share A's side slices.
+    __shared__ __attribute__((aligned(16))) uint8_t slices_a[kWavesPerBlock][kChunkSteps * kWave];
+    __shared__ __attribute__((aligned(16))) uint8_t slices_b[kWavesPerBlock][kChunkSteps * kWave];
+    int32_t *map_start = reinterpret_cast<int32_t *>(&slices_a[0][0]);
+    int32_t *map_offset = map_start + kLanes;
+    int32_t *raw_encode = map_offset + kLanes;
+    uint32_t *stage_a = stages;
+    uint32_t *stage_b = stages + stage_bytes(W) / 4;
+    const int t = threadIdx.x;
+    const int64_t block = blockIdx.x;
+    const int64_t row_base = block * S;
+    const int64_t logical_base = row_base * kLanes;
+    const uint32_t block_elems = static_cast<uint32_t>(S) * kLanes;
+    const int64_t remaining = logical_numel - logical_base;
+    const uint32_t valid = remaining < block_elems ? static_cast<uint32_t>(remaining) : block_elems;
+    UpdateIo io;
+    io.side = make_rsrc(a.side + logical_base, block_elems);
+    io.other = make_rsrc(nullptr, 0u);
+    io.side_out = make_rsrc(side_out + logical_base, block_elems);
+    io.exponents = make_rsrc(exponents + logical_base, valid);
+    const __amdgpu_buffer_rsrc_t b_side = make_rsrc(b.side + logical_base, block_elems);
+    const SideChunk first_a = fetch_side_chunk(io.side, side_fetch_offset(), 0);
+    const SideChunk first_b = fetch_side_chunk(b_side, side_fetch_offset(), 0);
+
+    raw_encode[t] = base_encode[t];
+    center_from_partials(partials, n_groups, &shared_center);
+    build_decode_tables(tba, a.shifted_decode, a.center[0]);
+    build_decode_tables(tbb, b.shifted_decode, b.center[0]);
+    stage_payload(stage_a, a.encoded, n_blocks * kLanes, block, W);
+    stage_payload(stage_b, b.encoded, n_blocks * kLanes, block, W);
+    __syncthreads();   // center and raw encode table
+    const int32_t center = shared_center;
+    enc[t] = repack_encode_entry(static_cast<uint32_t>(raw_encode[byte_to_index(t, center)]));
+    if (block == 0) {
+        if (t == 0) center_out[0] = center;
+        for (int i = t; i < 1024; i += kLanes)
+            shifted_decode_out[i] = shifted_decode_entry(base_decode[i], center);
+    }
+    __syncthreads();   // raw_encode is no longer read (it shares the maps' LDS)
+    const LaneOverlay lane_a = build_overlay(a.ov, a.has_overlay != 0, block, n_blocks, S,
+                                             map_start, map_offset, scratch, nullptr, 0);
+    __syncthreads();   // B's overlay reuses the maps
+    const LaneOverlay lane_b = build_overlay(b.ov, b.has_overlay != 0, block, n_blocks, S,
+                                             map_start, map_offset, scratch, nullptr, 0);
+    const float alpha_value = alpha[0];
+    wait_memory();
+    __syncthreads();   // payloads and encode table visible; maps no longer read
+
+    StreamCursor ca, cb;
+    ca.init(stage_a + t, &tba, static_cast<uint32_t>(W), rare);
+    cb.init(stage_b + t, &tbb, static_cast<uint32_t>(W), rare);
+    const uint32_t row_bytes = static_cast<uint32_t>(n_blocks * kLanes * 4);
+    StreamWriter writer{make_rsrc(encoded_out + block * kLanes,
+                                  static_cast<uint32_t>(W - 1) * row_bytes + kLanes * 4),
+                        row_bytes, static_cast<uint32_t>(t) * 4u,
+                        static_cast<uint32_t>(W) * 32u, 0u, 0u, S};
+    uint8_t *slice_a = slices_a[t / kWave];
+    uint8_t *slice_b = slices_b[t / kWave];
+    const bool full = valid == block_elems;
+#define LCT_DUAL_ROWS(FULL, SS)                                                                \
+    dual_rows<FULL, SS>(ca, lane_a, cb, lane_b, slice_a, slice_b, first_a, first_b, b_side,    \
+                        writer, enc, io, row_base, valid, alpha_value)
+    if (S == 128) {
+        if (full) LCT_DUAL_ROWS(true, 128);
+        else LCT_DUAL_ROWS(false, 128);
+    } else {
+        if (full) LCT_DUAL_ROWS(true, 256);
+        else LCT_DUAL_ROWS(false, 256);
+    }
+#undef LCT_DUAL_ROWS
+    writer.finish();
+    const bool overflow = writer.overflowed();
+    extra_starts[block * kLanes + t] = static_cast<uint8_t>(overflow ? writer.extra : 255);
+    const int32_t count = block_sum(overflow ? 1 : 0, scratch);
+    const int32_t bytes = block_sum(overflow ? S - writer.extra : 0, scratch);
+    if (t == 0) {
+        summaries[block] = count;
+        summaries[n_blocks + block] = bytes;
+    }
+}
+
 int32_t check_operand(const int32_t *encoded, const uint8_t *side, const int32_t *shifted_decode,
                       const int32_t *center, const lct_overflow *overflow) {
     if (!encoded || !side || !shifted_decode || !center) return LCT_E_NULL;
@@ -614,5 +901,80 @@ extern "C" int32_t lct_pointwise_encode(
                        partials, groups, base_encode, base_decode, center_out,
                        shifted_decode_out, side_out, encoded_out, extra_starts, summaries,
                        exponents, n_blocks, logical_numel, g.steps, g.fixed_words, rare_length);
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_dual_sample(const int32_t *a_encoded, const uint8_t *a_side,
+                                   const int32_t *a_shifted_decode, const int32_t *a_center,
+                                   const lct_overflow *a_overflow, const void *a_samples,
+                                   const int32_t *b_encoded, const uint8_t *b_side,
+                                   const int32_t *b_shifted_decode, const int32_t *b_center,
+                                   const lct_overflow *b_overflow, const void *b_samples,
+                                   const float *alpha, int64_t size, int64_t logical_numel,
+                                   lct_geometry g, int32_t rare_length, int64_t sample_size,
+                                   int32_t *partials, void *result_samples,
+                                   hipStream_t stream) {
+    if (int32_t e = check_operand(a_encoded, a_side, a_shifted_decode, a_center, a_overflow))
+        return e;
+    if (int32_t e = check_operand(b_encoded, b_side, b_shifted_decode, b_center, b_overflow))
+        return e;
+    if (!alpha || !partials) return LCT_E_NULL;
+    if (int32_t e = check_shape(size, logical_numel, g, rare_length)) return e;
+    if (int32_t e = check_samples(sample_size, logical_numel)) return e;
+    const OperandA a{a_encoded, a_side, a_shifted_decode, a_center,
+                     a_overflow ? *a_overflow : lct_overflow{}, a_overflow != nullptr};
+    const OperandA b{b_encoded, b_side, b_shifted_decode, b_center,
+                     b_overflow ? *b_overflow : lct_overflow{}, b_overflow != nullptr};
+    const int64_t n_blocks = size / g.block_symbols;
+    const size_t lds = 2 * static_cast<size_t>(g.fixed_words + 1) * kSampleGroup * sizeof(uint32_t);
+    hipLaunchKernelGGL(dual_sample_kernel, dim3(sample_groups(sample_size)), dim3(kSampleGroup),
+                       lds, stream, a, static_cast<const uint16_t *>(a_samples), b,
+                       static_cast<const uint16_t *>(b_samples), alpha, n_blocks, logical_numel,
+                       sample_size, g.steps, g.fixed_words, rare_length, partials,
+                       static_cast<uint16_t *>(result_samples));
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_dual_encode(
+    const int32_t *a_encoded, const uint8_t *a_side, const int32_t *a_shifted_decode,
+    const int32_t *a_center, const lct_overflow *a_overflow, const int32_t *b_encoded,
+    const uint8_t *b_side, const int32_t *b_shifted_decode, const int32_t *b_center,
+    const lct_overflow *b_overflow, const float *alpha, const int32_t *partials,
+    int64_t sample_size, const int32_t *base_encode, const int32_t *base_decode,
+    int32_t *center_out, int32_t *shifted_decode_out, uint8_t *side_out, int32_t *encoded_out,
+    uint8_t *extra_starts, int32_t *summaries, uint8_t *exponents, int64_t size,
+    int64_t logical_numel, lct_geometry g, int32_t rare_length, hipStream_t stream) {
+    if (int32_t e = check_operand(a_encoded, a_side, a_shifted_decode, a_center, a_overflow))
+        return e;
+    if (int32_t e = check_operand(b_encoded, b_side, b_shifted_decode, b_center, b_overflow))
+        return e;
+    if (!alpha || !partials || !base_encode || !base_decode || !center_out
+        || !shifted_decode_out || !side_out || !encoded_out || !extra_starts || !summaries
+        || !exponents)
+        return LCT_E_NULL;
+    if (int32_t e = check_shape(size, logical_numel, g, rare_length)) return e;
+    if (int32_t e = check_samples(sample_size, logical_numel)) return e;
+    // 16-byte accesses: payload staging, A's, B's and the result's side bytes.
+    if (((reinterpret_cast<uintptr_t>(a_encoded) | reinterpret_cast<uintptr_t>(b_encoded)
+          | reinterpret_cast<uintptr_t>(a_side) | reinterpret_cast<uintptr_t>(b_side)
+          | reinterpret_cast<uintptr_t>(side_out)) & 15) != 0)
+        return LCT_E_ARG;
+    const int64_t n_blocks = size / g.block_symbols;
+    // The result's payload words are addressed with 32-bit buffer offsets.
+    if (static_cast<int64_t>(g.fixed_words) * n_blocks * kLanes * 4 >= (int64_t{1} << 31))
+        return LCT_E_SIZE;
+    const OperandA a{a_encoded, a_side, a_shifted_decode, a_center,
+                     a_overflow ? *a_overflow : lct_overflow{}, a_overflow != nullptr};
+    const OperandA b{b_encoded, b_side, b_shifted_decode, b_center,
+                     b_overflow ? *b_overflow : lct_overflow{}, b_overflow != nullptr};
+    const size_t lds = 2 * static_cast<size_t>(stage_bytes(g.fixed_words));
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&dual_encode_kernel),
+                                           lds))
+        return static_cast<int32_t>(e);
+    hipLaunchKernelGGL(dual_encode_kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes),
+                       lds, stream, a, b, alpha, partials, sample_groups(sample_size),
+                       base_encode, base_decode, center_out, shifted_decode_out, side_out,
+                       encoded_out, extra_starts, summaries, exponents, n_blocks, logical_numel,
+                       g.steps, g.fixed_words, rare_length);
     return static_cast<int32_t>(hipGetLastError());
 }

@@ -256,6 +256,49 @@ def pointwise_encode(encoded, sign_mantissa, shifted_decode, center, other, alph
              int(bool(beta_is_one)), _stream(encoded))
 
 
+def _byref(storage: FallbackStorage | None):
+    ov = storage.as_overflow() if storage is not None else None
+    return ov if ov is None else hip.ctypes.byref(ov)
+
+
+def dual_sample(a_encoded, a_sign_mantissa, a_shifted_decode, a_center, a_storage, b_encoded,
+                b_sign_mantissa, b_shifted_decode, b_center, b_storage, alpha, partials, size, *,
+                rare_length, logical_numel, block_symbols, lanes, steps, fixed_words,
+                sample_size, a_samples=None, b_samples=None, result_samples=None) -> None:
+    """``fma(a, alpha, b)`` at the center sample positions only, for two
+    compressed operands: exponent sum and count per group of 64 samples into
+    ``partials``.  ``a_samples``/``b_samples``: an operand's recorded values at
+    those positions (then its streams are not read); ``result_samples``
+    receives the result's."""
+    _require_device(a_encoded, b_encoded, alpha, partials)
+    geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
+    hip.call("lct_dual_sample", _ptr(a_encoded), _ptr(a_sign_mantissa), _ptr(a_shifted_decode),
+             _ptr(a_center), _byref(a_storage), _ptr(a_samples), _ptr(b_encoded),
+             _ptr(b_sign_mantissa), _ptr(b_shifted_decode), _ptr(b_center), _byref(b_storage),
+             _ptr(b_samples), _ptr(alpha), int(size), int(logical_numel), geometry,
+             int(rare_length), int(sample_size), _ptr(partials), _ptr(result_samples),
+             _stream(a_encoded))
+
+
+def dual_encode(a_encoded, a_sign_mantissa, a_shifted_decode, a_center, a_storage, b_encoded,
+                b_sign_mantissa, b_shifted_decode, b_center, b_storage, alpha, partials,
+                base_encode, base_decode, center_out, shifted_decode_out, side_out,
+                encoded_out, extra_starts, summaries, exponents, size, *, rare_length,
+                logical_numel, block_symbols, lanes, steps, fixed_words, sample_size) -> None:
+    """Decode A and B, ``fma(a, alpha, b)`` and re-encode in one pass: the
+    single-pass form of the compressed-output ``dual_mapped`` launch followed
+    by the encoder launch of ``encode_components(precomputed=True)``."""
+    _require_device(a_encoded, b_encoded, alpha, partials, encoded_out)
+    geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
+    hip.call("lct_dual_encode", _ptr(a_encoded), _ptr(a_sign_mantissa), _ptr(a_shifted_decode),
+             _ptr(a_center), _byref(a_storage), _ptr(b_encoded), _ptr(b_sign_mantissa),
+             _ptr(b_shifted_decode), _ptr(b_center), _byref(b_storage), _ptr(alpha),
+             _ptr(partials), int(sample_size), _ptr(base_encode), _ptr(base_decode),
+             _ptr(center_out), _ptr(shifted_decode_out), _ptr(side_out), _ptr(encoded_out),
+             _ptr(extra_starts), _ptr(summaries), _ptr(exponents), int(size),
+             int(logical_numel), geometry, int(rare_length), _stream(a_encoded))
+
+
 # ---------------------------------------------------------------------------
 # TensorBuffer allocator (LCT/tensor_buffer.py:93-136, tensor_buffer_ops.py)
 # ---------------------------------------------------------------------------

@@ -77,6 +77,13 @@ _SIGNATURES = {
                              _ptr, _c_int64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
                              _c_int64, _c_int64, Geometry, _c_int32, _c_int32, _c_int32, _c_int32,
                              _ptr],
+    "lct_dual_sample": [_ptr, _ptr, _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _ptr,
+                        _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _c_int64, _c_int64,
+                        Geometry, _c_int32, _c_int64, _ptr, _ptr, _ptr],
+    "lct_dual_encode": [_ptr, _ptr, _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _ptr,
+                        _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _c_int64, _ptr, _ptr, _ptr,
+                        _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64, _c_int64, Geometry,
+                        _c_int32, _ptr],
     "lct_buffer_reset": [_ptr, _c_int32, _c_int32, _ptr],
     "lct_buffer_allocate": [_ptr, _c_int32, _ptr, _ptr, _c_int32, _ptr, _ptr],
     "lct_buffer_free": [_ptr, _c_int32, _ptr, _ptr, _ptr],

@@ -33,6 +33,7 @@ from losslessly_compressed_tensors_amd.LCTensor import LCTTensor
 from losslessly_compressed_tensors_amd.operations import (
     a_compA_add_B,
     a_compA_add_b_B,
+    a_compA_add_compB,
     compA_add_B,
     compA_mul_B,
     compress,
@@ -327,6 +328,138 @@ def test_momentum_sequence_single_pass():
         previous = state
         state = oracle_from_components(side, exponents, dist, buffer=host)
         host.free(previous.descriptor)
+        assert_matches_oracle(tensor.x, state)
+    tensor.free()
+    verify_buffer(buffer)
+
+
+# ---- two compressed operands: alpha * A + B (LCTTensor.add_comp_)
+
+# (name, A's distribution, B's distribution, A, B): the operands share a stream
+# geometry; the patterns cases overflow in A, in B or in both.
+DUAL_CASES = [
+    ("gaussian", Distribution(DistType.GAUSSIAN), Distribution(DistType.GAUSSIAN),
+     lambda: _gaussian((1024, 1024), 40), lambda: _gaussian((1024, 1024), 41, 0.5)),
+    ("patterns-both", Distribution(DistType.LAPLACE, noise_level=NoiseLevel.SPARSE),
+     Distribution(DistType.LAPLACE, noise_level=NoiseLevel.SPARSE),
+     lambda: _patterns(42), lambda: _patterns(43)),
+    ("patterns-b-only", Distribution(DistType.GAUSSIAN, noise_level=NoiseLevel.MEDIUM),
+     Distribution(DistType.GAUSSIAN, noise_level=NoiseLevel.MEDIUM),
+     lambda: _gaussian((3, 33333), 44), lambda: _patterns(45, 3 * 33333)),
+    ("tiny-every-sample", Distribution(DistType.GAUSSIAN, noise_level=NoiseLevel.MEDIUM),
+     Distribution(DistType.LAPLACE, noise_level=NoiseLevel.MEDIUM),
+     lambda: _gaussian((37, 41), 46), lambda: _gaussian((37, 41), 47)),
+    ("empirical-high", Distribution(DistType.EMPIRICAL, noise_level=NoiseLevel.HIGH),
+     Distribution(DistType.EMPIRICAL, noise_level=NoiseLevel.HIGH),
+     lambda: _spread((3 * 32768 + 1000,), 48), lambda: _patterns(49, 3 * 32768 + 1000)),
+]
+
+# Which operands' recorded sample values the sampler is given.
+RECORDED = [(False, False), (True, False), (False, True), (True, True)]
+
+
+def _dual_operands(case, buffer=None, host=None):
+    name, dist_a, dist_b, make_a, make_b = case
+    a = make_a()
+    b = make_b().reshape(a.shape)
+    ca, cb = compress(a.cuda(), dist_a, buffer=buffer), compress(b.cuda(), dist_b, buffer=buffer)
+    assert ca.codec_geometry == cb.codec_geometry, "dual cases need one stream geometry"
+    oa = oracle_compress(a, dist_a, buffer=host)
+    ob = oracle_compress(b, dist_b, buffer=host)
+    return ca, cb, oa, ob
+
+
+@pytest.mark.parametrize("case", DUAL_CASES, ids=[c[0] for c in DUAL_CASES])
+@pytest.mark.parametrize("recorded", RECORDED, ids=["streams", "a-recorded", "b-recorded",
+                                                    "both-recorded"])
+def test_dual_sampler_partials_match_the_oracle(case, recorded):
+    """lct_dual_sample's group sums and recorded result values, with each
+    operand's value taken from its streams or from its recorded samples."""
+    require_gpu()
+    print(f"case dual sampler {case[0]} recorded={recorded}", flush=True)
+    ca, cb, oa, ob = _dual_operands(case)
+    n = ca.logical_numel
+    sample_size = min(n, 4096)
+    groups = -(-sample_size // 64)
+    partials = torch.full((2 * groups,), -7, dtype=torch.int32, device="cuda")
+    result_samples = torch.full((sample_size,), -7, dtype=torch.int16, device="cuda")
+    B, L, S, W = ca.codec_geometry
+    _, _, rare = get_distribution_tables(ca.distribution, "cuda")
+    dispatch.dual_sample(ca.data, ca.sign_mantissa, shifted_decode_table(ca), ca.center,
+                         overlay_of(ca), cb.data, cb.sign_mantissa, shifted_decode_table(cb),
+                         cb.center, overlay_of(cb), _scalar(ALPHA), partials, ca.size,
+                         rare_length=rare, logical_numel=n, block_symbols=B, lanes=L, steps=S,
+                         fixed_words=W, sample_size=sample_size,
+                         a_samples=ca.sample_values if recorded[0] else None,
+                         b_samples=cb.sample_values if recorded[1] else None,
+                         result_samples=result_samples)
+    expected_values = oracle.dual(oa, ob, ALPHA)[oracle.sample_positions(n)]
+    assert np.array_equal(bits_of(result_samples), expected_values)
+    got = partials.cpu().numpy().reshape(groups, 2)
+    assert np.array_equal(got, _group_sums(expected_values))
+
+
+@pytest.mark.parametrize("case", DUAL_CASES, ids=[c[0] for c in DUAL_CASES])
+@pytest.mark.parametrize("buffered", [False, True], ids=["private", "buffered"])
+def test_dual_single_pass_compressed_output(case, buffered):
+    """a_compA_add_compB with compressed output: every stored field equals the
+    oracle's re-encode of the oracle's dual components, and the recorded sample
+    values are the result's."""
+    require_gpu()
+    print(f"case dual single-pass {case[0]} buffered={buffered}", flush=True)
+    buffer = TensorBuffer(8 << 20, max_free_regions=64, device="cuda") if buffered else None
+    host = oracle.Buffer(8 << 20, 64) if buffered else None
+    ca, cb, oa, ob = _dual_operands(case, buffer, host)
+    result = a_compA_add_compB(ca, _scalar(ALPHA), cb, dense_output=False, buffer=buffer)
+    side, exponents = oracle.dual(oa, ob, ALPHA, policy=1)
+    expected = oracle_from_components(side, exponents, ca.distribution, buffer=host)
+    assert_matches_oracle(result, expected)
+    dense = oracle.dual(oa, ob, ALPHA)
+    assert np.array_equal(bits_of(decompress(result)), dense)
+    assert np.array_equal(bits_of(result.sample_values),
+                          dense[oracle.sample_positions(ca.logical_numel)])
+    if buffered:
+        result.free()
+        cb.free()
+        ca.free()
+        verify_buffer(buffer)
+
+
+def test_dual_cases_exercise_overflow():
+    """The overflow branches of the two-operand kernel are reached: both
+    operands overflow in one case, only B in another, and so does a result."""
+    require_gpu()
+    _, _, oa, ob = _dual_operands(DUAL_CASES[1])
+    assert oa.counts[0] > 0 and ob.counts[0] > 0
+    _, _, oa, ob = _dual_operands(DUAL_CASES[2])
+    assert oa.counts[0] == 0 and ob.counts[0] > 0
+    side, exponents = oracle.dual(oa, ob, ALPHA, policy=1)
+    assert oracle_from_components(side, exponents, DUAL_CASES[2][1]).counts[0] > 0
+
+
+def test_weight_update_sequence_single_pass():
+    """Eight add_comp_ steps (weight += alpha * compressed update) on a
+    buffer-backed LCTTensor, each checked against the oracle; the sampler
+    reads both operands' recorded sample values."""
+    require_gpu()
+    dist = Distribution(DistType.EMPIRICAL)
+    shape = (1024, 1100)
+    buffer = TensorBuffer(32 << 20, max_free_regions=64, device="cuda")
+    host = oracle.Buffer(32 << 20, 64)
+    w0 = _gaussian(shape, 50, 0.02)
+    tensor = LCTTensor(w0.cuda(), buffer, dist)
+    state = oracle_compress(w0, dist, buffer=host)
+    for step in range(8):
+        u = _gaussian(shape, 500 + step, 1e-3)
+        update = LCTTensor(u.cuda(), buffer, dist)
+        update_state = oracle_compress(u, dist, buffer=host)
+        tensor.add_comp_(update, _scalar(ALPHA))
+        side, exponents = oracle.dual(update_state, state, ALPHA, policy=1)
+        previous = state
+        state = oracle_from_components(side, exponents, dist, buffer=host)
+        host.free(previous.descriptor)
+        update.free()
+        host.free(update_state.descriptor)
         assert_matches_oracle(tensor.x, state)
     tensor.free()
     verify_buffer(buffer)
