@@ -159,14 +159,41 @@ int32_t lct_prefix_allocate(int32_t *summaries, int32_t *counts,
                             int32_t *blocks, int64_t n_blocks, int32_t buffered,
                             int32_t max_free_regions, hipStream_t stream);
 
-/* ---- replaces dispatch.py:113-130 (compact_extra, summaries path): for the
- * blocks listed by lct_prefix_allocate, write the overflowing streams' lane
- * and start bytes (ascending lane) at entries blocks[nb+k].. and their
- * exponent tails int8(e-127) for steps start..S-1 from byte blocks[2nb+k].
- * Private: lanes/starts/tail are exact-size arrays, tails at tail + base.
- * Buffered: all three point at the arena; offsets from descriptor and count
- * as in lct_overflow.  A buffered allocation whose status is not 0 gets no
- * entries or tails written. */
+/* ---- replaces dispatch.py:88-95 (count_bad_streams, the atomic path's
+ * totals, LCT/kernels/generic/compaction.py:31-51): adds the number of
+ * overflowing streams (extra_starts[s] != 255) to count[0] and their tail
+ * bytes (steps - start) to total[0] with device atomics; the caller zeroes
+ * both first. */
+int32_t lct_count_bad_streams(const uint8_t *extra_starts, int32_t *count,
+                              int32_t *total, int64_t n_streams, int32_t steps,
+                              hipStream_t stream);
+
+/* ---- replaces dispatch.py:98-110 (compact_bad_streams, compaction.py:54-96):
+ * one workgroup per codec block reserves its entry slots and tail bytes with
+ * atomics on bad_count[0] / fallback_total[0] (zeroed by the caller), writes
+ * blocks[3*nb] = {count, first, byte_base} (0, 0, 0 for blocks without
+ * overflow) and its entries (lane, start; lanes ascending) at first.. .
+ * Buffered: lanes/starts point at the arena, entries at descriptor[0] and
+ * starts at descriptor[0] + final_counts[0]; a failed reservation (status
+ * != 0) gets no entries.  The order of the blocks' slices follows the
+ * atomics; lct_compact_extra with summaries = NULL then writes the tails. */
+int32_t lct_compact_bad_streams(const uint8_t *extra_starts, uint8_t *lanes,
+                                uint8_t *starts, const int32_t *descriptor,
+                                int32_t *blocks, const int32_t *final_counts,
+                                int32_t *bad_count, int32_t *fallback_total,
+                                int64_t n_streams, int32_t steps, int64_t n_blocks,
+                                int32_t buffered, hipStream_t stream);
+
+/* ---- replaces dispatch.py:113-130 (compact_extra): for the blocks listed by
+ * lct_prefix_allocate (summaries path), or for every block with overflow
+ * when summaries is NULL (block metadata from lct_compact_bad_streams,
+ * BUILD_META=False), write the overflowing streams' lane and start bytes
+ * (ascending lane) at entries blocks[nb+k].. and their exponent tails
+ * int8(e-127) for steps start..S-1 from byte blocks[2nb+k].  Private:
+ * lanes/starts/tail are exact-size arrays, tails at tail + base.  Buffered:
+ * all three point at the arena; offsets from descriptor and count as in
+ * lct_overflow.  A buffered allocation whose status is not 0 gets no entries
+ * or tails written. */
 int32_t lct_compact_extra(const void *source, uint8_t *lanes, uint8_t *starts,
                           uint8_t *tail, const int32_t *descriptor,
                           const int32_t *count, const int32_t *blocks, int64_t base,
@@ -184,9 +211,18 @@ int32_t lct_decode(const int32_t *encoded, const uint8_t *side, int16_t *output,
                    int32_t rare_length, const lct_overflow *overflow,
                    hipStream_t stream);
 
+/* ---- replaces dispatch.py:146-165 (scatter_fallback,
+ * LCT/kernels/generic/compaction.py:238-306): after a decode without the
+ * overlay, rebuilds every overflow tail byte into BF16 with its side byte
+ * and writes it at its logical position of output (int16[logical_numel]). */
+int32_t lct_scatter_fallback(const lct_overflow *overflow, const uint8_t *side,
+                             void *output, int64_t size, int64_t logical_numel,
+                             lct_geometry geometry, hipStream_t stream);
+
 /* ---- fused pointwise, one compressed + one dense operand: replaces
- * dispatch.py:168-187 (pointwise_dense) together with dispatch.py:190-212
- * (pointwise_fallback); overflow rows are overlaid in the same pass.
+ * dispatch.py:168-187 (pointwise_dense); with overflow != NULL the overflow
+ * rows are overlaid in the same pass (what dispatch.py:190-212,
+ * pointwise_fallback, does as a second launch; see lct_pointwise_fallback).
  * other: bf16[logical_numel].  alpha/beta: float32[1] device scalars, read
  * only for LCT_OP_SCALAR_MUL_ADD when !alpha_is_one / !beta_is_one.
  * Dense policy: output bf16[logical_numel]; auxiliary unused.  Compressed
@@ -202,9 +238,22 @@ int32_t lct_pointwise_dense(const int32_t *encoded, const uint8_t *side,
                             int32_t beta_is_one, int32_t output_policy,
                             const lct_overflow *overflow, hipStream_t stream);
 
+/* ---- replaces dispatch.py:190-212 (pointwise_fallback,
+ * LCT/kernels/generic/pointwise.py:265-340): after lct_pointwise_dense
+ * without the overlay, recomputes op(A, other) at every overflow tail byte
+ * of A and stores it as lct_pointwise_dense does (dense BF16 at logical
+ * positions, or side byte at the storage position, 0 for padding, and
+ * exponent byte at the logical position). */
+int32_t lct_pointwise_fallback(const lct_overflow *overflow, const uint8_t *side,
+                               const void *other, void *output, uint8_t *auxiliary,
+                               const float *alpha, const float *beta, int64_t size,
+                               int64_t logical_numel, lct_geometry geometry, int32_t op,
+                               int32_t alpha_is_one, int32_t beta_is_one,
+                               int32_t output_policy, hipStream_t stream);
+
 /* ---- fused alpha*A + B with both operands compressed (same geometry):
  * replaces dispatch.py:215-286 (dual_maps_init + dual_tables_and_maps +
- * dual_mapped) with one launch; a_shifted/b_shifted are each operand's
+ * dual_mapped) with one launch, the maps built per block in the prologue; a_shifted/b_shifted are each operand's
  * shifted decode table.  Outputs as lct_pointwise_dense. */
 int32_t lct_dual(const int32_t *a_encoded, const uint8_t *a_side,
                  const int32_t *a_shifted_decode, const int32_t *a_center,
@@ -215,6 +264,43 @@ int32_t lct_dual(const int32_t *a_encoded, const uint8_t *a_side,
                  int64_t size, int64_t logical_numel, lct_geometry geometry,
                  int32_t rare_length, int32_t output_policy,
                  hipStream_t stream);
+
+/* ---- the reference's three-launch form of the fused dual, for callers that
+ * sequence it themselves.  lct_dual_maps_init replaces dispatch.py:215-225
+ * (dual_maps_init): both operands' per-stream maps int32[n_streams] get
+ * start = steps and offset 0. */
+int32_t lct_dual_maps_init(int32_t *a_stream_starts, int32_t *a_stream_offsets,
+                           int32_t *b_stream_starts, int32_t *b_stream_offsets,
+                           int64_t n_streams, int32_t steps, hipStream_t stream);
+
+/* ---- replaces dispatch.py:228-252 (dual_tables_and_maps): shifts both base
+ * decode tables (int32[1024]) by their centers into a/b_shifted_decode and
+ * writes, for every overflowing stream of either operand, its start step and
+ * tail byte offset (from the tail base: descriptor[0] + 2*count when
+ * buffered, overflow->base when private) into that operand's maps.  An
+ * operand with overflow = NULL, or a buffered one whose reservation failed,
+ * writes no map entries. */
+int32_t lct_dual_tables_and_maps(const int32_t *a_base_decode, const int32_t *a_center,
+                                 int32_t *a_shifted_decode, const int32_t *b_base_decode,
+                                 const int32_t *b_center, int32_t *b_shifted_decode,
+                                 const lct_overflow *a_overflow, const lct_overflow *b_overflow,
+                                 int32_t *a_stream_starts, int32_t *a_stream_offsets,
+                                 int32_t *b_stream_starts, int32_t *b_stream_offsets,
+                                 int64_t n_blocks, int32_t steps, hipStream_t stream);
+
+/* ---- replaces dispatch.py:255-286 (dual_mapped): lct_dual with each
+ * operand's overlay read from its per-stream maps instead of its compact
+ * list (the overflow struct then supplies only the tail bytes). */
+int32_t lct_dual_mapped(const int32_t *a_encoded, const uint8_t *a_side,
+                        const int32_t *a_shifted_decode, const int32_t *a_center,
+                        const int32_t *a_stream_starts, const int32_t *a_stream_offsets,
+                        const lct_overflow *a_overflow, const int32_t *b_encoded,
+                        const uint8_t *b_side, const int32_t *b_shifted_decode,
+                        const int32_t *b_center, const int32_t *b_stream_starts,
+                        const int32_t *b_stream_offsets, const lct_overflow *b_overflow,
+                        const float *alpha, void *output, uint8_t *auxiliary, int64_t size,
+                        int64_t logical_numel, lct_geometry geometry, int32_t rare_length,
+                        int32_t output_policy, hipStream_t stream);
 
 /* ---- single-pass compressed-output pointwise, step 1 of 2: replaces the
  * center estimate that dispatch.py:33-48 (estimate_and_shift_encoding_table)

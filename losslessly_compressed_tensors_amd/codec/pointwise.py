@@ -225,7 +225,7 @@ def _launch_scalar_mul_add_compressed_compressed(data: CompressedTensor,
     block_symbols, lanes, steps, fixed_words = data.codec_geometry
     output, auxiliary = _allocate_outputs(data, policy)
     if data.logical_numel:
-        dispatch.dual_mapped(
+        dispatch.dual(
             data.data, data.sign_mantissa, shifted_decode_table(data), data.center,
             overlay_of(data),
             other.data, other.sign_mantissa, shifted_decode_table(other), other.center,

@@ -9,6 +9,7 @@
 // start..S-1 concatenated from byte_base, and blocks[3*nb] = {count, first,
 // byte_base} so every reader walks the list one block at a time.
 #include "allocator.h"
+#include "overflow_walk.h"
 
 namespace lct {
 namespace {
@@ -243,12 +244,113 @@ __global__ __launch_bounds__(kLanes) void compact_extra_kernel(
         start_off = arena + total;
         tail_off = arena + 2 * total;
     }
-    const int32_t *list = summaries + 4 * n_blocks;
-    const int32_t listed = summaries[5 * n_blocks];
-    for (int32_t i = blockIdx.x; i < listed; i += gridDim.x)
+    // Without summaries (block metadata from compact_bad_streams_kernel) every
+    // block is visited; the entries it rewrites are the ones already there.
+    const int32_t *list = summaries != nullptr ? summaries + 4 * n_blocks : nullptr;
+    const int64_t listed = summaries != nullptr ? summaries[5 * n_blocks] : n_blocks;
+    for (int64_t i = blockIdx.x; i < listed; i += gridDim.x) {
+        const int64_t block = list != nullptr ? list[i] : i;
+        if (list == nullptr && blocks[block] == 0) continue;   // uniform
         compact_block(source, lanes, starts, tail, lane_off, start_off, tail_off, blocks,
-                      extra_starts, list[i], n_blocks, logical_numel, S, precomputed, scratch,
+                      extra_starts, block, n_blocks, logical_numel, S, precomputed, scratch,
                       entry_offset, entry_start, entry_lane);
+    }
+}
+
+// Totals of the overflowing streams and their tail bytes, added atomically to
+// count[0] and total[0] (compaction.py:31-51: the atomic path's counts; the
+// caller zeroes both).  Each thread reads 16 streams' extra starts.
+__global__ __launch_bounds__(kLanes) void count_bad_streams_kernel(
+    const uint8_t *__restrict__ extra_starts, int32_t *__restrict__ count,
+    int32_t *__restrict__ total, int64_t n_streams, int S) {
+    __shared__ int32_t scratch[kWavesPerBlock];
+    const int64_t first = (static_cast<int64_t>(blockIdx.x) * kLanes + threadIdx.x) * 16;
+    int32_t bad = 0, bytes = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int64_t s = first + k;
+        const int32_t start = s < n_streams ? extra_starts[s] : 255;
+        bad += start != 255 ? 1 : 0;
+        bytes += start != 255 ? S - start : 0;
+    }
+    bad = block_sum(bad, scratch);
+    bytes = block_sum(bytes, scratch);
+    if (threadIdx.x == 0) {
+        if (bad != 0)
+            __hip_atomic_fetch_add(count, bad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (bytes != 0)
+            __hip_atomic_fetch_add(total, bytes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// One workgroup per codec block (compaction.py:54-96): the block reserves its
+// entry slots and tail bytes with two atomics on bad_count / fallback_total
+// (which start at 0), records {count, first, byte_base} and writes its
+// entries, lanes ascending.  Slot order across blocks follows the atomics;
+// every reader locates a block's slice through its own metadata.  Blocks
+// without overflow record first = byte_base = 0.  A buffered reservation that
+// failed (descriptor status != 0) gets its metadata but no entries.
+__global__ __launch_bounds__(kLanes) void compact_bad_streams_kernel(
+    const uint8_t *__restrict__ extra_starts, uint8_t *__restrict__ lanes,
+    uint8_t *__restrict__ starts, const int32_t *__restrict__ descriptor,
+    int32_t *__restrict__ blocks, const int32_t *__restrict__ final_counts,
+    int32_t *__restrict__ bad_count, int32_t *__restrict__ fallback_total, int64_t n_streams,
+    int64_t n_blocks, int S, int buffered) {
+    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ int32_t reserved[2];
+    const int t = threadIdx.x;
+    const int64_t block = blockIdx.x;
+    const int64_t stream = block * kLanes + t;
+    const int32_t start = stream < n_streams ? extra_starts[stream] : 255;
+    const bool bad = start != 255;
+    int32_t count;
+    const int32_t rank = block_exclusive_scan(bad ? 1 : 0, scratch, &count);
+    const int32_t bytes = block_sum(bad ? S - start : 0, scratch);
+    if (t == 0) {
+        reserved[0] = count != 0 ? __hip_atomic_fetch_add(bad_count, count, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT)
+                                 : 0;
+        reserved[1] = bytes != 0 ? __hip_atomic_fetch_add(fallback_total, bytes,
+                                                          __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT)
+                                 : 0;
+        blocks[block] = count;
+        blocks[n_blocks + block] = reserved[0];
+        blocks[2 * n_blocks + block] = reserved[1];
+    }
+    __syncthreads();
+    if (!bad) return;
+    int64_t lane_off = 0, start_off = 0;
+    if (buffered) {
+        if (descriptor[2] != kStatusOk) return;
+        lane_off = descriptor[0];
+        start_off = lane_off + final_counts[0];
+    }
+    const int64_t pos = reserved[0] + rank;
+    lanes[lane_off + pos] = static_cast<uint8_t>(t);
+    starts[start_off + pos] = static_cast<uint8_t>(start);
+}
+
+// Overflow rows of a decode made without the overlay (compaction.py:238-306):
+// every tail byte of every block, rebuilt into BF16 with its side byte and
+// written at its logical position.  A grid-stride loop over blocks.
+__global__ __launch_bounds__(kLanes) void scatter_fallback_kernel(
+    lct_overflow ov, const uint8_t *__restrict__ side, uint16_t *__restrict__ output,
+    int64_t n_blocks, int64_t logical_numel, int S) {
+    __shared__ TailEntries entries;
+    for (int64_t block = blockIdx.x; block < n_blocks; block += gridDim.x) {
+        const TailWalk w = stage_block_entries(ov, block, n_blocks, S, entries);
+        if (w.count == 0) continue;   // uniform
+        for (int32_t i = threadIdx.x; i < w.bytes; i += kLanes) {
+            int32_t step, lane;
+            tail_position(w, entries, i, step, lane);
+            const int64_t row = block * S + step;
+            const int64_t logical = row * kLanes + (lane ^ static_cast<int32_t>(row & 254));
+            if (logical < logical_numel)
+                output[logical] = static_cast<uint16_t>(pack_tail(w.tail[i], side[row * kLanes + lane]));
+        }
+        __syncthreads();   // the entries are restaged for the next block
+    }
 }
 
 }  // namespace
@@ -280,7 +382,7 @@ extern "C" int32_t lct_compact_extra(const void *source, uint8_t *lanes, uint8_t
                                      int64_t size, int64_t logical_numel, lct_geometry g,
                                      int32_t precomputed, int32_t buffered,
                                      hipStream_t stream) {
-    if (!source || !blocks || !extra_starts || !summaries) return LCT_E_NULL;
+    if (!source || !blocks || !extra_starts) return LCT_E_NULL;
     if (buffered && (!descriptor || !count || !tail)) return LCT_E_NULL;
     if (!geometry_ok(g)) return LCT_E_GEOMETRY;
     if (size <= 0 || size % g.block_symbols != 0 || logical_numel <= 0 || logical_numel > size)
@@ -291,5 +393,55 @@ extern "C" int32_t lct_compact_extra(const void *source, uint8_t *lanes, uint8_t
     hipLaunchKernelGGL(compact_extra_kernel, dim3(grid), dim3(kLanes), 0, stream, source, lanes, starts, tail, descriptor, count, blocks, base,
                        extra_starts, summaries, n_blocks, logical_numel, g.steps, precomputed,
                        buffered);
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_count_bad_streams(const uint8_t *extra_starts, int32_t *count,
+                                         int32_t *total, int64_t n_streams, int32_t steps,
+                                         hipStream_t stream) {
+    if (!extra_starts || !count || !total) return LCT_E_NULL;
+    if (n_streams <= 0 || n_streams > kMaxBlocks * kLanes) return LCT_E_SIZE;
+    if (steps != 128 && steps != 256) return LCT_E_GEOMETRY;
+    const int64_t per_group = 16 * kLanes;
+    const uint32_t grid = static_cast<uint32_t>((n_streams + per_group - 1) / per_group);
+    hipLaunchKernelGGL(count_bad_streams_kernel, dim3(grid), dim3(kLanes), 0, stream,
+                       extra_starts, count, total, n_streams, static_cast<int>(steps));
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_compact_bad_streams(const uint8_t *extra_starts, uint8_t *lanes,
+                                           uint8_t *starts, const int32_t *descriptor,
+                                           int32_t *blocks, const int32_t *final_counts,
+                                           int32_t *bad_count, int32_t *fallback_total,
+                                           int64_t n_streams, int32_t steps, int64_t n_blocks,
+                                           int32_t buffered, hipStream_t stream) {
+    if (!extra_starts || !lanes || !starts || !blocks || !bad_count || !fallback_total)
+        return LCT_E_NULL;
+    if (buffered && (!descriptor || !final_counts)) return LCT_E_NULL;
+    if (n_blocks <= 0 || n_blocks > kMaxBlocks || n_streams <= 0 || n_streams > n_blocks * kLanes)
+        return LCT_E_SIZE;
+    if (steps != 128 && steps != 256) return LCT_E_GEOMETRY;
+    hipLaunchKernelGGL(compact_bad_streams_kernel, dim3(static_cast<uint32_t>(n_blocks)),
+                       dim3(kLanes), 0, stream, extra_starts, lanes, starts, descriptor, blocks,
+                       final_counts, bad_count, fallback_total, n_streams, n_blocks,
+                       static_cast<int>(steps), buffered);
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_scatter_fallback(const lct_overflow *overflow, const uint8_t *side,
+                                        void *output, int64_t size, int64_t logical_numel,
+                                        lct_geometry g, hipStream_t stream) {
+    if (!overflow || !side || !output) return LCT_E_NULL;
+    if (!overflow->lanes || !overflow->starts || !overflow->tail || !overflow->blocks)
+        return LCT_E_NULL;
+    if (overflow->descriptor != nullptr && overflow->count == nullptr) return LCT_E_NULL;
+    if (!geometry_ok(g)) return LCT_E_GEOMETRY;
+    if (size <= 0 || size % g.block_symbols != 0 || logical_numel <= 0 || logical_numel > size)
+        return LCT_E_SIZE;
+    const int64_t n_blocks = size / g.block_symbols;
+    if (n_blocks > kMaxBlocks) return LCT_E_SIZE;
+    const uint32_t grid = static_cast<uint32_t>(n_blocks < kCompactGrid ? n_blocks : kCompactGrid);
+    hipLaunchKernelGGL(scatter_fallback_kernel, dim3(grid), dim3(kLanes), 0, stream, *overflow,
+                       side, static_cast<uint16_t *>(output), n_blocks, logical_numel, g.steps);
     return static_cast<int32_t>(hipGetLastError());
 }

@@ -16,6 +16,7 @@
 // fma(b, beta, a) when alpha is one); the result is rounded to BF16 to
 // nearest-even.  Compressed output: side byte at the storage offset (0 for
 // padding), exponent byte at the logical offset.
+#include "overflow_walk.h"
 #include "pointwise_ops.h"
 
 namespace lct {
@@ -293,7 +294,37 @@ struct DualOperand {
     const int32_t *center;
     lct_overflow ov;
     int32_t has_overlay;
+    // Per-stream maps from dual_tables_and_maps_kernel (start step, tail byte
+    // offset from the tail base), or NULL: the overlay is built from the
+    // compact list in the prologue.
+    const int32_t *map_start;
+    const int32_t *map_offset;
 };
+
+// Tail bytes of a tensor's overflow storage start here (the arena region
+// after the entries when buffered); NULL when the tensor has no tails (no
+// overlay, or a buffered reservation that failed).
+__device__ __forceinline__ const uint8_t *tail_base_of(const lct_overflow &ov, bool present) {
+    if (!present) return nullptr;
+    if (ov.descriptor == nullptr) return ov.tail + ov.base;
+    if (ov.descriptor[2] != 0) return nullptr;
+    return ov.tail + ov.descriptor[0] + 2 * static_cast<int64_t>(ov.count[0]);
+}
+
+// This lane's overlay from the per-stream maps
+// (LCT/kernels/generic/pointwise_scalar_dual.py:33-113 writes them).
+__device__ __forceinline__ LaneOverlay overlay_from_maps(const DualOperand &x, int64_t block,
+                                                         int S) {
+    LaneOverlay lane{nullptr, S, 0, S, 0};
+    const uint8_t *tails = tail_base_of(x.ov, x.has_overlay != 0);
+    if (tails == nullptr) return lane;   // uniform
+    const int64_t stream = block * kLanes + threadIdx.x;
+    lane.tail = tails;
+    lane.start = x.map_start[stream];
+    lane.offset = x.map_offset[stream];
+    lane.wave_start = __builtin_amdgcn_readfirstlane(wave_min(lane.start));
+    return lane;
+}
 
 __global__ __launch_bounds__(kLanes) void dual_kernel(DualOperand a, DualOperand b,
                                                       const float *__restrict__ alpha,
@@ -310,11 +341,17 @@ __global__ __launch_bounds__(kLanes) void dual_kernel(DualOperand a, DualOperand
     build_decode_tables(tb_b, b.shifted_decode, b.center[0]);
     stage_payload(stage_a, a.encoded, n_blocks * kLanes, block, W);
     stage_payload(stage_b, b.encoded, n_blocks * kLanes, block, W);
-    const LaneOverlay a_lane = build_overlay(a.ov, a.has_overlay != 0, block, n_blocks, S,
-                                             map_start, map_offset, scratch, nullptr, 0);
+    // build_overlay returns the tail pointer relative to the tail base of the
+    // compact list's byte offsets; the maps carry the same offsets.
+    const LaneOverlay a_lane = a.map_start != nullptr
+        ? overlay_from_maps(a, block, S)
+        : build_overlay(a.ov, a.has_overlay != 0, block, n_blocks, S, map_start, map_offset,
+                        scratch, nullptr, 0);
     __syncthreads();
-    const LaneOverlay b_lane = build_overlay(b.ov, b.has_overlay != 0, block, n_blocks, S,
-                                             map_start, map_offset, scratch, nullptr, 0);
+    const LaneOverlay b_lane = b.map_start != nullptr
+        ? overlay_from_maps(b, block, S)
+        : build_overlay(b.ov, b.has_overlay != 0, block, n_blocks, S, map_start, map_offset,
+                        scratch, nullptr, 0);
     wait_memory();
     __syncthreads();
 
@@ -348,6 +385,110 @@ __global__ __launch_bounds__(kLanes) void dual_kernel(DualOperand a, DualOperand
         else { LCT_DUAL_CASE(false, LCT_COMPRESSED_OUTPUT) }
     }
 #undef LCT_DUAL_CASE
+}
+
+// Overflow rows of a pointwise result computed without the overlay
+// (LCT/kernels/generic/pointwise.py:265-340): every tail byte of A is rebuilt
+// into BF16 with its side byte, combined with B at its logical position and
+// stored as pointwise_kernel stores results (_store_result, pointwise.py:44-65:
+// dense BF16 at logical positions, or the side byte at the storage position
+// and the exponent byte at the logical position, padding positions giving 0).
+__global__ __launch_bounds__(kLanes) void pointwise_fallback_kernel(
+    lct_overflow ov, const uint8_t *__restrict__ side, const uint16_t *__restrict__ other,
+    void *__restrict__ output, uint8_t *__restrict__ auxiliary, const float *__restrict__ alpha,
+    const float *__restrict__ beta, int64_t n_blocks, int64_t logical_numel, int S, int32_t op,
+    int32_t alpha_is_one, int32_t beta_is_one, int32_t policy) {
+    __shared__ TailEntries entries;
+    const OpParams p = load_op_params(op, alpha_is_one, beta_is_one, alpha, beta);
+    for (int64_t block = blockIdx.x; block < n_blocks; block += gridDim.x) {
+        const TailWalk w = stage_block_entries(ov, block, n_blocks, S, entries);
+        if (w.count == 0) continue;   // uniform
+        for (int32_t i = threadIdx.x; i < w.bytes; i += kLanes) {
+            int32_t step, lane;
+            tail_position(w, entries, i, step, lane);
+            const int64_t row = block * S + step;
+            const int64_t storage = row * kLanes + lane;
+            const int64_t logical = row * kLanes + (lane ^ static_cast<int32_t>(row & 254));
+            const bool valid = logical < logical_numel;
+            const uint32_t a = pack_tail(w.tail[i], side[storage]);
+            const uint32_t r = valid ? apply_op(p, a, other[logical]) : 0u;
+            if (policy == LCT_DENSE_OUTPUT) {
+                if (valid) static_cast<uint16_t *>(output)[logical] = static_cast<uint16_t>(r);
+            } else {
+                static_cast<uint8_t *>(output)[storage] =
+                    static_cast<uint8_t>((r & 0x7Fu) | ((r >> 8) & 0x80u));
+                if (valid) auxiliary[logical] = static_cast<uint8_t>((r >> 7) & 0xFFu);
+            }
+        }
+        __syncthreads();   // the entries are restaged for the next block
+    }
+}
+
+// Both operands' per-stream maps set to "no overflow": start S, offset 0
+// (pointwise_scalar_dual.py:17-30).
+__global__ __launch_bounds__(kLanes) void dual_maps_init_kernel(int32_t *__restrict__ a_start,
+                                                                int32_t *__restrict__ a_offset,
+                                                                int32_t *__restrict__ b_start,
+                                                                int32_t *__restrict__ b_offset,
+                                                                int64_t n_streams, int S) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kLanes + threadIdx.x; i < n_streams;
+         i += static_cast<int64_t>(gridDim.x) * kLanes) {
+        a_start[i] = S;
+        b_start[i] = S;
+        a_offset[i] = 0;
+        b_offset[i] = 0;
+    }
+}
+
+// One operand's entries of one block into its per-stream maps: start step
+// and tail byte offset (from the tail base) of every overflowing stream.
+__device__ __forceinline__ void scatter_block_maps(const lct_overflow &ov, bool present,
+                                                   int64_t block, int64_t n_blocks, int S,
+                                                   int32_t *map_start, int32_t *map_offset,
+                                                   int32_t *scratch) {
+    if (tail_base_of(ov, present) == nullptr) return;   // uniform
+    const int32_t count = ov.blocks[block];
+    if (count <= 0) return;
+    int64_t lane_off = 0, start_off = 0;
+    if (ov.descriptor != nullptr) {
+        lane_off = ov.descriptor[0];
+        start_off = lane_off + ov.count[0];
+    }
+    const int32_t first = ov.blocks[n_blocks + block];
+    const int32_t byte_base = ov.blocks[2 * n_blocks + block];
+    const int t = threadIdx.x;
+    const bool valid = t < count;
+    const int32_t start = valid ? static_cast<int32_t>(ov.starts[start_off + first + t]) : S;
+    const int32_t lane = valid ? static_cast<int32_t>(ov.lanes[lane_off + first + t]) : 0;
+    int32_t total;
+    const int32_t local = block_exclusive_scan(valid ? S - start : 0, scratch, &total);
+    if (valid) {
+        map_start[block * kLanes + lane] = start;
+        map_offset[block * kLanes + lane] = byte_base + local;
+    }
+}
+
+// pointwise_scalar_dual.py:33-113: workgroups 0 and 1 shift A's and B's
+// decode tables by their centers; workgroup 2 + k expands block k's compact
+// overflow lists of both operands into the per-stream maps.
+__global__ __launch_bounds__(kLanes) void dual_tables_and_maps_kernel(
+    const int32_t *__restrict__ a_base_decode, const int32_t *__restrict__ a_center,
+    int32_t *__restrict__ a_shifted, const int32_t *__restrict__ b_base_decode,
+    const int32_t *__restrict__ b_center, int32_t *__restrict__ b_shifted, lct_overflow a_ov,
+    int32_t a_present, lct_overflow b_ov, int32_t b_present, int32_t *__restrict__ a_start,
+    int32_t *__restrict__ a_offset, int32_t *__restrict__ b_start, int32_t *__restrict__ b_offset,
+    int64_t n_blocks, int S) {
+    __shared__ int32_t scratch[kWavesPerBlock];
+    if (blockIdx.x < 2) {
+        const int32_t *base = blockIdx.x == 0 ? a_base_decode : b_base_decode;
+        const int32_t center = blockIdx.x == 0 ? a_center[0] : b_center[0];
+        int32_t *out = blockIdx.x == 0 ? a_shifted : b_shifted;
+        for (int i = threadIdx.x; i < 1024; i += kLanes) out[i] = shifted_decode_entry(base[i], center);
+        return;
+    }
+    const int64_t block = blockIdx.x - 2;
+    scatter_block_maps(a_ov, a_present != 0, block, n_blocks, S, a_start, a_offset, scratch);
+    scatter_block_maps(b_ov, b_present != 0, block, n_blocks, S, b_start, b_offset, scratch);
 }
 
 int32_t check_overflow(const lct_overflow *o) {
@@ -421,9 +562,114 @@ extern "C" int32_t lct_dual(const int32_t *a_encoded, const uint8_t *a_side,
     if (((reinterpret_cast<uintptr_t>(a_encoded) | reinterpret_cast<uintptr_t>(b_encoded)) & 15) != 0)
         return LCT_E_ARG;
     const DualOperand a{a_encoded, a_side, a_shifted_decode, a_center,
-                        a_overflow ? *a_overflow : lct_overflow{}, a_overflow != nullptr};
+                        a_overflow ? *a_overflow : lct_overflow{}, a_overflow != nullptr,
+                        nullptr, nullptr};
     const DualOperand b{b_encoded, b_side, b_shifted_decode, b_center,
-                        b_overflow ? *b_overflow : lct_overflow{}, b_overflow != nullptr};
+                        b_overflow ? *b_overflow : lct_overflow{}, b_overflow != nullptr,
+                        nullptr, nullptr};
+    const int64_t n_blocks = size / g.block_symbols;
+    const size_t lds = 2 * static_cast<size_t>(stage_bytes(g.fixed_words));
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&dual_kernel), lds))
+        return static_cast<int32_t>(e);
+    hipLaunchKernelGGL(dual_kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes), lds,
+                       stream, a, b, alpha, output, auxiliary, n_blocks, logical_numel, g.steps,
+                       g.fixed_words, rare_length, output_policy);
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_pointwise_fallback(const lct_overflow *overflow, const uint8_t *side,
+                                          const void *other, void *output, uint8_t *auxiliary,
+                                          const float *alpha, const float *beta, int64_t size,
+                                          int64_t logical_numel, lct_geometry g, int32_t op,
+                                          int32_t alpha_is_one, int32_t beta_is_one,
+                                          int32_t output_policy, hipStream_t stream) {
+    if (!overflow || !side || !other || !output) return LCT_E_NULL;
+    if (output_policy == LCT_COMPRESSED_OUTPUT && !auxiliary) return LCT_E_NULL;
+    if (op == LCT_OP_SCALAR_MUL_ADD && ((!alpha_is_one && !alpha) || (!beta_is_one && !beta)))
+        return LCT_E_NULL;
+    if (int32_t e = check_overflow(overflow)) return e;
+    if (int32_t e = check_sizes(size, logical_numel, g)) return e;
+    if (op < LCT_OP_ADD || op > LCT_OP_SCALAR_MUL_ADD) return LCT_E_ARG;
+    if (output_policy != LCT_DENSE_OUTPUT && output_policy != LCT_COMPRESSED_OUTPUT) return LCT_E_ARG;
+    const int64_t n_blocks = size / g.block_symbols;
+    const uint32_t grid = static_cast<uint32_t>(n_blocks < 2048 ? n_blocks : 2048);
+    hipLaunchKernelGGL(pointwise_fallback_kernel, dim3(grid), dim3(kLanes), 0, stream, *overflow,
+                       side, static_cast<const uint16_t *>(other), output, auxiliary, alpha, beta,
+                       n_blocks, logical_numel, g.steps, op, alpha_is_one, beta_is_one,
+                       output_policy);
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_dual_maps_init(int32_t *a_stream_starts, int32_t *a_stream_offsets,
+                                      int32_t *b_stream_starts, int32_t *b_stream_offsets,
+                                      int64_t n_streams, int32_t steps, hipStream_t stream) {
+    if (!a_stream_starts || !a_stream_offsets || !b_stream_starts || !b_stream_offsets)
+        return LCT_E_NULL;
+    if (n_streams <= 0 || n_streams > kMaxBlocks * kLanes) return LCT_E_SIZE;
+    if (steps != 128 && steps != 256) return LCT_E_GEOMETRY;
+    const int64_t groups = (n_streams + kLanes - 1) / kLanes;
+    const uint32_t grid = static_cast<uint32_t>(groups < 4096 ? groups : 4096);
+    hipLaunchKernelGGL(dual_maps_init_kernel, dim3(grid), dim3(kLanes), 0, stream,
+                       a_stream_starts, a_stream_offsets, b_stream_starts, b_stream_offsets,
+                       n_streams, static_cast<int>(steps));
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_dual_tables_and_maps(
+    const int32_t *a_base_decode, const int32_t *a_center, int32_t *a_shifted_decode,
+    const int32_t *b_base_decode, const int32_t *b_center, int32_t *b_shifted_decode,
+    const lct_overflow *a_overflow, const lct_overflow *b_overflow, int32_t *a_stream_starts,
+    int32_t *a_stream_offsets, int32_t *b_stream_starts, int32_t *b_stream_offsets,
+    int64_t n_blocks, int32_t steps, hipStream_t stream) {
+    if (!a_base_decode || !a_center || !a_shifted_decode || !b_base_decode || !b_center
+        || !b_shifted_decode || !a_stream_starts || !a_stream_offsets || !b_stream_starts
+        || !b_stream_offsets)
+        return LCT_E_NULL;
+    if (int32_t e = check_overflow(a_overflow)) return e;
+    if (int32_t e = check_overflow(b_overflow)) return e;
+    if (n_blocks <= 0 || n_blocks > kMaxBlocks) return LCT_E_SIZE;
+    if (steps != 128 && steps != 256) return LCT_E_GEOMETRY;
+    hipLaunchKernelGGL(dual_tables_and_maps_kernel, dim3(static_cast<uint32_t>(n_blocks + 2)),
+                       dim3(kLanes), 0, stream, a_base_decode, a_center, a_shifted_decode,
+                       b_base_decode, b_center, b_shifted_decode,
+                       a_overflow ? *a_overflow : lct_overflow{}, a_overflow != nullptr ? 1 : 0,
+                       b_overflow ? *b_overflow : lct_overflow{}, b_overflow != nullptr ? 1 : 0,
+                       a_stream_starts, a_stream_offsets, b_stream_starts, b_stream_offsets,
+                       n_blocks, static_cast<int>(steps));
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_dual_mapped(
+    const int32_t *a_encoded, const uint8_t *a_side, const int32_t *a_shifted_decode,
+    const int32_t *a_center, const int32_t *a_stream_starts, const int32_t *a_stream_offsets,
+    const lct_overflow *a_overflow, const int32_t *b_encoded, const uint8_t *b_side,
+    const int32_t *b_shifted_decode, const int32_t *b_center, const int32_t *b_stream_starts,
+    const int32_t *b_stream_offsets, const lct_overflow *b_overflow, const float *alpha,
+    void *output, uint8_t *auxiliary, int64_t size, int64_t logical_numel, lct_geometry g,
+    int32_t rare_length, int32_t output_policy, hipStream_t stream) {
+    if (!a_encoded || !a_side || !a_shifted_decode || !a_center || !b_encoded || !b_side
+        || !b_shifted_decode || !b_center || !alpha || !output)
+        return LCT_E_NULL;
+    if ((a_overflow && (!a_stream_starts || !a_stream_offsets))
+        || (b_overflow && (!b_stream_starts || !b_stream_offsets)))
+        return LCT_E_NULL;
+    if (output_policy == LCT_COMPRESSED_OUTPUT && !auxiliary) return LCT_E_NULL;
+    if (int32_t e = check_sizes(size, logical_numel, g)) return e;
+    if (int32_t e = check_overflow(a_overflow)) return e;
+    if (int32_t e = check_overflow(b_overflow)) return e;
+    if (output_policy != LCT_DENSE_OUTPUT && output_policy != LCT_COMPRESSED_OUTPUT) return LCT_E_ARG;
+    if (rare_length < 0 || rare_length > 8) return LCT_E_ARG;
+    if (((reinterpret_cast<uintptr_t>(a_encoded) | reinterpret_cast<uintptr_t>(b_encoded)) & 15) != 0)
+        return LCT_E_ARG;
+    // An operand without overflow storage reads no maps (its overlay is off).
+    const DualOperand a{a_encoded, a_side, a_shifted_decode, a_center,
+                        a_overflow ? *a_overflow : lct_overflow{}, a_overflow != nullptr,
+                        a_overflow ? a_stream_starts : nullptr,
+                        a_overflow ? a_stream_offsets : nullptr};
+    const DualOperand b{b_encoded, b_side, b_shifted_decode, b_center,
+                        b_overflow ? *b_overflow : lct_overflow{}, b_overflow != nullptr,
+                        b_overflow ? b_stream_starts : nullptr,
+                        b_overflow ? b_stream_offsets : nullptr};
     const int64_t n_blocks = size / g.block_symbols;
     const size_t lds = 2 * static_cast<size_t>(stage_bytes(g.fixed_words));
     if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&dual_kernel), lds))

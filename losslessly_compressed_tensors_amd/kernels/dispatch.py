@@ -30,6 +30,14 @@ def _stream(tensor: torch.Tensor) -> int:
     return torch.cuda.current_stream(tensor.device).cuda_stream
 
 
+def _byref(storage: FallbackStorage | None):
+    """The storage as a C-ABI overflow argument, or None when it holds no
+    entries: absent, or private with exact-size arrays of length 0."""
+    if storage is None or (not storage.buffered and storage.lanes.numel() == 0):
+        return None
+    return hip.ctypes.byref(storage.as_overflow())
+
+
 def _require_device(*tensors: torch.Tensor) -> None:
     for tensor in tensors:
         if tensor is not None and tensor.device.type != "cuda":
@@ -153,11 +161,37 @@ def prefix_allocate(summaries, counts, descriptor, buffer, blocks_out, blocks, b
              _stream(summaries))
 
 
+def count_bad_streams(extra_starts, count, total, streams, steps) -> None:
+    """Atomic-path totals (``dispatch.py:88-95``): adds the overflowing
+    streams and their tail bytes to ``count[0]`` and ``total[0]`` (zeroed by
+    the caller)."""
+    _require_device(extra_starts, count, total)
+    hip.call("lct_count_bad_streams", _ptr(extra_starts), _ptr(count), _ptr(total),
+             int(streams), int(steps), _stream(extra_starts))
+
+
+def compact_bad_streams(extra_starts, storage: FallbackStorage, final_counts, bad_count,
+                        fallback_total, n_streams, steps, n_blocks, buffered, lanes) -> None:
+    """Atomic-path entries and block metadata (``dispatch.py:98-110``): each
+    block reserves its slice with atomics on ``bad_count``/``fallback_total``
+    (zeroed by the caller); ``compact_extra(..., summaries=None)`` then writes
+    the tails."""
+    _require_device(extra_starts, storage.blocks, bad_count, fallback_total)
+    if lanes != 256:
+        raise ValueError("LCT streams have 256 lanes per block")
+    hip.call("lct_compact_bad_streams", _ptr(extra_starts), _ptr(storage.lanes),
+             _ptr(storage.starts), _ptr(storage.descriptor), _ptr(storage.blocks),
+             _ptr(final_counts), _ptr(bad_count), _ptr(fallback_total), int(n_streams),
+             int(steps), int(n_blocks), int(bool(buffered)), _stream(extra_starts))
+
+
 def compact_extra(source, storage: FallbackStorage, n_blocks, n_elements, *, precomputed,
                   buffered, logical_numel, block_symbols, lanes, steps, extra_starts,
                   summaries) -> None:
-    """Overflow entries and tails of the listed blocks (``dispatch.py:113-130``)."""
-    _require_device(source, extra_starts, summaries)
+    """Overflow entries and tails (``dispatch.py:113-130``): of the blocks
+    ``prefix_allocate`` listed, or, with ``summaries=None``, of every block
+    whose metadata ``compact_bad_streams`` wrote."""
+    _require_device(source, extra_starts)
     geometry = hip.Geometry(block_symbols, lanes, steps, 2)
     hip.call("lct_compact_extra", _ptr(source), _ptr(storage.lanes), _ptr(storage.starts),
              _ptr(storage.tail), _ptr(storage.descriptor), _ptr(storage.count),
@@ -183,6 +217,36 @@ def decode_kernel(encoded, side, output, shifted_decode, center, size, *, logica
              ov if ov is None else hip.ctypes.byref(ov), _stream(encoded))
 
 
+def scatter_fallback(storage: FallbackStorage, sign_mantissa, output, n_elements,
+                     logical_numel, block_symbols, lanes, steps) -> None:
+    """Overflow rows of a decode made without the overlay
+    (``dispatch.py:146-165``)."""
+    _require_device(sign_mantissa, output)
+    overflow = _byref(storage)
+    if overflow is None:
+        return
+    geometry = hip.Geometry(block_symbols, lanes, steps, 2)
+    hip.call("lct_scatter_fallback", overflow, _ptr(sign_mantissa), _ptr(output),
+             int(n_elements), int(logical_numel), geometry, _stream(sign_mantissa))
+
+
+def pointwise_fallback(storage: FallbackStorage, sign_mantissa, other, output, auxiliary,
+                       n_elements, alpha, beta, *, logical_numel, block_symbols, lanes, steps,
+                       output_policy, op, alpha_is_one, beta_is_one) -> None:
+    """Overflow rows of a pointwise result computed without the overlay
+    (``dispatch.py:190-212``); the operation's flags are the reference's
+    ``operation_meta`` (OP, ALPHA_IS_ONE, BETA_IS_ONE) as plain arguments."""
+    _require_device(sign_mantissa, other, output)
+    overflow = _byref(storage)
+    if overflow is None:
+        return
+    geometry = hip.Geometry(block_symbols, lanes, steps, 2)
+    hip.call("lct_pointwise_fallback", overflow, _ptr(sign_mantissa), _ptr(other),
+             _ptr(output), _ptr(auxiliary), _ptr(alpha), _ptr(beta), int(n_elements),
+             int(logical_numel), geometry, int(op), int(bool(alpha_is_one)),
+             int(bool(beta_is_one)), int(output_policy), _stream(sign_mantissa))
+
+
 def pointwise_dense(encoded, sign_mantissa, other, output, auxiliary, shifted_decode, size,
                     center, alpha, beta, *, rare_length, logical_numel, block_symbols, lanes,
                     steps, fixed_words, output_policy, op, alpha_is_one, beta_is_one,
@@ -198,11 +262,13 @@ def pointwise_dense(encoded, sign_mantissa, other, output, auxiliary, shifted_de
              ov if ov is None else hip.ctypes.byref(ov), _stream(encoded))
 
 
-def dual_mapped(a_encoded, a_sign_mantissa, a_shifted_decode, a_center, a_storage,
-                b_encoded, b_sign_mantissa, b_shifted_decode, b_center, b_storage,
-                output, auxiliary, alpha, size, *, rare_length, logical_numel,
-                block_symbols, lanes, steps, fixed_words, output_policy) -> None:
-    """Fused ``alpha * A + B`` over two compressed operands (one launch)."""
+def dual(a_encoded, a_sign_mantissa, a_shifted_decode, a_center, a_storage,
+         b_encoded, b_sign_mantissa, b_shifted_decode, b_center, b_storage,
+         output, auxiliary, alpha, size, *, rare_length, logical_numel,
+         block_symbols, lanes, steps, fixed_words, output_policy) -> None:
+    """Fused ``alpha * A + B`` over two compressed operands: the reference's
+    ``dual_maps_init`` + ``dual_tables_and_maps`` + ``dual_mapped``
+    (``dispatch.py:215-286``) in one launch."""
     _require_device(a_encoded, b_encoded, output, alpha)
     geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
     a_ov = a_storage.as_overflow() if a_storage is not None else None
@@ -213,6 +279,49 @@ def dual_mapped(a_encoded, a_sign_mantissa, a_shifted_decode, a_center, a_storag
              b_ov if b_ov is None else hip.ctypes.byref(b_ov), _ptr(alpha), _ptr(output),
              _ptr(auxiliary), int(size), int(logical_numel), geometry, int(rare_length),
              int(output_policy), _stream(a_encoded))
+
+
+def dual_maps_init(a_stream_starts, a_stream_offsets, b_stream_starts, b_stream_offsets,
+                   a_count, b_count, n_streams, steps) -> None:
+    """Both operands' per-stream maps to "no overflow" (``dispatch.py:215-225``;
+    the counts are not needed to initialise them)."""
+    _require_device(a_stream_starts, b_stream_starts)
+    hip.call("lct_dual_maps_init", _ptr(a_stream_starts), _ptr(a_stream_offsets),
+             _ptr(b_stream_starts), _ptr(b_stream_offsets), int(n_streams), int(steps),
+             _stream(a_stream_starts))
+
+
+def dual_tables_and_maps(a_decode_table, a_center, a_shifted, b_decode_table, b_center,
+                         b_shifted, a_storage, b_storage, a_stream_starts, a_stream_offsets,
+                         b_stream_starts, b_stream_offsets, blocks, *, lanes, steps,
+                         buffered) -> None:
+    """Shift both decode tables and expand both compact overflow lists into
+    the per-stream maps (``dispatch.py:228-252``)."""
+    _require_device(a_decode_table, b_decode_table, a_stream_starts, b_stream_starts)
+    if lanes != 256:
+        raise ValueError("LCT streams have 256 lanes per block")
+    hip.call("lct_dual_tables_and_maps", _ptr(a_decode_table), _ptr(a_center), _ptr(a_shifted),
+             _ptr(b_decode_table), _ptr(b_center), _ptr(b_shifted), _byref(a_storage),
+             _byref(b_storage), _ptr(a_stream_starts), _ptr(a_stream_offsets),
+             _ptr(b_stream_starts), _ptr(b_stream_offsets), int(blocks), int(steps),
+             _stream(a_decode_table))
+
+
+def dual_mapped(a_encoded, a_sign_mantissa, a_shifted, a_center, a_stream_starts,
+                a_stream_offsets, a_storage, b_encoded, b_sign_mantissa, b_shifted, b_center,
+                b_stream_starts, b_stream_offsets, b_storage, output, auxiliary, alpha,
+                n_elements, n_streams, blocks, *, rare_length, logical_numel, buffered,
+                block_symbols, lanes, steps, fixed_words, output_policy) -> None:
+    """``alpha * A + B`` with each operand's overlay read from its per-stream
+    maps (``dispatch.py:255-286``)."""
+    _require_device(a_encoded, b_encoded, output, alpha)
+    geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
+    hip.call("lct_dual_mapped", _ptr(a_encoded), _ptr(a_sign_mantissa), _ptr(a_shifted),
+             _ptr(a_center), _ptr(a_stream_starts), _ptr(a_stream_offsets), _byref(a_storage),
+             _ptr(b_encoded), _ptr(b_sign_mantissa), _ptr(b_shifted), _ptr(b_center),
+             _ptr(b_stream_starts), _ptr(b_stream_offsets), _byref(b_storage), _ptr(alpha),
+             _ptr(output), _ptr(auxiliary), int(n_elements), int(logical_numel), geometry,
+             int(rare_length), int(output_policy), _stream(a_encoded))
 
 
 def pointwise_sample(encoded, sign_mantissa, shifted_decode, center, other, alpha, beta,
@@ -254,11 +363,6 @@ def pointwise_encode(encoded, sign_mantissa, shifted_decode, center, other, alph
              _ptr(extra_starts), _ptr(summaries), _ptr(exponents), int(size),
              int(logical_numel), geometry, int(rare_length), int(op), int(bool(alpha_is_one)),
              int(bool(beta_is_one)), _stream(encoded))
-
-
-def _byref(storage: FallbackStorage | None):
-    ov = storage.as_overflow() if storage is not None else None
-    return ov if ov is None else hip.ctypes.byref(ov)
 
 
 def dual_sample(a_encoded, a_sign_mantissa, a_shifted_decode, a_center, a_storage, b_encoded,

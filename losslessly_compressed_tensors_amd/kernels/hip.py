@@ -84,6 +84,21 @@ _SIGNATURES = {
                         _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _c_int64, _ptr, _ptr, _ptr,
                         _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64, _c_int64, Geometry,
                         _c_int32, _ptr],
+    "lct_count_bad_streams": [_ptr, _ptr, _ptr, _c_int64, _c_int32, _ptr],
+    "lct_compact_bad_streams": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64,
+                                _c_int32, _c_int64, _c_int32, _ptr],
+    "lct_scatter_fallback": [ctypes.POINTER(Overflow), _ptr, _ptr, _c_int64, _c_int64, Geometry,
+                             _ptr],
+    "lct_pointwise_fallback": [ctypes.POINTER(Overflow), _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
+                               _c_int64, _c_int64, Geometry, _c_int32, _c_int32, _c_int32,
+                               _c_int32, _ptr],
+    "lct_dual_maps_init": [_ptr, _ptr, _ptr, _ptr, _c_int64, _c_int32, _ptr],
+    "lct_dual_tables_and_maps": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, ctypes.POINTER(Overflow),
+                                 ctypes.POINTER(Overflow), _ptr, _ptr, _ptr, _ptr, _c_int64,
+                                 _c_int32, _ptr],
+    "lct_dual_mapped": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr,
+                        _ptr, _ptr, _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _ptr,
+                        _c_int64, _c_int64, Geometry, _c_int32, _c_int32, _ptr],
     "lct_buffer_reset": [_ptr, _c_int32, _c_int32, _ptr],
     "lct_buffer_allocate": [_ptr, _c_int32, _ptr, _ptr, _c_int32, _ptr, _ptr],
     "lct_buffer_free": [_ptr, _c_int32, _ptr, _ptr, _ptr],
