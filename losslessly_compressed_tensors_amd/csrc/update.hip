@@ -197,60 +197,74 @@ __global__ __launch_bounds__(kSampleGroup) void pointwise_sample_kernel(
 constexpr uint32_t kOutOfRange = 0x80000000u;
 
 // Encoder state of one lane's output stream.  Word r of the stream is at byte
-// r * row_bytes + 4 * lane of the block's payload resource.  Once a pair does
-// not fit, pos is parked at limit + 1: every later pair then overflows too and
-// stores nothing (encode.py:73-90: only the first overflowing pair matters).
+// r * row_bytes + 4 * lane of the block's payload resource.  pos counts the
+// bits of every pair so far, so once a pair does not fit, pos stays above the
+// limit and every later pair overflows too (encode.py:73-90: only the first
+// overflowing pair matters); word and row_off then keep the bits before that
+// pair, which finish() stores.
 struct StreamWriter {
     __amdgpu_buffer_rsrc_t out;
     uint32_t row_bytes;   // 4 * n_streams
-    uint32_t row_off;     // byte offset of the word at row pos / 32
+    uint32_t row_off;     // byte offset of the word being filled
+    uint32_t end_off;     // row_off of row W
     uint32_t limit;       // 32 W
-    uint32_t pos;         // bits emitted; limit + 1 after an overflow
-    uint32_t word;        // bits of the word at row pos / 32 so far
-    int32_t extra;        // the first pair that did not fit (its even step)
+    uint32_t pos;         // bits of all pairs so far
+    uint32_t word;        // bits of the word being filled
+    uint32_t fits;        // pairs that fit
 
     __device__ __forceinline__ bool overflowed() const { return pos > limit; }
 
-    // Append the pair code of encode entries e0/e1 (reversed code in bits
-    // 0..15, length in 16..20; 0 = no code) for the pair at `step`, following
-    // encode.py:66-90.  Returns whether the pair (and so every later one)
-    // overflows.  One store per pair: the word this pair completes, or, at the
-    // stream's first pair that does not fit, the bits before it (unless the
-    // stream is exactly full).
-    __device__ __forceinline__ bool put(uint32_t e0, uint32_t e1, int step) {
-        const uint32_t len0 = e0 >> 16;
-        const uint32_t code = (e0 & 0xFFFFu) | ((e1 & 0xFFFFu) << len0);
-        const uint32_t len = len0 + (e1 >> 16);
+    // The first pair that did not fit is the one after the pairs that fit, so
+    // its (even) step is twice their count.
+    __device__ __forceinline__ int32_t extra_start() const { return static_cast<int32_t>(2 * fits); }
+
+    // Append the pair code of encode entries e0/e1 ({reversed code, length};
+    // {0, 0} = no code), following encode.py:66-90.  Returns whether the pair
+    // (and so every later one) overflows.  A pair that completes a word
+    // stores it.
+    __device__ __forceinline__ bool put(uint2 e0, uint2 e1) {
+        const uint32_t code = e0.x | (e1.x << e0.y);
+        const uint32_t len = e0.y + e1.y;
         const uint32_t shift = pos & 31u;
         const uint64_t placed = static_cast<uint64_t>(code) << shift;
         const uint32_t new_word = word | static_cast<uint32_t>(placed);
         const uint32_t after = pos + len;
-        const bool over = after > limit;
-        const bool completes = shift + len >= 32u;
-        const bool write = over ? pos < limit : completes;
-        __builtin_amdgcn_raw_buffer_store_b32(over ? word : new_word, out,
-                                              write ? row_off : kOutOfRange, 0, 0);
-        extra = over && pos <= limit ? step : extra;
+        const bool ok = after <= limit;
+        const bool completes = ok && shift + len >= 32u;
+        __builtin_amdgcn_raw_buffer_store_b32(new_word, out, completes ? row_off : kOutOfRange,
+                                              0, 0);
         row_off += completes ? row_bytes : 0u;
-        word = completes ? static_cast<uint32_t>(placed >> 32) : new_word;
-        pos = over ? limit + 1u : after;
-        return over;
+        word = ok ? (completes ? static_cast<uint32_t>(placed >> 32) : new_word) : word;
+        fits += ok ? 1u : 0u;
+        pos = after;
+        return !ok;
     }
 
-    // After the last pair: the partial word, then zero words up to row W-1.
+    // After the last pair: the word being filled (the bits before the first
+    // pair that did not fit, for an overflowing stream), then zero words up to
+    // row W-1.
     __device__ __forceinline__ void finish() {
-        for (uint32_t r = pos; r < limit; r += 32u) {
+        for (; row_off < end_off; row_off += row_bytes) {
             __builtin_amdgcn_raw_buffer_store_b32(word, out, row_off, 0, 0);
             word = 0u;
-            row_off += row_bytes;
         }
     }
 };
 
-// Encode-table entry repacked for the kernel: reversed code (<= 16 bits) in
-// bits 0..15, code length in bits 16..20 (shifted tables: tables.py:53-67).
-__device__ __forceinline__ uint32_t repack_encode_entry(uint32_t packed) {
-    return (packed & 0xFFFFu) | ((packed >> 20) << 16);
+// Encode-table entry as the kernel keeps it in LDS: {reversed code (<= 16
+// bits), code length}, 8 bytes, so one 8-byte read gives both without masks
+// (shifted tables: tables.py:53-67).
+__device__ __forceinline__ uint2 repack_encode_entry(uint32_t packed) {
+    return make_uint2(packed & 0xFFFFu, packed >> 20);
+}
+
+// The side byte of a high-half BF16 result in bits 16..23: the mantissa stays
+// in bits 16..22 and the sign comes down from bit 31 (one v_bfi_b32 after a
+// shift; the compiler otherwise builds it from three instructions).
+__device__ __forceinline__ uint32_t side_byte_at_16(uint32_t h) {
+    uint32_t out;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(out) : "s"(0x007F0000u), "v"(h), "v"(h >> 8));
+    return out;
 }
 
 struct UpdateIo {
@@ -277,19 +291,18 @@ __device__ __forceinline__ void fetch_b_chunk(uint32_t (&bw)[kChunkSteps / 2],
 // bytes replace A's in the wave's slice, the exponent bytes are encoded, and
 // an overflowing pair's exponent bytes go to the exponent array (positions
 // past the tensor's end are outside its resource and are dropped).
-__device__ __forceinline__ void emit_pair(StreamWriter &writer, const uint32_t *enc,
+__device__ __forceinline__ void emit_pair(StreamWriter &writer, const uint2 *enc,
                                           uint8_t *slice, int s0, uint32_t h0, uint32_t h1,
-                                          bool v0, bool v1, uint32_t off0, int step,
-                                          const UpdateIo &io) {
+                                          bool v0, bool v1, uint32_t off0, const UpdateIo &io) {
     const uint32_t lane = threadIdx.x & (kWave - 1);
-    slice[s0 * kWave + lane] = static_cast<uint8_t>(high_side_byte(h0));
-    slice[(s0 + 1) * kWave + lane] = static_cast<uint8_t>(high_side_byte(h1));
+    slice[s0 * kWave + lane] = static_cast<uint8_t>(side_byte_at_16(h0) >> 16);
+    slice[(s0 + 1) * kWave + lane] = static_cast<uint8_t>(side_byte_at_16(h1) >> 16);
     const uint32_t x0 = high_exponent_byte(h0);
     const uint32_t x1 = high_exponent_byte(h1);
     // Positions past the logical end carry no code (encode.py:255-256).
-    const uint32_t e0 = v0 ? enc[x0] : 0u;
-    const uint32_t e1 = v1 ? enc[x1] : 0u;
-    const bool over = writer.put(e0, e1, step);
+    const uint2 e0 = v0 ? enc[x0] : make_uint2(0u, 0u);
+    const uint2 e1 = v1 ? enc[x1] : make_uint2(0u, 0u);
+    const bool over = writer.put(e0, e1);
     const uint32_t exp_off = over ? off0 : kOutOfRange;
     __builtin_amdgcn_raw_buffer_store_b8(x0, io.exponents, exp_off, 0, 0);
     __builtin_amdgcn_raw_buffer_store_b8(x1, io.exponents, exp_off + kLanes, 0, 0);
@@ -304,7 +317,7 @@ __device__ __forceinline__ void update_chunks(StreamCursor &cursor, const LaneOv
                                               const uint8_t *tail_lds, uint8_t *slice,
                                               SideChunk &side_next,
                                               uint32_t (&b_next)[kChunkSteps / 2],
-                                              StreamWriter &writer, const uint32_t *enc,
+                                              StreamWriter &writer, const uint2 *enc,
                                               const UpdateIo &io, const LanePair &lp,
                                               int64_t row_base, uint32_t valid_in_block,
                                               int c_begin, int c_end, const OpParams &p) {
@@ -355,7 +368,7 @@ __device__ __forceinline__ void update_chunks(StreamCursor &cursor, const LaneOv
                     h0 = v0 ? apply_op(p, a0, b0) << 16 : 0u;
                     h1 = v1 ? apply_op(p, a1, b1) << 16 : 0u;
                 }
-                emit_pair(writer, enc, slice, s0, h0, h1, v0, v1, off0, step, io);
+                emit_pair(writer, enc, slice, s0, h0, h1, v0, v1, off0, io);
             }
         }
         // The slice now holds the chunk's result side bytes.
@@ -370,7 +383,7 @@ template <bool kFull, int S, int kForm>
 __device__ __forceinline__ void update_rows(StreamCursor cursor, const LaneOverlay &lane,
                                             const uint8_t *tail_lds, uint8_t *slice,
                                             SideChunk side_next, StreamWriter &writer,
-                                            const uint32_t *enc, const UpdateIo &io,
+                                            const uint2 *enc, const UpdateIo &io,
                                             int64_t row_base, uint32_t valid_in_block,
                                             const OpParams &p) {
     const LanePair lp;
@@ -397,7 +410,7 @@ template <int S>
 __device__ __forceinline__ void update_block(int32_t form, bool full, const StreamCursor &cursor,
                                              const LaneOverlay &lane, const uint8_t *tail_lds,
                                              uint8_t *slice, const SideChunk &side_next,
-                                             StreamWriter &writer, const uint32_t *enc,
+                                             StreamWriter &writer, const uint2 *enc,
                                              const UpdateIo &io, int64_t row_base,
                                              uint32_t valid_in_block, const OpParams &p) {
     if (!full) {
@@ -436,7 +449,7 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     int rare) {
     extern __shared__ uint32_t stage[];   // A's payload: stage_bytes(W)
     __shared__ DecodeTables tb;
-    __shared__ uint32_t enc[256];
+    __shared__ uint2 enc[256];
     __shared__ int32_t scratch[kWavesPerBlock];
     __shared__ int32_t shared_center;
     __shared__ uint8_t tail_lds[kTailLds];
@@ -487,7 +500,8 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     StreamWriter writer{make_rsrc(encoded_out + block * kLanes,
                                   static_cast<uint32_t>(W - 1) * row_bytes + kLanes * 4),
                         row_bytes, static_cast<uint32_t>(t) * 4u,
-                        static_cast<uint32_t>(W) * 32u, 0u, 0u, S};
+                        static_cast<uint32_t>(W) * row_bytes + static_cast<uint32_t>(t) * 4u,
+                        static_cast<uint32_t>(W) * 32u, 0u, 0u, 0u};
     uint8_t *slice = side_slices[t / kWave];
     const bool full = valid == block_elems;
     const int32_t form = form_of(args.op, args.alpha_is_one, args.beta_is_one);
@@ -499,9 +513,10 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
                           row_base, valid, p);
     writer.finish();
     const bool overflow = writer.overflowed();
-    extra_starts[block * kLanes + t] = static_cast<uint8_t>(overflow ? writer.extra : 255);
+    const int32_t extra = writer.extra_start();
+    extra_starts[block * kLanes + t] = static_cast<uint8_t>(overflow ? extra : 255);
     const int32_t count = block_sum(overflow ? 1 : 0, scratch);
-    const int32_t bytes = block_sum(overflow ? S - writer.extra : 0, scratch);
+    const int32_t bytes = block_sum(overflow ? S - extra : 0, scratch);
     if (t == 0) {
         summaries[block] = count;
         summaries[n_blocks + block] = bytes;
@@ -636,7 +651,7 @@ __device__ __forceinline__ void dual_chunks(StreamCursor &ca, const LaneOverlay 
                                             uint8_t *slice_a, uint8_t *slice_b,
                                             SideChunk &side_a, SideChunk &side_b,
                                             __amdgpu_buffer_rsrc_t b_side, StreamWriter &writer,
-                                            const uint32_t *enc, const UpdateIo &io,
+                                            const uint2 *enc, const UpdateIo &io,
                                             int64_t row_base, uint32_t valid_in_block,
                                             int c_begin, int c_end, float alpha) {
     const uint32_t voffset = side_fetch_offset();
@@ -671,7 +686,7 @@ __device__ __forceinline__ void dual_chunks(StreamCursor &ca, const LaneOverlay 
                 // Padding positions hold 0 (side byte 0, no code).
                 const uint32_t h0 = v0 ? round_bf16_high(__builtin_fmaf(a0, alpha, b0)) : 0u;
                 const uint32_t h1 = v1 ? round_bf16_high(__builtin_fmaf(a1, alpha, b1)) : 0u;
-                emit_pair(writer, enc, slice_a, s0, h0, h1, v0, v1, off0, step, io);
+                emit_pair(writer, enc, slice_a, s0, h0, h1, v0, v1, off0, io);
             }
         }
         const uint4 q = reinterpret_cast<const uint4 *>(slice_a)[threadIdx.x & (kWave - 1)];
@@ -686,7 +701,7 @@ __device__ __forceinline__ void dual_rows(StreamCursor ca, const LaneOverlay &la
                                           StreamCursor cb, const LaneOverlay &lane_b,
                                           uint8_t *slice_a, uint8_t *slice_b, SideChunk side_a,
                                           SideChunk side_b, __amdgpu_buffer_rsrc_t b_side,
-                                          StreamWriter &writer, const uint32_t *enc,
+                                          StreamWriter &writer, const uint2 *enc,
                                           const UpdateIo &io, int64_t row_base,
                                           uint32_t valid_in_block, float alpha) {
     const int split = min(S, min(lane_a.wave_start, lane_b.wave_start) & ~(kChunkSteps - 1));
@@ -710,7 +725,7 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     int rare) {
     extern __shared__ uint32_t stages[];   // A's payload then B's: 2 x stage_bytes(W)
     __shared__ DecodeTables tba, tbb;
-    __shared__ uint32_t enc[256];
+    __shared__ uint2 enc[256];
     __shared__ int32_t scratch[kWavesPerBlock];
     __shared__ int32_t shared_center;
     // The overflow maps (2 KiB) and the raw encode table (1 KiB) are only used
@@ -769,7 +784,8 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     StreamWriter writer{make_rsrc(encoded_out + block * kLanes,
                                   static_cast<uint32_t>(W - 1) * row_bytes + kLanes * 4),
                         row_bytes, static_cast<uint32_t>(t) * 4u,
-                        static_cast<uint32_t>(W) * 32u, 0u, 0u, S};
+                        static_cast<uint32_t>(W) * row_bytes + static_cast<uint32_t>(t) * 4u,
+                        static_cast<uint32_t>(W) * 32u, 0u, 0u, 0u};
     uint8_t *slice_a = slices_a[t / kWave];
     uint8_t *slice_b = slices_b[t / kWave];
     const bool full = valid == block_elems;
@@ -786,9 +802,10 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
 #undef LCT_DUAL_ROWS
     writer.finish();
     const bool overflow = writer.overflowed();
-    extra_starts[block * kLanes + t] = static_cast<uint8_t>(overflow ? writer.extra : 255);
+    const int32_t extra = writer.extra_start();
+    extra_starts[block * kLanes + t] = static_cast<uint8_t>(overflow ? extra : 255);
     const int32_t count = block_sum(overflow ? 1 : 0, scratch);
-    const int32_t bytes = block_sum(overflow ? S - writer.extra : 0, scratch);
+    const int32_t bytes = block_sum(overflow ? S - extra : 0, scratch);
     if (t == 0) {
         summaries[block] = count;
         summaries[n_blocks + block] = bytes;
