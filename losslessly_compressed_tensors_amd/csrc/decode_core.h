@@ -194,6 +194,27 @@ struct StreamCursorT {
         rare = rare_length;
     }
 
+    // Start with the stream's words 0..2 in registers and rows 3..W-1 staged
+    // (row r at stage_rows[(r - 3) * kStride]).  Past the stream's last word
+    // the window re-reads word W-1 instead of a zero pad row: bits beyond a
+    // stream's end never reach a decoded value (a code's table entries do not
+    // depend on the bits after it).  Needs W >= 4.
+    __device__ __forceinline__ void init_registers(const uint32_t *stage_rows,
+                                                   const DecodeTables *tables, uint32_t words,
+                                                   int32_t rare_length, uint32_t w0, uint32_t w1,
+                                                   uint32_t w2) {
+        stage = stage_rows - 3 * kStride;
+        tb = tables;
+        pos = 0;
+        pad_row = words - 1;
+        lo = w0;
+        hi = w1;
+        nx = w2;
+        next_row = 3;
+        pending = 0;
+        rare = rare_length;
+    }
+
     // Decode the next two symbols into entries f0/f1 (length | field << 7) and
     // return len0 + len1.  Also starts the read of the word a crossing needs.
     __device__ __forceinline__ uint32_t next_fields(uint32_t &f0, uint32_t &f1) {

@@ -642,76 +642,120 @@ __global__ __launch_bounds__(kSampleGroup) void dual_sample_kernel(
     }
 }
 
-// Chunks [c_begin, c_end) of the two-operand pass with one overlay variant for
-// both operands (tails read from HBM).  On entry side_a/side_b hold chunk
+// The two-operand kernel keeps its LDS to about 52 KiB at W = 25, so that
+// three workgroups fit per CU and the C4-sized grid (688 codec blocks) runs
+// in one round on 256 CUs:
+//  * payload rows 0..2 of each stream live in registers (the cursor's initial
+//    window) and only rows 3..W-1 are staged; past a stream's last word the
+//    cursor re-reads word W-1 instead of a zero pad row (bits beyond a
+//    stream's end never reach a decoded value);
+//  * side bytes move in 8-step halves: each wave's 1 KiB slice holds A's half
+//    (which the result's side bytes then overwrite) and B's half.
+constexpr int kRegisterRows = 3;
+constexpr int kHalfSlice = kHalfSteps * kWave;   // one operand's 8-step half, one wave
+
+__host__ __device__ constexpr int32_t dual_stage_bytes(int W) {
+    return (W - kRegisterRows) * kLanes * 4;
+}
+
+// Rows first..W-1 of the block's payload into stage rows 0.. (16 bytes per lane
+// per row, non-temporal, as stage_payload).
+__device__ __forceinline__ void stage_payload_rows(uint32_t *stage,
+                                                   const int32_t *__restrict__ encoded,
+                                                   int64_t n_streams, int64_t block, int first,
+                                                   int W) {
+    const int wave = threadIdx.x / kWave;
+    const int j = threadIdx.x % kWave;
+    for (int row = first + wave; row < W; row += kWavesPerBlock) {
+        const int32_t *src = encoded + row * n_streams + block * kLanes + j * 4;
+        __builtin_amdgcn_global_load_lds(
+            src, (__attribute__((address_space(3))) void *)(stage + (row - first) * kLanes), 16,
+            0, kStreaming);
+    }
+}
+
+using u32x2 = __attribute__((ext_vector_type(2))) uint32_t;
+
+// This lane's 8 bytes of a wave's 8-step half: step j >> 3, lanes (j & 7) * 8..
+// of the wave's 64 columns, so lane j's bytes land at j * 8 of the half.
+__device__ __forceinline__ uint32_t half_side_offset() {
+    const uint32_t j = threadIdx.x & (kWave - 1);
+    const uint32_t wave = threadIdx.x / kWave;
+    return (j >> 3) * kLanes + wave * kWave + (j & 7) * 8;
+}
+
+__device__ __forceinline__ u32x2 fetch_half_side(__amdgpu_buffer_rsrc_t side, uint32_t voffset,
+                                                 int first_step) {
+    return __builtin_amdgcn_raw_buffer_load_b64(side, voffset, first_step * kLanes, 0);
+}
+
+__device__ __forceinline__ void store_half_side(uint8_t *half, u32x2 q) {
+    reinterpret_cast<u32x2 *>(half)[threadIdx.x & (kWave - 1)] = q;
+}
+
+// Halves [c_begin, c_end) (steps, multiples of 8) with one overlay variant for
+// both operands (tails read from HBM).  On entry side_a/side_b hold half
 // c_begin's side bytes of A and B.
 template <bool kFull, Overlay kOverlay, int S>
-__device__ __forceinline__ void dual_chunks(StreamCursor &ca, const LaneOverlay &lane_a,
+__device__ __forceinline__ void dual_halves(StreamCursor &ca, const LaneOverlay &lane_a,
                                             StreamCursor &cb, const LaneOverlay &lane_b,
-                                            uint8_t *slice_a, uint8_t *slice_b,
-                                            SideChunk &side_a, SideChunk &side_b,
+                                            uint8_t *slice, u32x2 &side_a, u32x2 &side_b,
                                             __amdgpu_buffer_rsrc_t b_side, StreamWriter &writer,
                                             const uint2 *enc, const UpdateIo &io,
                                             int64_t row_base, uint32_t valid_in_block,
                                             int c_begin, int c_end, float alpha) {
-    const uint32_t voffset = side_fetch_offset();
+    const uint32_t voffset = half_side_offset();
+    uint8_t *half_a = slice;
+    uint8_t *half_b = slice + kHalfSlice;
 #pragma unroll 1
-    for (int c = c_begin; c < c_end; c += kChunkSteps) {
-        store_side_chunk(slice_a, side_a);
-        store_side_chunk(slice_b, side_b);
-        const bool more = c + kChunkSteps < S;
-        side_a = fetch_side_chunk(io.side, more ? voffset : kOutOfRange, c + kChunkSteps);
-        side_b = fetch_side_chunk(b_side, more ? voffset : kOutOfRange, c + kChunkSteps);
+    for (int c = c_begin; c < c_end; c += kHalfSteps) {
+        store_half_side(half_a, side_a);
+        store_half_side(half_b, side_b);
+        const bool more = c + kHalfSteps < S;
+        side_a = fetch_half_side(io.side, more ? voffset : kOutOfRange, c + kHalfSteps);
+        side_b = fetch_half_side(b_side, more ? voffset : kOutOfRange, c + kHalfSteps);
+        // c is a multiple of 8 and the block's first row one of S, so the
+        // swizzle mask of row c + j (j < 8 even) is mask ^ j.
         const uint32_t mask = static_cast<uint32_t>((row_base + c) & 254);
+        uint32_t fa[kHalfSteps], fb[kHalfSteps];
+        decode_fields<kFull, kOverlay>(ca, lane_a, nullptr, c, row_base, valid_in_block, fa);
+        decode_fields<kFull, kOverlay>(cb, lane_b, nullptr, c, row_base, valid_in_block, fb);
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int first = c + half * kHalfSteps;
-            uint32_t fa[kHalfSteps], fb[kHalfSteps];
-            decode_fields<kFull, kOverlay>(ca, lane_a, nullptr, first, row_base, valid_in_block,
-                                           fa);
-            decode_fields<kFull, kOverlay>(cb, lane_b, nullptr, first, row_base, valid_in_block,
-                                           fb);
-#pragma unroll
-            for (int j = 0; j < kHalfSteps; j += 2) {
-                const int s0 = half * kHalfSteps + j;
-                const int step = c + s0;
-                const uint32_t off0 = static_cast<uint32_t>(step) * kLanes
-                    + (threadIdx.x ^ mask ^ static_cast<uint32_t>(s0));
-                const bool v0 = kFull || off0 < valid_in_block;
-                const bool v1 = kFull || off0 + kLanes < valid_in_block;
-                const float a0 = bf16_to_float(join_entry(fa[j], side_byte(slice_a, s0)));
-                const float a1 = bf16_to_float(join_entry(fa[j + 1], side_byte(slice_a, s0 + 1)));
-                const float b0 = bf16_to_float(join_entry(fb[j], side_byte(slice_b, s0)));
-                const float b1 = bf16_to_float(join_entry(fb[j + 1], side_byte(slice_b, s0 + 1)));
-                // Padding positions hold 0 (side byte 0, no code).
-                const uint32_t h0 = v0 ? round_bf16_high(__builtin_fmaf(a0, alpha, b0)) : 0u;
-                const uint32_t h1 = v1 ? round_bf16_high(__builtin_fmaf(a1, alpha, b1)) : 0u;
-                emit_pair(writer, enc, slice_a, s0, h0, h1, v0, v1, off0, io);
-            }
+        for (int j = 0; j < kHalfSteps; j += 2) {
+            const int step = c + j;
+            const uint32_t off0 = static_cast<uint32_t>(step) * kLanes
+                + (threadIdx.x ^ mask ^ static_cast<uint32_t>(j));
+            const bool v0 = kFull || off0 < valid_in_block;
+            const bool v1 = kFull || off0 + kLanes < valid_in_block;
+            const float a0 = bf16_to_float(join_entry(fa[j], side_byte(half_a, j)));
+            const float a1 = bf16_to_float(join_entry(fa[j + 1], side_byte(half_a, j + 1)));
+            const float b0 = bf16_to_float(join_entry(fb[j], side_byte(half_b, j)));
+            const float b1 = bf16_to_float(join_entry(fb[j + 1], side_byte(half_b, j + 1)));
+            // Padding positions hold 0 (side byte 0, no code).
+            const uint32_t h0 = v0 ? round_bf16_high(__builtin_fmaf(a0, alpha, b0)) : 0u;
+            const uint32_t h1 = v1 ? round_bf16_high(__builtin_fmaf(a1, alpha, b1)) : 0u;
+            emit_pair(writer, enc, half_a, j, h0, h1, v0, v1, off0, io);
         }
-        const uint4 q = reinterpret_cast<const uint4 *>(slice_a)[threadIdx.x & (kWave - 1)];
-        __builtin_amdgcn_raw_buffer_store_b128(
-            __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, q), io.side_out,
-            voffset, c * kLanes, kStreaming);
+        // A's half now holds the result's side bytes.
+        const u32x2 q = reinterpret_cast<const u32x2 *>(half_a)[threadIdx.x & (kWave - 1)];
+        __builtin_amdgcn_raw_buffer_store_b64(q, io.side_out, voffset, c * kLanes, kStreaming);
     }
 }
 
 template <bool kFull, int S>
 __device__ __forceinline__ void dual_rows(StreamCursor ca, const LaneOverlay &lane_a,
                                           StreamCursor cb, const LaneOverlay &lane_b,
-                                          uint8_t *slice_a, uint8_t *slice_b, SideChunk side_a,
-                                          SideChunk side_b, __amdgpu_buffer_rsrc_t b_side,
-                                          StreamWriter &writer, const uint2 *enc,
-                                          const UpdateIo &io, int64_t row_base,
-                                          uint32_t valid_in_block, float alpha) {
-    const int split = min(S, min(lane_a.wave_start, lane_b.wave_start) & ~(kChunkSteps - 1));
-    dual_chunks<kFull, kNoOverlay, S>(ca, lane_a, cb, lane_b, slice_a, slice_b, side_a, side_b,
-                                      b_side, writer, enc, io, row_base, valid_in_block, 0, split,
-                                      alpha);
+                                          uint8_t *slice, u32x2 side_a, u32x2 side_b,
+                                          __amdgpu_buffer_rsrc_t b_side, StreamWriter &writer,
+                                          const uint2 *enc, const UpdateIo &io,
+                                          int64_t row_base, uint32_t valid_in_block, float alpha) {
+    const int split = min(S, min(lane_a.wave_start, lane_b.wave_start) & ~(kHalfSteps - 1));
+    dual_halves<kFull, kNoOverlay, S>(ca, lane_a, cb, lane_b, slice, side_a, side_b, b_side,
+                                      writer, enc, io, row_base, valid_in_block, 0, split, alpha);
     if (split < S)
-        dual_chunks<kFull, kHbmOverlay, S>(ca, lane_a, cb, lane_b, slice_a, slice_b, side_a,
-                                           side_b, b_side, writer, enc, io, row_base,
-                                           valid_in_block, split, S, alpha);
+        dual_halves<kFull, kHbmOverlay, S>(ca, lane_a, cb, lane_b, slice, side_a, side_b, b_side,
+                                           writer, enc, io, row_base, valid_in_block, split, S,
+                                           alpha);
 }
 
 __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
@@ -723,22 +767,22 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
     uint8_t *__restrict__ exponents, int64_t n_blocks, int64_t logical_numel, int S, int W,
     int rare) {
-    extern __shared__ uint32_t stages[];   // A's payload then B's: 2 x stage_bytes(W)
+    extern __shared__ uint32_t stages[];   // A's rows 3..W-1, then B's
     __shared__ DecodeTables tba, tbb;
     __shared__ uint2 enc[256];
     __shared__ int32_t scratch[kWavesPerBlock];
     __shared__ int32_t shared_center;
     // The overflow maps (2 KiB) and the raw encode table (1 KiB) are only used
-    // before the first side chunks are stored, so they share A's side slices.
-    __shared__ __attribute__((aligned(16))) uint8_t slices_a[kWavesPerBlock][kChunkSteps * kWave];
-    __shared__ __attribute__((aligned(16))) uint8_t slices_b[kWavesPerBlock][kChunkSteps * kWave];
-    int32_t *map_start = reinterpret_cast<int32_t *>(&slices_a[0][0]);
+    // before the first side halves are stored, so they share the slices.
+    __shared__ __attribute__((aligned(16))) uint8_t slices[kWavesPerBlock][2 * kHalfSlice];
+    int32_t *map_start = reinterpret_cast<int32_t *>(&slices[0][0]);
     int32_t *map_offset = map_start + kLanes;
     int32_t *raw_encode = map_offset + kLanes;
     uint32_t *stage_a = stages;
-    uint32_t *stage_b = stages + stage_bytes(W) / 4;
+    uint32_t *stage_b = stages + dual_stage_bytes(W) / 4;
     const int t = threadIdx.x;
     const int64_t block = blockIdx.x;
+    const int64_t n_streams = n_blocks * kLanes;
     const int64_t row_base = block * S;
     const int64_t logical_base = row_base * kLanes;
     const uint32_t block_elems = static_cast<uint32_t>(S) * kLanes;
@@ -750,15 +794,24 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     io.side_out = make_rsrc(side_out + logical_base, block_elems);
     io.exponents = make_rsrc(exponents + logical_base, valid);
     const __amdgpu_buffer_rsrc_t b_side = make_rsrc(b.side + logical_base, block_elems);
-    const SideChunk first_a = fetch_side_chunk(io.side, side_fetch_offset(), 0);
-    const SideChunk first_b = fetch_side_chunk(b_side, side_fetch_offset(), 0);
+    const u32x2 first_a = fetch_half_side(io.side, half_side_offset(), 0);
+    const u32x2 first_b = fetch_half_side(b_side, half_side_offset(), 0);
+    // Each stream's first three words: the cursors' initial windows.
+    const int32_t *col_a = a.encoded + block * kLanes + t;
+    const int32_t *col_b = b.encoded + block * kLanes + t;
+    uint32_t wa[kRegisterRows], wb[kRegisterRows];
+#pragma unroll
+    for (int r = 0; r < kRegisterRows; ++r) {
+        wa[r] = static_cast<uint32_t>(__builtin_nontemporal_load(col_a + r * n_streams));
+        wb[r] = static_cast<uint32_t>(__builtin_nontemporal_load(col_b + r * n_streams));
+    }
 
     raw_encode[t] = base_encode[t];
     center_from_partials(partials, n_groups, &shared_center);
     build_decode_tables(tba, a.shifted_decode, a.center[0]);
     build_decode_tables(tbb, b.shifted_decode, b.center[0]);
-    stage_payload(stage_a, a.encoded, n_blocks * kLanes, block, W);
-    stage_payload(stage_b, b.encoded, n_blocks * kLanes, block, W);
+    stage_payload_rows(stage_a, a.encoded, n_streams, block, kRegisterRows, W);
+    stage_payload_rows(stage_b, b.encoded, n_streams, block, kRegisterRows, W);
     __syncthreads();   // center and raw encode table
     const int32_t center = shared_center;
     enc[t] = repack_encode_entry(static_cast<uint32_t>(raw_encode[byte_to_index(t, center)]));
@@ -778,20 +831,19 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     __syncthreads();   // payloads and encode table visible; maps no longer read
 
     StreamCursor ca, cb;
-    ca.init(stage_a + t, &tba, static_cast<uint32_t>(W), rare);
-    cb.init(stage_b + t, &tbb, static_cast<uint32_t>(W), rare);
-    const uint32_t row_bytes = static_cast<uint32_t>(n_blocks * kLanes * 4);
+    ca.init_registers(stage_a + t, &tba, static_cast<uint32_t>(W), rare, wa[0], wa[1], wa[2]);
+    cb.init_registers(stage_b + t, &tbb, static_cast<uint32_t>(W), rare, wb[0], wb[1], wb[2]);
+    const uint32_t row_bytes = static_cast<uint32_t>(n_streams * 4);
     StreamWriter writer{make_rsrc(encoded_out + block * kLanes,
                                   static_cast<uint32_t>(W - 1) * row_bytes + kLanes * 4),
                         row_bytes, static_cast<uint32_t>(t) * 4u,
                         static_cast<uint32_t>(W) * row_bytes + static_cast<uint32_t>(t) * 4u,
                         static_cast<uint32_t>(W) * 32u, 0u, 0u, 0u};
-    uint8_t *slice_a = slices_a[t / kWave];
-    uint8_t *slice_b = slices_b[t / kWave];
+    uint8_t *slice = slices[t / kWave];
     const bool full = valid == block_elems;
 #define LCT_DUAL_ROWS(FULL, SS)                                                                \
-    dual_rows<FULL, SS>(ca, lane_a, cb, lane_b, slice_a, slice_b, first_a, first_b, b_side,    \
-                        writer, enc, io, row_base, valid, alpha_value)
+    dual_rows<FULL, SS>(ca, lane_a, cb, lane_b, slice, first_a, first_b, b_side, writer, enc,  \
+                        io, row_base, valid, alpha_value)
     if (S == 128) {
         if (full) LCT_DUAL_ROWS(true, 128);
         else LCT_DUAL_ROWS(false, 128);
@@ -984,7 +1036,10 @@ extern "C" int32_t lct_dual_encode(
                      a_overflow ? *a_overflow : lct_overflow{}, a_overflow != nullptr};
     const OperandA b{b_encoded, b_side, b_shifted_decode, b_center,
                      b_overflow ? *b_overflow : lct_overflow{}, b_overflow != nullptr};
-    const size_t lds = 2 * static_cast<size_t>(stage_bytes(g.fixed_words));
+    // Rows 0..2 of every stream start in registers (W = 2 or 3 never occurs in
+    // a reference geometry).
+    if (g.fixed_words <= kRegisterRows) return LCT_E_GEOMETRY;
+    const size_t lds = 2 * static_cast<size_t>(dual_stage_bytes(g.fixed_words));
     if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&dual_encode_kernel),
                                            lds))
         return static_cast<int32_t>(e);
