@@ -117,28 +117,44 @@ def cpu_baseline(x_cpu, dist, min_seconds: float):
     book = distribution_codebook(dist)
     geometry = oracle.geometry_of("gaussian", "clean")
     bits = x_cpu.view(-1).view(__import__("torch").int16).numpy()
-    reps = 0
-    enc_s = dec_s = 0.0
-    compressed = None
-    while reps < 2 or enc_s + dec_s < min_seconds:
-        t0 = time.perf_counter()
-        compressed = oracle.compress(bits, geometry, book.encode, book.decode, book.rare_length)
-        t1 = time.perf_counter()
-        restored = oracle.decompress(compressed)
-        t2 = time.perf_counter()
-        enc_s += t1 - t0
-        dec_s += t2 - t1
-        reps += 1
-    assert np.array_equal(restored, bits.view(np.uint16))
     nbytes = 2 * bits.size
+
+    def timed(seconds):
+        reps = 0
+        enc_s = dec_s = 0.0
+        restored = None
+        while reps < 2 or enc_s + dec_s < seconds:
+            t0 = time.perf_counter()
+            compressed = oracle.compress(bits, geometry, book.encode, book.decode,
+                                         book.rare_length)
+            t1 = time.perf_counter()
+            restored = oracle.decompress(compressed)
+            t2 = time.perf_counter()
+            enc_s += t1 - t0
+            dec_s += t2 - t1
+            reps += 1
+        assert np.array_equal(restored, bits.view(np.uint16))
+        return reps, enc_s, dec_s
+
+    cores = oracle.num_threads()
+    reps, enc_s, dec_s = timed(min_seconds)
+    # The same on one thread, over a shorter window.
+    oracle.set_num_threads(1)
+    try:
+        reps1, enc1, dec1 = timed(min_seconds / 4)
+    finally:
+        oracle.set_num_threads(cores)
     return {
         "value": round(nbytes * reps / dec_s / 1e9, 3),
         "unit": "GB/s",
-        "cores": oracle.num_threads(),
+        "cores": cores,
         "kind": "port",
         "sample": f"full workload tensor ({bits.size} BF16), {reps} decompressions "
-                  f"({dec_s:.1f} s) and compressions ({enc_s:.1f} s)",
+                  f"({dec_s:.1f} s) and compressions ({enc_s:.1f} s) on {cores} threads; "
+                  f"{reps1} of each ({dec1:.1f} s, {enc1:.1f} s) on 1 thread",
         "compress_value": round(nbytes * reps / enc_s / 1e9, 3),
+        "one_thread_value": round(nbytes * reps1 / dec1 / 1e9, 3),
+        "one_thread_compress_value": round(nbytes * reps1 / enc1 / 1e9, 3),
     }
 
 

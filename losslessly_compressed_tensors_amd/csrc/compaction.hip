@@ -54,8 +54,9 @@ __device__ __forceinline__ void block_exclusive_scan3(const int32_t (&v)[3], int
 // stored as four 16-byte buffer accesses per array (blocks past the end read
 // as 0 and are not written); running totals carry from pass to pass, so any
 // block count gives the same deterministic layout (entries in block order,
-// lanes ascending within a block).  A buffered call takes the arena's lock and
-// reads its free list before scanning, so that latency overlaps the scan.
+// lanes ascending within a block).  A buffered call requests the arena's lock
+// and reads its free list while the first pass's loads are in flight, and
+// before scanning, so those latencies overlap.
 __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     int32_t *__restrict__ summaries, int32_t *__restrict__ counts,
     int32_t *__restrict__ descriptor, int32_t *__restrict__ buffer_meta,
@@ -65,9 +66,6 @@ __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     __shared__ int32_t flag;
     const int t = threadIdx.x;
     const AllocatorMeta meta(buffer_meta, max_free_regions);
-    AllocatorSnapshot snap;
-    if (buffered) allocator_begin(meta, snap, &flag);
-
     const int64_t nb = n_blocks;
     const uint32_t bytes = static_cast<uint32_t>(n_blocks) * 4u;
     const __amdgpu_buffer_rsrc_t count_in = make_rsrc(summaries, bytes);
@@ -79,15 +77,14 @@ __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     const __amdgpu_buffer_rsrc_t meta_base = make_rsrc(blocks + 2 * nb, bytes);
     int32_t *list = summaries + 4 * nb;
     int32_t carry[3] = {0, 0, 0};   // entries, tail bytes, listed blocks
-    for (int base = 0; base < n_blocks; base += kPrefixPass) {
+    // A thread whose 16 blocks all exist moves them with 16-byte accesses; the
+    // one that straddles the end (and those past it) use 4-byte accesses,
+    // which the range check reads as 0 or drops one by one.
+    int32_t c[kPrefixPer], v[kPrefixPer];
+    auto load_pass = [&](int base) {
         const int32_t first_block = base + t * kPrefixPer;
         const uint32_t off = static_cast<uint32_t>(first_block) * 4u;
-        // A thread whose 16 blocks all exist moves them with 16-byte accesses;
-        // the one that straddles the end (and those past it) use 4-byte
-        // accesses, which the range check reads as 0 or drops one by one.
-        const bool whole = first_block + kPrefixPer <= n_blocks;
-        int32_t c[kPrefixPer], v[kPrefixPer];
-        if (whole) {
+        if (first_block + kPrefixPer <= n_blocks) {
 #pragma unroll
             for (int q = 0; q < kPrefixPer / 4; ++q) {
                 const auto cq = __builtin_amdgcn_raw_buffer_load_b128(count_in, off + 16 * q, 0, 0);
@@ -105,6 +102,17 @@ __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
                 v[k] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(bytes_in, off + 4 * k, 0, 0));
             }
         }
+    };
+    // The first pass's loads are issued before the arena lock is requested,
+    // so their latency and the lock's overlap.
+    load_pass(0);
+    AllocatorSnapshot snap;
+    if (buffered) allocator_begin(meta, snap, &flag);
+    for (int base = 0; base < n_blocks; base += kPrefixPass) {
+        const int32_t first_block = base + t * kPrefixPer;
+        const uint32_t off = static_cast<uint32_t>(first_block) * 4u;
+        const bool whole = first_block + kPrefixPer <= n_blocks;
+        if (base > 0) load_pass(base);
         int32_t run[3] = {0, 0, 0};
 #pragma unroll
         for (int k = 0; k < kPrefixPer; ++k) {

@@ -83,6 +83,11 @@ def num_threads() -> int:
     return int(lib().lcto_num_threads())
 
 
+def set_num_threads(n: int) -> None:
+    """Thread count of the oracle's later parallel loops."""
+    lib().lcto_set_num_threads(ctypes.c_int32(int(n)))
+
+
 # ---- allocator ------------------------------------------------------------
 
 

@@ -27,6 +27,16 @@ int32_t lcto_num_threads(void) {
 #endif
 }
 
+/* Thread count of later parallel regions (the CPU baseline's 1-thread
+ * figure); no effect without OpenMP. */
+void lcto_set_num_threads(int32_t n) {
+#ifdef _OPENMP
+    omp_set_num_threads(n > 0 ? n : 1);
+#else
+    (void)n;
+#endif
+}
+
 /* Storage row r, lane l -> logical column l ^ (r & 254)
  * (LCT/kernels/generic/layout.py:15-18). */
 static inline int64_t logical_offset(int64_t row, int32_t lane, int32_t lanes) {

@@ -124,6 +124,7 @@ int32_t lcto_buffer_free(int32_t *meta, int32_t max_free_regions,
 /* Number of OpenMP threads the oracle's parallel loops use (1 if built
  * without OpenMP). */
 int32_t lcto_num_threads(void);
+void lcto_set_num_threads(int32_t n);
 
 #ifdef __cplusplus
 }
