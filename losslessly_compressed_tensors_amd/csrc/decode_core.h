@@ -83,6 +83,41 @@ __device__ __forceinline__ void stage_payload(uint32_t *stage, const int32_t *__
 // LDS bytes of the payload stage for W words per stream (W rows + 1 pad row).
 __host__ __device__ constexpr int32_t stage_bytes(int W) { return (W + 1) * kLanes * 4; }
 
+// Stages without the first three rows: each stream's words 0..2 start in
+// registers (StreamCursorT::init_registers) and only rows 3..W-1 are staged,
+// with no pad row.  Saves four rows (4 KiB) of LDS per workgroup.
+constexpr int kRegisterRows = 3;
+
+__host__ __device__ constexpr int32_t register_stage_bytes(int W) {
+    return (W - kRegisterRows) * kLanes * 4;
+}
+
+// Rows first..W-1 of the block's payload into stage rows 0.. (16 bytes per lane
+// per row, non-temporal, as stage_payload).
+__device__ __forceinline__ void stage_payload_rows(uint32_t *stage,
+                                                   const int32_t *__restrict__ encoded,
+                                                   int64_t n_streams, int64_t block, int first,
+                                                   int W) {
+    const int wave = threadIdx.x / kWave;
+    const int j = threadIdx.x % kWave;
+    for (int row = first + wave; row < W; row += kWavesPerBlock) {
+        const int32_t *src = encoded + row * n_streams + block * kLanes + j * 4;
+        __builtin_amdgcn_global_load_lds(
+            src, (__attribute__((address_space(3))) void *)(stage + (row - first) * kLanes), 16,
+            0, kStreaming);
+    }
+}
+
+// Words 0..2 of this lane's stream of `block` (non-temporal loads).
+__device__ __forceinline__ void load_register_rows(const int32_t *__restrict__ encoded,
+                                                   int64_t n_streams, int64_t block,
+                                                   uint32_t (&w)[kRegisterRows]) {
+    const int32_t *col = encoded + block * kLanes + threadIdx.x;
+#pragma unroll
+    for (int r = 0; r < kRegisterRows; ++r)
+        w[r] = static_cast<uint32_t>(__builtin_nontemporal_load(col + r * n_streams));
+}
+
 // Wait for this thread's outstanding memory operations (including direct
 // global-to-LDS loads) before a barrier publishes the staged data.
 __device__ __forceinline__ void wait_memory() { __builtin_amdgcn_s_waitcnt(0); }

@@ -651,28 +651,7 @@ __global__ __launch_bounds__(kSampleGroup) void dual_sample_kernel(
 //    stream's end never reach a decoded value);
 //  * side bytes move in 8-step halves: each wave's 1 KiB slice holds A's half
 //    (which the result's side bytes then overwrite) and B's half.
-constexpr int kRegisterRows = 3;
 constexpr int kHalfSlice = kHalfSteps * kWave;   // one operand's 8-step half, one wave
-
-__host__ __device__ constexpr int32_t dual_stage_bytes(int W) {
-    return (W - kRegisterRows) * kLanes * 4;
-}
-
-// Rows first..W-1 of the block's payload into stage rows 0.. (16 bytes per lane
-// per row, non-temporal, as stage_payload).
-__device__ __forceinline__ void stage_payload_rows(uint32_t *stage,
-                                                   const int32_t *__restrict__ encoded,
-                                                   int64_t n_streams, int64_t block, int first,
-                                                   int W) {
-    const int wave = threadIdx.x / kWave;
-    const int j = threadIdx.x % kWave;
-    for (int row = first + wave; row < W; row += kWavesPerBlock) {
-        const int32_t *src = encoded + row * n_streams + block * kLanes + j * 4;
-        __builtin_amdgcn_global_load_lds(
-            src, (__attribute__((address_space(3))) void *)(stage + (row - first) * kLanes), 16,
-            0, kStreaming);
-    }
-}
 
 using u32x2 = __attribute__((ext_vector_type(2))) uint32_t;
 
@@ -779,7 +758,7 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     int32_t *map_offset = map_start + kLanes;
     int32_t *raw_encode = map_offset + kLanes;
     uint32_t *stage_a = stages;
-    uint32_t *stage_b = stages + dual_stage_bytes(W) / 4;
+    uint32_t *stage_b = stages + register_stage_bytes(W) / 4;
     const int t = threadIdx.x;
     const int64_t block = blockIdx.x;
     const int64_t n_streams = n_blocks * kLanes;
@@ -797,14 +776,9 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     const u32x2 first_a = fetch_half_side(io.side, half_side_offset(), 0);
     const u32x2 first_b = fetch_half_side(b_side, half_side_offset(), 0);
     // Each stream's first three words: the cursors' initial windows.
-    const int32_t *col_a = a.encoded + block * kLanes + t;
-    const int32_t *col_b = b.encoded + block * kLanes + t;
     uint32_t wa[kRegisterRows], wb[kRegisterRows];
-#pragma unroll
-    for (int r = 0; r < kRegisterRows; ++r) {
-        wa[r] = static_cast<uint32_t>(__builtin_nontemporal_load(col_a + r * n_streams));
-        wb[r] = static_cast<uint32_t>(__builtin_nontemporal_load(col_b + r * n_streams));
-    }
+    load_register_rows(a.encoded, n_streams, block, wa);
+    load_register_rows(b.encoded, n_streams, block, wb);
 
     raw_encode[t] = base_encode[t];
     center_from_partials(partials, n_groups, &shared_center);
@@ -1039,7 +1013,7 @@ extern "C" int32_t lct_dual_encode(
     // Rows 0..2 of every stream start in registers (W = 2 or 3 never occurs in
     // a reference geometry).
     if (g.fixed_words <= kRegisterRows) return LCT_E_GEOMETRY;
-    const size_t lds = 2 * static_cast<size_t>(dual_stage_bytes(g.fixed_words));
+    const size_t lds = 2 * static_cast<size_t>(register_stage_bytes(g.fixed_words));
     if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&dual_encode_kernel),
                                            lds))
         return static_cast<int32_t>(e);
