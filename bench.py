@@ -9,7 +9,8 @@ alternate so the 256 MB Infinity Cache cannot serve repeats.
 Prints one JSON line: ``value`` is decompression throughput in GB/s of
 uncompressed BF16 (2n bytes / time), with compression throughput, the
 compression ratio, the decoder kernel's roofline fraction (``roofline``), the
-encoder kernel's (``encode_roofline``), the fused momentum update of config
+encoder kernel's (``encode_roofline``), config C2 (an 8192x8192 weight-like
+tensor, MEDIUM layout: ``config2``), the fused momentum update of config
 C4 with its single-pass kernel's roofline (``update``), the weight step of
 compressed SGD-momentum with its single-pass kernel's roofline
 (``weight_update``) and a host-core CPU baseline (the C oracle, OpenMP over
@@ -326,6 +327,43 @@ def time_weight_update(args, torch, device):
     }
 
 
+def time_config2(args, torch, device):
+    """a weight-like 8192x8192 BF16 tensor,
+    randn * 0.02 with CPU seed 1, Distribution(GAUSSIAN) MEDIUM layout (the
+    family's unit shape: the sampled center absorbs the 0.02 scale); compress
+    (buffered, the previous result freed) and decompress timed separately
+    through the public API.  Two sets alternate."""
+    from losslessly_compressed_tensors_amd.comp_format import DistType, Distribution, NoiseLevel
+    from losslessly_compressed_tensors_amd.operations import compress, decompress
+    from losslessly_compressed_tensors_amd.tensor_buffer import TensorBuffer
+
+    dist = Distribution(DistType.GAUSSIAN, noise_level=NoiseLevel.MEDIUM)
+    xs = []
+    for seed in (1, 2):
+        gen = torch.Generator().manual_seed(seed)
+        xs.append((torch.randn(8192, 8192, generator=gen) * 0.02).to(torch.bfloat16).to(device))
+    buffer = TensorBuffer(64 << 20, device=device)
+    cts = [compress(x, dist, buffer=buffer) for x in xs]
+    for ct, x in zip(cts, xs):
+        if not torch.equal(decompress(ct).view(torch.int16), x.view(torch.int16)):
+            raise AssertionError("config C2 round trip is not bit-exact")
+    nbytes = 2 * xs[0].numel()
+    dec_ms = _time_events(lambda i: decompress(cts[i % 2]), args.steps, args.warmup, torch)
+    enc_ms = _time_events(lambda i: compress(xs[i % 2], dist, buffer=buffer).free(),
+                          args.steps, args.warmup, torch)
+    dec_alg, enc_alg = decode_bytes(cts[0]), encode_bytes(cts[0])
+    return {
+        "workload": "C2: randn(8192, 8192) * 0.02, CPU seed 1, BF16 (128 MiB); "
+                    "Distribution(GAUSSIAN) MEDIUM; public API, buffered",
+        "geometry": list(cts[0].codec_geometry),
+        "compression_ratio": round(nbytes / cts[0].memory_size(), 5),
+        "decompress_gbps": round(nbytes / (dec_ms * 1e-3) / 1e9, 2),
+        "decompress_hbm_frac": round(dec_alg / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "compress_gbps": round(nbytes / (enc_ms * 1e-3) / 1e9, 2),
+        "compress_hbm_frac": round(enc_alg / (enc_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+    }
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -434,6 +472,8 @@ def main() -> int:
         launch_encode(i)
     encode_kernel_ms = _kernel_ms(launch_encode, args.steps, torch)
 
+    _log("timing config C2")
+    config2 = time_config2(args, torch, device)
     _log("timing fused update (C4)")
     update = time_update(args, torch, device)
     _log("timing fused weight update")
@@ -493,6 +533,7 @@ def main() -> int:
             "traffic": measured_traffic("encode_kernel", nb),
         },
     }
+    result["config2"] = config2
     result["update"] = update
     result["weight_update"] = weight_update
     if not args.skip_cpu:

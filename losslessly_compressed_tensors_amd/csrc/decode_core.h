@@ -381,31 +381,35 @@ enum Overlay { kNoOverlay, kLdsOverlay, kHbmOverlay };
 // in 8 registers.
 constexpr int kHalfSteps = kChunkSteps / 2;
 
+// The entries of steps `step` and `step + 1` of this lane's stream.
+template <bool kFull, Overlay kOverlay>
+__device__ __forceinline__ void decode_pair(StreamCursor &cursor, const LaneOverlay &lane,
+                                            const uint8_t *tail_lds, int step, int64_t row_base,
+                                            uint32_t valid_in_block, uint32_t &f0,
+                                            uint32_t &f1) {
+    constexpr bool kRecount = !kFull || kOverlay != kNoOverlay;
+    uint32_t sum = cursor.next_fields(f0, f1);
+    if (kOverlay != kNoOverlay) overlay_pair<kOverlay == kLdsOverlay>(lane, tail_lds, step, f0, f1);
+    if (!kFull) {
+        // Padding positions of the last block consume no payload bits.
+        const uint32_t off0 = static_cast<uint32_t>(step) * kLanes
+            + (logical_col2(row_base, step) >> 1);
+        if (off0 >= valid_in_block) f0 &= ~31u;
+        if (off0 + kLanes >= valid_in_block) f1 &= ~31u;
+    }
+    if (kRecount) sum = (f0 + f1) & 127u;
+    cursor.advance(sum);
+}
+
 template <bool kFull, Overlay kOverlay>
 __device__ __forceinline__ void decode_fields(StreamCursor &cursor, const LaneOverlay &lane,
                                               const uint8_t *tail_lds, int first_step,
                                               int64_t row_base, uint32_t valid_in_block,
                                               uint32_t (&f)[kHalfSteps]) {
-    constexpr bool kRecount = !kFull || kOverlay != kNoOverlay;
 #pragma unroll
-    for (int j = 0; j < kHalfSteps; j += 2) {
-        const int step = first_step + j;
-        uint32_t f0, f1;
-        uint32_t sum = cursor.next_fields(f0, f1);
-        if (kOverlay != kNoOverlay)
-            overlay_pair<kOverlay == kLdsOverlay>(lane, tail_lds, step, f0, f1);
-        if (!kFull) {
-            // Padding positions of the last block consume no payload bits.
-            const uint32_t off0 = static_cast<uint32_t>(step) * kLanes
-                + (logical_col2(row_base, step) >> 1);
-            if (off0 >= valid_in_block) f0 &= ~31u;
-            if (off0 + kLanes >= valid_in_block) f1 &= ~31u;
-        }
-        if (kRecount) sum = (f0 + f1) & 127u;
-        f[j] = f0;
-        f[j + 1] = f1;
-        cursor.advance(sum);
-    }
+    for (int j = 0; j < kHalfSteps; j += 2)
+        decode_pair<kFull, kOverlay>(cursor, lane, tail_lds, first_step + j, row_base,
+                                     valid_in_block, f[j], f[j + 1]);
 }
 
 // ---- lane pairs
