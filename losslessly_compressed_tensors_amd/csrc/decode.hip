@@ -57,9 +57,7 @@ __device__ __forceinline__ void store_fields_tile(const uint32_t (&f)[kHalfSteps
     const uint32_t mask = m0 ^ (r & 6u);
     const uint32_t group = ((threadIdx.x & ~(kWave - 1u)) ^ (mask & 192u));
     const uint32_t offset = (group + (lane & 7u) * 8u) * 2u + r * (kLanes * 2u);
-    __builtin_amdgcn_raw_buffer_store_b128(
-        __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, q), out, offset,
-        first_step * kLanes * 2, kStreaming);
+    store_b128<kStreaming>(q, out, offset + static_cast<uint32_t>(first_step) * (kLanes * 2));
 }
 
 // Store phase of the last, partial block: 2-byte stores of the positions

@@ -33,6 +33,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
                                              kBufferConfig);
 }
 
+// 16-byte buffer store with the whole offset in the VGPR and soffset 0.
+// A store of more than 8 bytes reads its data VGPRs after issue, and a VALU
+// write to them must wait one cycle; the compiler inserts that wait only when
+// soffset is a constant (it treats an SGPR soffset as hazard-free).  On gfx950
+// the hazard does occur with an SGPR soffset: with two or more workgroups per
+// CU, a 16-byte store followed at once by a VALU write of its first data
+// register wrote the new value.  16-byte buffer stores pass soffset 0, directly
+// or through this helper.
+template <int kAux>
+__device__ __forceinline__ void store_b128(uint4 q, __amdgpu_buffer_rsrc_t rsrc, uint32_t offset) {
+    __builtin_amdgcn_raw_buffer_store_b128(
+        __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, q), rsrc, offset, 0,
+        kAux);
+}
+
 // Unbiased exponent of Huffman table index `symbol` under `center`
 // (tables.py:109-116, primitives.py:29-35).
 __device__ __forceinline__ int32_t index_to_exponent(int32_t symbol, int32_t center) {

@@ -157,9 +157,7 @@ __device__ __forceinline__ void pointwise_chunks(StreamCursor &cursor, const Lan
         if (kPolicy == LCT_COMPRESSED_OUTPUT) {
             // The slice now holds the chunk's result side bytes.
             const uint4 q = reinterpret_cast<const uint4 *>(slice)[threadIdx.x & (kWave - 1)];
-            __builtin_amdgcn_raw_buffer_store_b128(
-                __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, q), io.side_out,
-                voffset, c * kLanes, kStreaming);
+            store_b128<kStreaming>(q, io.side_out, voffset + static_cast<uint32_t>(c) * kLanes);
         }
     }
 }
