@@ -23,6 +23,11 @@ _MODULES = (
     "compression",
     "compression.probabilities",
     "compression.huffman_tables",
+    "components",
+    "components.dist_configs",
+    "components.ops",
+    "components.layers",
+    "components.sparse_utils",
 )
 
 for _name in _MODULES:

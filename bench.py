@@ -13,10 +13,12 @@ encoder kernel's (``encode_roofline``), config C2 (an 8192x8192 weight-like
 tensor, MEDIUM layout: ``config2``), the fused momentum update of config
 C4 with its single-pass kernel's roofline (``update``), the weight step of
 compressed SGD-momentum with its single-pass kernel's roofline
-(``weight_update``) and a host-core CPU baseline (the C oracle, OpenMP over
-codec blocks) beside them.
+(``weight_update``), config 5 (a GPT-2-small training step with weights,
+activations and Muon momentum compressed, against the same step uncompressed:
+``config5``) and a host-core CPU baseline (the C oracle, OpenMP over codec
+blocks) beside them.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-train]
 """
 from __future__ import annotations
 
@@ -364,6 +366,30 @@ def time_config2(args, torch, device):
     }
 
 
+def time_config5(torch, device, steps: int = 5, warmup: int = 2):
+    """one GPT-2-small-shaped training step (12
+    layers, width 768, 12 heads, sequence 1024, batch 8, random init, uniform
+    random token ids), with weights, activations and Muon momentum compressed
+    and without; tokens per second and peak allocated device memory of each
+    (examples/nanogpt/train_gpt_lct.py)."""
+    from examples.nanogpt import train_gpt_lct as gpt
+
+    runs = {mode: gpt.measure(device, compressed=mode == "lct", steps=steps, warmup=warmup)
+            for mode in ("dense", "lct")}
+    return {
+        "workload": "GPT-2-small step: 12 layers, d_model 768, 12 heads, seq 1024, batch 8 "
+                    "(8192 tokens), vocab 50304 (ids < 50257), AdamW + Muon; synthetic tokens",
+        "steps": steps,
+        "warmup": warmup,
+        **runs,
+        "tokens_per_s_ratio": round(runs["lct"]["tokens_per_s"] / runs["dense"]["tokens_per_s"], 4),
+        "peak_hbm_ratio": round(runs["lct"]["peak_allocated_mib"]
+                                / runs["dense"]["peak_allocated_mib"], 4),
+        "resident_state_ratio": round(runs["lct"]["resident_state_mib"]
+                                      / runs["dense"]["resident_state_mib"], 4),
+    }
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -371,6 +397,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--skip-cpu", action="store_true")
+    parser.add_argument("--skip-train", action="store_true",
+                        help="leave out the config-5 training step")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the codec path has no multi-GPU form here "
@@ -536,6 +564,11 @@ def main() -> int:
     result["config2"] = config2
     result["update"] = update
     result["weight_update"] = weight_update
+    if not args.skip_train:
+        _log("timing config 5 (GPT-2-small training step)")
+        del copy_out
+        torch.cuda.empty_cache()
+        result["config5"] = time_config5(torch, device)
     if not args.skip_cpu:
         _log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(host_inputs[0], dist, args.cpu_seconds)

@@ -67,6 +67,19 @@ def compA_mul_B(A_comp: CompressedTensor, B: Tensor, *, dense_output: bool = Tru
                                       buffer=buffer, distribution=distribution)
 
 
+def _alpha_operand(a, device) -> Tensor:
+    """The scalar operand as the kernels read it: the first element of a
+    device tensor, as FP32 (a tensor of another float dtype is cast on the
+    device's stream, without a host sync)."""
+    if not isinstance(a, torch.Tensor):
+        raise TypeError("alpha must be a torch.Tensor")
+    if a.device != device:
+        raise ValueError("alpha must be on the compressed tensor's device")
+    if a.numel() == 0:
+        raise ValueError("alpha must hold at least one element")
+    return a if a.dtype == torch.float32 else a.reshape(-1)[:1].to(torch.float32)
+
+
 def a_compA_add_B(A_comp: CompressedTensor, a: Tensor, B: Tensor, *, alpha_is_one: bool = False,
                   dense_output: bool = True, buffer: TensorBuffer | None = None,
                   distribution=None):
@@ -76,6 +89,8 @@ def a_compA_add_B(A_comp: CompressedTensor, a: Tensor, B: Tensor, *, alpha_is_on
     """
     if not isinstance(a, torch.Tensor):
         raise TypeError("alpha must be a torch.Tensor")
+    if not alpha_is_one:
+        a = _alpha_operand(a, A_comp.data.device)
     return pointwise_compressed_dense(A_comp, B, SCALAR_MUL_ADD, alpha=a,
                                       alpha_is_one=alpha_is_one, dense_output=dense_output,
                                       buffer=buffer, distribution=distribution)
@@ -104,7 +119,6 @@ def a_compA_add_compB(A_comp: CompressedTensor, a: Tensor, B_comp: CompressedTen
                       dense_output: bool = True, buffer: TensorBuffer | None = None,
                       distribution=None):
     """``a * A_comp + B_comp`` with both operands compressed (one fused pass)."""
-    if not isinstance(a, torch.Tensor):
-        raise TypeError("alpha must be a torch.Tensor")
+    a = _alpha_operand(a, A_comp.data.device)
     return pointwise_scale_add_compressed(A_comp, B_comp, a, dense_output=dense_output,
                                           buffer=buffer, distribution=distribution)

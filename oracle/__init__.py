@@ -325,5 +325,20 @@ def apply(op: int, left: int, right: int, alpha: float = 1.0, beta: float = 1.0,
                                 int(alpha_is_one), int(beta_is_one)))
 
 
+def apply_array(op: int, left_bits: np.ndarray, right_bits: np.ndarray, alpha: float = 1.0,
+                beta: float = 1.0, alpha_is_one: bool = False,
+                beta_is_one: bool = True) -> np.ndarray:
+    """``apply`` elementwise over two equal-length BF16 bit arrays."""
+    left = np.ascontiguousarray(left_bits.reshape(-1)).view(np.uint16)
+    right = np.ascontiguousarray(right_bits.reshape(-1)).view(np.uint16)
+    if left.size != right.size:
+        raise ValueError("operands differ in length")
+    out = np.zeros(left.size, dtype=np.uint16)
+    lib().lcto_apply_n(int(op), _p(left), _p(right), ctypes.c_int64(left.size),
+                       ctypes.c_float(alpha), ctypes.c_float(beta), int(alpha_is_one),
+                       int(beta_is_one), _p(out))
+    return out
+
+
 def f32_to_bf16(value: float) -> int:
     return int(lib().lcto_f32_to_bf16(value))

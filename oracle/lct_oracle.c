@@ -407,6 +407,14 @@ uint16_t lcto_apply(int op, uint16_t left, uint16_t right, float alpha,
     return lcto_f32_to_bf16(r);
 }
 
+/* lcto_apply over n element pairs (dense operands of an optimizer step). */
+void lcto_apply_n(int op, const uint16_t *left, const uint16_t *right, int64_t n,
+                  float alpha, float beta, int alpha_is_one, int beta_is_one,
+                  uint16_t *out) {
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = lcto_apply(op, left[i], right[i], alpha, beta, alpha_is_one, beta_is_one);
+}
+
 /* _store_result (pointwise.py:43-65) for one storage position. */
 static inline void store_result(uint16_t bits, int policy, int logical_valid,
                                 int64_t storage, int64_t logical, void *output,

@@ -87,6 +87,9 @@ enum { LCTO_ADD = 0, LCTO_MULTIPLY = 1, LCTO_SCALAR_MUL_ADD = 2 };
 uint16_t lcto_apply(int op, uint16_t left, uint16_t right, float alpha,
                     float beta, int alpha_is_one, int beta_is_one);
 uint16_t lcto_f32_to_bf16(float value);
+void lcto_apply_n(int op, const uint16_t *left, const uint16_t *right, int64_t n,
+                  float alpha, float beta, int alpha_is_one, int beta_is_one,
+                  uint16_t *out);
 
 /* Fused decode + op on one compressed and one dense operand
  * (LCT/kernels/generic/pointwise.py:84-337).  policy 0: dense BF16 output
