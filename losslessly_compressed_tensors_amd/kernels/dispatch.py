@@ -27,7 +27,8 @@ def _ptr(tensor: torch.Tensor | None):
 
 
 def _stream(tensor: torch.Tensor) -> int:
-    return torch.cuda.current_stream(tensor.device).cuda_stream
+    """The raw handle of the current stream of ``tensor``'s device."""
+    return torch._C._cuda_getCurrentRawStream(tensor.get_device())
 
 
 def _byref(storage: FallbackStorage | None):

@@ -139,12 +139,17 @@ class LCTKernelError(RuntimeError):
     """A codec entry point rejected its arguments or failed to launch."""
 
 
+_entry_points: dict = {}
+
+
 def call(name: str, *args) -> None:
     """Invoke entry point ``name`` and raise on a non-zero return code."""
-    lib = load_library()
-    code = getattr(lib, name)(*args)
+    fn = _entry_points.get(name)
+    if fn is None:
+        fn = _entry_points[name] = getattr(load_library(), name)
+    code = fn(*args)
     if code != 0:
-        message = lib.lct_error_string(code).decode()
+        message = load_library().lct_error_string(code).decode()
         raise LCTKernelError(f"{name} failed with code {code}: {message}")
 
 

@@ -42,13 +42,18 @@ class Allocation:
         return self.descriptor[3]
 
 
+def _free_now(storage: torch.Tensor, descriptor: torch.Tensor,
+              max_free_regions: int) -> torch.Tensor:
+    status = torch.empty(1, dtype=torch.int32, device=storage.device)
+    dispatch.buffer_free(storage, max_free_regions, descriptor, status)
+    return status
+
+
 @torch.library.custom_op("lct::tensor_buffer_free", mutates_args=("storage", "descriptor"))
 def tensor_buffer_free(storage: torch.Tensor, descriptor: torch.Tensor,
                        max_free_regions: int) -> torch.Tensor:
     """Opaque free for ``torch.compile`` (``LCT/kernels/tensor_buffer_ops.py:5-15``)."""
-    status = torch.empty(1, dtype=torch.int32, device=storage.device)
-    dispatch.buffer_free(storage, max_free_regions, descriptor, status)
-    return status
+    return _free_now(storage, descriptor, max_free_regions)
 
 
 @tensor_buffer_free.register_fake
@@ -120,7 +125,11 @@ class TensorBuffer:
             raise ValueError("allocation belongs to a different allocator")
         if allocation.descriptor.device != self.device:
             raise ValueError("allocation must be on the allocator device")
-        return tensor_buffer_free(self._storage, allocation.descriptor, self.max_free_regions)
+        if torch.compiler.is_compiling():
+            return tensor_buffer_free(self._storage, allocation.descriptor,
+                                      self.max_free_regions)
+        # Eager callers skip the operator dispatch (same kernel, same stream).
+        return _free_now(self._storage, allocation.descriptor, self.max_free_regions)
 
     def reset(self) -> None:
         """Reset asynchronously; previously returned descriptors become stale."""
