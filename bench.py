@@ -10,7 +10,8 @@ Prints one JSON line: ``value`` is decompression throughput in GB/s of
 uncompressed BF16 (2n bytes / time), with compression throughput, the
 compression ratio, the decoder kernel's roofline fraction (``roofline``), the
 encoder kernel's (``encode_roofline``), config C2 (an 8192x8192 weight-like
-tensor, MEDIUM layout: ``config2``), the fused momentum update of config
+tensor, MEDIUM layout: ``config2``), config C3 (a sparse activation-like
+tensor with forced overflow in a shared 64 MiB buffer: ``config3``), the fused momentum update of config
 C4 with its single-pass kernel's roofline (``update``), the weight step of
 compressed SGD-momentum with its single-pass kernel's roofline
 (``weight_update``), config 5 (a GPT-2-small training step with weights,
@@ -366,6 +367,74 @@ def time_config2(args, torch, device):
     }
 
 
+def time_config3(args, torch, device):
+    """an activation-like 8x2048x4096 BF16 tensor,
+    relu(randn) with CPU seed 2 (about half exact zeros), 0.1% of its entries
+    (randperm with CPU seed 3) scaled by 1e4 in FP32 to force escapes and
+    stream overflow; Distribution(LAPLACE, 1.0, zero_prob=0.5) SPARSE in a
+    64 MiB TensorBuffer.  A step is the config's compress, decompress, free
+    sequence through the public API; compress+free and decompress are also
+    timed on their own.  Two sets alternate (the second from seeds 4 and 5)."""
+    from losslessly_compressed_tensors_amd.comp_format import (
+        DistType, Distribution, NoiseLevel,
+    )
+    from losslessly_compressed_tensors_amd.operations import compress, decompress
+    from losslessly_compressed_tensors_amd.tensor_buffer import (
+        TensorBuffer, _free_regions_snapshot, verify_buffer,
+    )
+
+    dist = Distribution(DistType.LAPLACE, 1.0, zero_prob=0.5, noise_level=NoiseLevel.SPARSE)
+    xs = []
+    for seed, perm_seed in ((2, 3), (4, 5)):
+        z = torch.relu(torch.randn(8, 2048, 4096, generator=torch.Generator().manual_seed(seed)))
+        n = z.numel()
+        idx = torch.randperm(n, generator=torch.Generator().manual_seed(perm_seed))[: n // 1000]
+        z.view(-1)[idx] *= 1e4
+        xs.append(z.to(torch.bfloat16).to(device))
+    buffer = TensorBuffer(64 << 20, device=device)
+    cts = [compress(x, dist, buffer=buffer) for x in xs]
+    for ct, x in zip(cts, xs):
+        if not torch.equal(decompress(ct).view(torch.int16), x.view(torch.int16)):
+            raise AssertionError("config C3 round trip is not bit-exact")
+    nbytes = 2 * xs[0].numel()
+    overflow_streams = int(cts[0].fallback_count.item())
+    tail_bytes = int(cts[0].fallback_used.item())
+    ratio = nbytes / cts[0].memory_size()
+    dec_alg, enc_alg = decode_bytes(cts[0]), encode_bytes(cts[0])
+    dec_ms = _time_events(lambda i: decompress(cts[i % 2]), args.steps, args.warmup, torch)
+    for ct in cts:
+        ct.free()
+
+    def sequence(i):
+        ct = compress(xs[i % 2], dist, buffer=buffer)
+        decompress(ct)
+        ct.free()
+
+    enc_ms = _time_events(lambda i: compress(xs[i % 2], dist, buffer=buffer).free(),
+                          args.steps, args.warmup, torch)
+    seq_ms = _time_events(sequence, args.steps, args.warmup, torch)
+    torch.cuda.synchronize()
+    verify_buffer(buffer)
+    regions = _free_regions_snapshot(buffer)
+    if len(regions) != 1:
+        raise AssertionError(f"config C3 left {len(regions)} free regions, expected 1")
+    return {
+        "workload": "C3: relu(randn(8, 2048, 4096)), CPU seed 2, 0.1% of entries x 1e4 "
+                    "(randperm seed 3), BF16 (128 MiB); Distribution(LAPLACE, 1.0, "
+                    "zero_prob=0.5) SPARSE; 64 MiB TensorBuffer; public API",
+        "geometry": list(cts[0].codec_geometry),
+        "compression_ratio": round(ratio, 5),
+        "overflow_streams": overflow_streams,
+        "tail_bytes": tail_bytes,
+        "decompress_gbps": round(nbytes / (dec_ms * 1e-3) / 1e9, 2),
+        "decompress_hbm_frac": round(dec_alg / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "compress_gbps": round(nbytes / (enc_ms * 1e-3) / 1e9, 2),
+        "compress_hbm_frac": round(enc_alg / (enc_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "sequence_ms": round(seq_ms, 5),
+        "sequence_gbps": round(2 * nbytes / (seq_ms * 1e-3) / 1e9, 2),
+    }
+
+
 def time_config5(torch, device, steps: int = 5, warmup: int = 2):
     """one GPT-2-small-shaped training step (12
     layers, width 768, 12 heads, sequence 1024, batch 8, random init, uniform
@@ -502,6 +571,8 @@ def main() -> int:
 
     _log("timing config C2")
     config2 = time_config2(args, torch, device)
+    _log("timing config C3")
+    config3 = time_config3(args, torch, device)
     _log("timing fused update (C4)")
     update = time_update(args, torch, device)
     _log("timing fused weight update")
@@ -562,6 +633,7 @@ def main() -> int:
         },
     }
     result["config2"] = config2
+    result["config3"] = config3
     result["update"] = update
     result["weight_update"] = weight_update
     if not args.skip_train:
