@@ -59,6 +59,15 @@ typedef struct {
     int64_t base;              /* private tail base */
 } lct_overflow;
 
+/* Frees a caller deferred to its next arena reservation (at most
+ * LCT_MAX_PENDING_FREES descriptors of the same TensorBuffer, applied in
+ * order). */
+#define LCT_MAX_PENDING_FREES 4
+typedef struct {
+    int32_t *descriptor[LCT_MAX_PENDING_FREES];
+    int32_t count;
+} lct_pending_frees;
+
 /* Pointwise operation selectors: LCT/codec/pointwise.py:289-304. */
 #define LCT_OP_ADD 0
 #define LCT_OP_MULTIPLY 1
@@ -158,6 +167,29 @@ int32_t lct_prefix_allocate(int32_t *summaries, int32_t *counts,
                             int32_t *descriptor, int32_t *buffer_meta,
                             int32_t *blocks, int64_t n_blocks, int32_t buffered,
                             int32_t max_free_regions, hipStream_t stream);
+
+/* ---- replaces the buffered sequence dispatch.py:70-85 (prefix_allocate)
+ * + dispatch.py:113-130 (compact_extra), LCT/codec/encode.py:77-170, with
+ * TensorBuffer.free (LCT/tensor_buffer.py:121-128) of up to
+ * LCT_MAX_PENDING_FREES earlier allocations folded in: one launch.
+ * Workgroup 0 takes the arena lock, applies `frees` in order (each as
+ * lct_buffer_free would; statuses are not reported, a freed descriptor gets
+ * status 5), then does what lct_prefix_allocate does with buffered = 1 and
+ * stores `epoch` to *ready.  Every other workgroup waits (bounded) until
+ * *ready == epoch and then writes the entries and tails of the listed blocks,
+ * as lct_compact_extra with buffered = 1 (lanes, starts and tails in `arena`).
+ * summaries: int32[5*nb + 1] as for lct_prefix_allocate.  ready: a device
+ * uint64 whose value before the launch differs from `epoch` (use a value no
+ * earlier call used).  The result (counts, descriptor, blocks, arena bytes)
+ * equals lct_buffer_free on each pending descriptor followed by
+ * lct_prefix_allocate and lct_compact_extra. */
+int32_t lct_allocate_compact(const void *source, int32_t *summaries, int32_t *counts,
+                             int32_t *descriptor, int32_t *buffer_meta,
+                             int32_t max_free_regions, uint8_t *arena, int32_t *blocks,
+                             const uint8_t *extra_starts, const lct_pending_frees *frees,
+                             uint64_t *ready, uint64_t epoch, int64_t size,
+                             int64_t logical_numel, lct_geometry g, int32_t precomputed,
+                             hipStream_t stream);
 
 /* ---- replaces dispatch.py:88-95 (count_bad_streams, the atomic path's
  * totals, LCT/kernels/generic/compaction.py:31-51): adds the number of

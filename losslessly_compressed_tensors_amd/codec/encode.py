@@ -70,8 +70,10 @@ def encode_components(
     encoded = torch.empty(streams * fixed_words + 4, dtype=torch.int32, device=device)
     extra_starts = torch.empty(streams, dtype=torch.uint8, device=device)
     # Per-block overflow counts/bytes, their scans and the list of blocks
-    # that overflow (int32[5*blocks + 1], see lct_prefix_allocate).
-    summaries = torch.empty(5 * blocks + 1, dtype=torch.int32, device=device)
+    # that overflow (int32[5*blocks + 1], see lct_prefix_allocate), then the
+    # ready word of lct_allocate_compact.
+    summaries = torch.empty(dispatch.summaries_length(blocks), dtype=torch.int32,
+                            device=device)
     launch = dict(precomputed=precomputed, logical_numel=logical_numel,
                   block_symbols=block_symbols, lanes=lanes, steps=steps, fixed_words=fixed_words)
     sample_values = None
@@ -127,7 +129,10 @@ def finish_encode(
     arena reservation; for private storage one device->host sync that sizes
     the exact lane/start/tail arrays; then the compaction, which reads the
     tails' exponents from ``tail_source`` (BF16 bits, or exponent bytes in
-    logical order when ``precomputed``)."""
+    logical order when ``precomputed``).  For a shared buffer the scans, the
+    reservation (after the buffer's deferred frees) and the compaction are one
+    launch; ``summaries`` then holds ``dispatch.summaries_length(blocks)``
+    entries."""
     device = encoded.device
     stream_geometry = geometry(distribution)
     block_symbols, lanes, steps, _ = stream_geometry
@@ -136,9 +141,14 @@ def finish_encode(
     blocks_out = torch.empty(3 * blocks, dtype=torch.int32, device=device)
     buffered = buffer is not None
     descriptor = torch.empty(4, dtype=torch.int32, device=device) if buffered else counts
-    if blocks > 0:
+    if blocks > 0 and buffered:
+        dispatch.allocate_compact(
+            tail_source, summaries, counts, descriptor, buffer, blocks_out, extra_starts,
+            buffer._take_frees(), blocks, size, logical_numel=logical_numel,
+            block_symbols=block_symbols, lanes=lanes, steps=steps, precomputed=precomputed)
+    elif blocks > 0:
         dispatch.prefix_allocate(summaries, counts, descriptor, buffer, blocks_out, blocks,
-                                 buffered, buffer.max_free_regions if buffered else 256)
+                                 False, 256)
     else:
         counts.zero_()
         if buffered:
@@ -147,7 +157,7 @@ def finish_encode(
             descriptor = buffer_descriptor.descriptor
 
     final_count, final_total = counts[:1], counts[1:2]
-    needs_compaction = blocks > 0
+    needs_compaction = False
     if buffered:
         arena = buffer.data
         storage = FallbackStorage(tail=arena, count=final_count, lanes=arena, starts=arena,
@@ -155,7 +165,7 @@ def finish_encode(
                                   allocation=descriptor)
     else:
         count, tail_bytes = (int(v) for v in counts[:2].tolist())
-        needs_compaction = needs_compaction and count > 0
+        needs_compaction = blocks > 0 and count > 0
         storage = FallbackStorage(
             tail=torch.empty(tail_bytes, dtype=torch.uint8, device=device),
             count=final_count,

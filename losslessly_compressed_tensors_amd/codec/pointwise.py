@@ -140,7 +140,8 @@ def _fused_compressed_output(data: CompressedTensor, other: torch.Tensor,
     side = torch.empty(data.size, dtype=torch.uint8, device=device)
     encoded = torch.empty(streams * fixed_words + 4, dtype=torch.int32, device=device)
     extra_starts = torch.empty(streams, dtype=torch.uint8, device=device)
-    summaries = torch.empty(5 * blocks + 1, dtype=torch.int32, device=device)
+    summaries = torch.empty(dispatch.summaries_length(blocks), dtype=torch.int32,
+                            device=device)
     # Only the rows of overflowing streams are written (and read back by the
     # compaction); the rest stays unwritten.
     exponents = torch.empty(n, dtype=torch.uint8, device=device)
@@ -200,7 +201,8 @@ def _fused_dual_compressed_output(data: CompressedTensor, other: CompressedTenso
     side = torch.empty(data.size, dtype=torch.uint8, device=device)
     encoded = torch.empty(streams * fixed_words + 4, dtype=torch.int32, device=device)
     extra_starts = torch.empty(streams, dtype=torch.uint8, device=device)
-    summaries = torch.empty(5 * blocks + 1, dtype=torch.int32, device=device)
+    summaries = torch.empty(dispatch.summaries_length(blocks), dtype=torch.int32,
+                            device=device)
     # Only the rows of overflowing streams are written (and read back by the
     # compaction); the rest stays unwritten.
     exponents = torch.empty(n, dtype=torch.uint8, device=device)

@@ -89,12 +89,19 @@ class CompressedTensor:
         return int(self.fallback_descriptor[1].item())
 
     def free(self) -> None:
-        """Release this tensor's arena reservation, if buffer-backed."""
+        """Release this tensor's arena reservation, if buffer-backed
+        (``LCT/comp_tensor.py:80-86``).  Eagerly the free rides on the
+        buffer's next reservation on this stream (the arena then holds what an
+        immediate free would have left); under ``torch.compile`` it is the
+        ``lct::tensor_buffer_free`` operator."""
         if self.fallback_descriptor is None or self.buffer is None:
             return
         from .tensor_buffer import Allocation
 
-        self.buffer.free(Allocation(self.fallback_descriptor, self.buffer))
+        if torch.compiler.is_compiling():
+            self.buffer.free(Allocation(self.fallback_descriptor, self.buffer))
+        else:
+            self.buffer._defer_free(self.fallback_descriptor)
 
     @property
     def logical_numel(self) -> int:

@@ -199,11 +199,12 @@ __device__ __forceinline__ void allocator_allocate(const AllocatorMeta &m, int32
     allocator_finish(m, snap, request, descriptor, scratch);
 }
 
-// tensor_buffer.py:94-179.  Returns the status in every thread.
-__device__ __forceinline__ int32_t allocator_free(const AllocatorMeta &m, int32_t *descriptor,
-                                                  int32_t *scratch, int32_t *flag) {
+// tensor_buffer.py:94-179 with the lock already held.  Returns the status in
+// every thread.  Contains barriers; the free list in memory is updated (and
+// visible to the whole workgroup) when it returns.
+__device__ __forceinline__ int32_t allocator_free_locked(const AllocatorMeta &m,
+                                                         int32_t *descriptor, int32_t *scratch) {
     __shared__ int32_t shared2[2];
-    if (!allocator_lock(m.lock, flag)) return kStatusLock;
     const int32_t offset = descriptor[0];
     const int32_t size = descriptor[1];
     const int32_t status = descriptor[2];
@@ -257,8 +258,35 @@ __device__ __forceinline__ int32_t allocator_free(const AllocatorMeta &m, int32_
         }
         if (result == kStatusOk && threadIdx.x == 0) descriptor[2] = kStatusFreed;
     }
+    __syncthreads();   // metadata writes visible to the next reader in the workgroup
+    return result;
+}
+
+// tensor_buffer.py:94-179.  Returns the status in every thread.
+__device__ __forceinline__ int32_t allocator_free(const AllocatorMeta &m, int32_t *descriptor,
+                                                  int32_t *scratch, int32_t *flag) {
+    if (!allocator_lock(m.lock, flag)) return kStatusLock;
+    const int32_t result = allocator_free_locked(m, descriptor, scratch);
     allocator_unlock(m.lock);
     return result;
+}
+
+// allocator_begin that first returns the caller's deferred frees, in order,
+// under the same lock (each exactly as allocator_free would, its status
+// discarded), so the allocation that follows sees the free list those frees
+// leave.  Contains barriers.
+__device__ __forceinline__ void allocator_begin_after_frees(const AllocatorMeta &m,
+                                                            AllocatorSnapshot &snap,
+                                                            const lct_pending_frees &frees,
+                                                            int32_t *flag, int32_t *scratch) {
+    snap.locked = allocator_lock(m.lock, flag);
+    snap.generation = 0;
+    snap.count = 0;
+    if (!snap.locked) return;
+    for (int i = 0; i < frees.count; ++i) allocator_free_locked(m, frees.descriptor[i], scratch);
+    snap.generation = *m.generation;
+    snap.count = *m.count;
+    load_regions(m, snap.r);
 }
 
 }  // namespace lct

@@ -57,11 +57,17 @@ __device__ __forceinline__ void block_exclusive_scan3(const int32_t (&v)[3], int
 // lanes ascending within a block).  A buffered call requests the arena's lock
 // and reads its free list while the first pass's loads are in flight, and
 // before scanning, so those latencies overlap.
-__global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
-    int32_t *__restrict__ summaries, int32_t *__restrict__ counts,
-    int32_t *__restrict__ descriptor, int32_t *__restrict__ buffer_meta,
-    int32_t *__restrict__ blocks, int32_t n_blocks, int32_t buffered,
-    int32_t max_free_regions) {
+//
+// A buffered call may first apply deferred frees (`frees`) under the same lock,
+// before the free list is read for the reservation.  Workgroup-wide; contains
+// barriers.
+__device__ __forceinline__ void scan_allocate(int32_t *__restrict__ summaries,
+                                              int32_t *__restrict__ counts,
+                                              int32_t *__restrict__ descriptor,
+                                              int32_t *__restrict__ buffer_meta,
+                                              int32_t *__restrict__ blocks, int32_t n_blocks,
+                                              int32_t buffered, int32_t max_free_regions,
+                                              const lct_pending_frees &frees) {
     __shared__ int32_t scratch[3 * kWavesPerBlock];
     __shared__ int32_t flag;
     const int t = threadIdx.x;
@@ -107,7 +113,7 @@ __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     // so their latency and the lock's overlap.
     load_pass(0);
     AllocatorSnapshot snap;
-    if (buffered) allocator_begin(meta, snap, &flag);
+    if (buffered) allocator_begin_after_frees(meta, snap, frees, &flag, scratch);
     for (int base = 0; base < n_blocks; base += kPrefixPass) {
         const int32_t first_block = base + t * kPrefixPer;
         const uint32_t off = static_cast<uint32_t>(first_block) * 4u;
@@ -179,6 +185,16 @@ __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     if (buffered) allocator_finish(meta, snap, carry[1] + 2 * carry[0], descriptor, scratch);
 }
 
+__global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
+    int32_t *__restrict__ summaries, int32_t *__restrict__ counts,
+    int32_t *__restrict__ descriptor, int32_t *__restrict__ buffer_meta,
+    int32_t *__restrict__ blocks, int32_t n_blocks, int32_t buffered,
+    int32_t max_free_regions) {
+    const lct_pending_frees none{};
+    scan_allocate(summaries, counts, descriptor, buffer_meta, blocks, n_blocks, buffered,
+                  max_free_regions, none);
+}
+
 // One codec block's overflow entries and tails (compaction.py:137-228).  The
 // block's tail bytes are produced one per thread: tail byte i belongs to the
 // overflowing lane whose local byte range holds i (binary search over the
@@ -187,13 +203,11 @@ __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
 __device__ __forceinline__ void compact_block(
     const void *__restrict__ source, uint8_t *__restrict__ lanes, uint8_t *__restrict__ starts,
     uint8_t *__restrict__ tail, int64_t lane_off, int64_t start_off, int64_t tail_off,
-    const int32_t *__restrict__ blocks, const uint8_t *__restrict__ extra_starts,
-    int64_t block, int64_t n_blocks, int64_t logical_numel, int S, int precomputed,
-    int32_t *scratch, int32_t *entry_offset, int32_t *entry_start, int32_t *entry_lane) {
+    int32_t count, int32_t first, int32_t byte_base,
+    const uint8_t *__restrict__ extra_starts, int64_t block, int64_t logical_numel, int S,
+    int precomputed, int32_t *scratch, int32_t *entry_offset, int32_t *entry_start,
+    int32_t *entry_lane) {
     const int t = threadIdx.x;
-    const int32_t count = blocks[block];
-    const int32_t first = blocks[n_blocks + block];
-    const int32_t byte_base = blocks[2 * n_blocks + block];
     const int32_t start = extra_starts[block * kLanes + t];
     const bool bad = start != 255;
     int32_t block_bytes, ignored;
@@ -259,9 +273,86 @@ __global__ __launch_bounds__(kLanes) void compact_extra_kernel(
     for (int64_t i = blockIdx.x; i < listed; i += gridDim.x) {
         const int64_t block = list != nullptr ? list[i] : i;
         if (list == nullptr && blocks[block] == 0) continue;   // uniform
-        compact_block(source, lanes, starts, tail, lane_off, start_off, tail_off, blocks,
-                      extra_starts, block, n_blocks, logical_numel, S, precomputed, scratch,
+        compact_block(source, lanes, starts, tail, lane_off, start_off, tail_off,
+                      blocks[block], blocks[n_blocks + block], blocks[2 * n_blocks + block],
+                      extra_starts, block, logical_numel, S, precomputed, scratch,
                       entry_offset, entry_start, entry_lane);
+    }
+}
+
+// Waits of the compacting workgroups for workgroup 0's reservation: polls of
+// the ready word with a sleep between them, about 4 s at most (workgroup 0's
+// own wait for the arena lock is bounded well below that, and it publishes
+// in every case).  A workgroup that gives up writes nothing.
+constexpr int kReadySpinLimit = 1 << 22;
+// Compacting workgroups of one launch: 511 measured best on gfx950 at 4096
+// blocks (694 with overflow) and at 1024 blocks (all with overflow), against
+// 255, 1023 and 2047.
+constexpr int64_t kAllocateCompactWaiters = 511;
+
+// A value workgroup 0 wrote in this launch: an agent-scope load, which reads
+// the coherent copy (workgroup 0 released its writes before the ready word).
+// An agent-scope acquire fence instead would invalidate the whole L2 once per
+// wave; measured on gfx950 that made the launch 22 us against 15 us for the
+// two launches it replaces.
+__device__ __forceinline__ int32_t published(const int32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Scan + reservation (workgroup 0, deferred frees first) and compaction of
+// the listed blocks (workgroups 1..G-1) in one launch.  Workgroup 0 publishes
+// its writes with an agent-scope release and then stores `epoch` to *ready;
+// the others poll *ready, read what workgroup 0 wrote with agent-scope loads
+// and walk the overflow-block list with stride G - 1.  Workgroup 0 is
+// dispatched first and waits for nothing but the arena lock, so every wait
+// ends.
+__global__ __launch_bounds__(kLanes) void allocate_compact_kernel(
+    const void *__restrict__ source, int32_t *__restrict__ summaries,
+    int32_t *__restrict__ counts, int32_t *__restrict__ descriptor,
+    int32_t *__restrict__ buffer_meta, int32_t max_free_regions, uint8_t *__restrict__ arena,
+    int32_t *__restrict__ blocks, const uint8_t *__restrict__ extra_starts,
+    lct_pending_frees frees, uint64_t *__restrict__ ready, uint64_t epoch, int32_t n_blocks,
+    int64_t logical_numel, int S, int precomputed) {
+    if (blockIdx.x == 0) {
+        scan_allocate(summaries, counts, descriptor, buffer_meta, blocks, n_blocks, 1,
+                      max_free_regions, frees);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_store(ready, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    __shared__ int32_t go;
+    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ int32_t entry_offset[kLanes], entry_start[kLanes], entry_lane[kLanes];
+    if (threadIdx.x == 0) {
+        int32_t seen = 0;
+        for (int i = 0; i < kReadySpinLimit; ++i) {
+            if (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch) {
+                seen = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(8);
+        }
+        go = seen;
+    }
+    __syncthreads();
+    if (go == 0) return;
+    const int64_t nb = n_blocks;
+    const int64_t listed = published(summaries + 5 * nb);
+    if (static_cast<int64_t>(blockIdx.x) - 1 >= listed) return;   // nothing for this workgroup
+    if (published(descriptor + 2) != kStatusOk) return;   // failed reservation: write nothing
+    const int64_t total = published(counts);
+    const int64_t lane_off = published(descriptor);
+    const int64_t start_off = lane_off + total;
+    const int64_t tail_off = lane_off + 2 * total;
+    const int32_t *list = summaries + 4 * nb;
+    for (int64_t i = blockIdx.x - 1; i < listed; i += gridDim.x - 1) {
+        const int64_t block = published(list + i);
+        compact_block(source, arena, arena, arena, lane_off, start_off, tail_off,
+                      published(blocks + block), published(blocks + nb + block),
+                      published(blocks + 2 * nb + block), extra_starts, block, logical_numel,
+                      S, precomputed, scratch, entry_offset, entry_start, entry_lane);
     }
 }
 
@@ -401,6 +492,45 @@ extern "C" int32_t lct_compact_extra(const void *source, uint8_t *lanes, uint8_t
     hipLaunchKernelGGL(compact_extra_kernel, dim3(grid), dim3(kLanes), 0, stream, source, lanes, starts, tail, descriptor, count, blocks, base,
                        extra_starts, summaries, n_blocks, logical_numel, g.steps, precomputed,
                        buffered);
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_allocate_compact(const void *source, int32_t *summaries,
+                                        int32_t *counts, int32_t *descriptor,
+                                        int32_t *buffer_meta, int32_t max_free_regions,
+                                        uint8_t *arena, int32_t *blocks,
+                                        const uint8_t *extra_starts,
+                                        const lct_pending_frees *frees, uint64_t *ready,
+                                        uint64_t epoch, int64_t size, int64_t logical_numel,
+                                        lct_geometry g, int32_t precomputed,
+                                        hipStream_t stream) {
+    if (!source || !summaries || !counts || !descriptor || !buffer_meta || !arena || !blocks
+        || !extra_starts || !ready)
+        return LCT_E_NULL;
+    if ((reinterpret_cast<uintptr_t>(ready) & 7) != 0) return LCT_E_ARG;
+    if (!geometry_ok(g)) return LCT_E_GEOMETRY;
+    if (size <= 0 || size % g.block_symbols != 0 || logical_numel <= 0 || logical_numel > size)
+        return LCT_E_SIZE;
+    const int64_t n_blocks = size / g.block_symbols;
+    if (n_blocks > kMaxBlocks) return LCT_E_SIZE;
+    if (max_free_regions <= 0 || max_free_regions > 4096
+        || (max_free_regions & (max_free_regions - 1)) != 0)
+        return LCT_E_ARG;
+    lct_pending_frees pending{};
+    if (frees != nullptr) {
+        if (frees->count < 0 || frees->count > LCT_MAX_PENDING_FREES) return LCT_E_ARG;
+        for (int i = 0; i < frees->count; ++i)
+            if (frees->descriptor[i] == nullptr) return LCT_E_NULL;
+        pending = *frees;
+    }
+    // Workgroup 0 plus up to kAllocateCompactWaiters compacting workgroups
+    // (every one fits on the device at once next to workgroup 0).
+    const uint32_t grid = 1u + static_cast<uint32_t>(
+        n_blocks < kAllocateCompactWaiters ? n_blocks : kAllocateCompactWaiters);
+    hipLaunchKernelGGL(allocate_compact_kernel, dim3(grid), dim3(kLanes), 0, stream, source,
+                       summaries, counts, descriptor, buffer_meta, max_free_regions, arena,
+                       blocks, extra_starts, pending, ready, epoch,
+                       static_cast<int32_t>(n_blocks), logical_numel, g.steps, precomputed);
     return static_cast<int32_t>(hipGetLastError());
 }
 

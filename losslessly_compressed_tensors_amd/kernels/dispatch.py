@@ -9,6 +9,8 @@ only engine.
 """
 from __future__ import annotations
 
+import itertools
+import os
 from dataclasses import dataclass
 
 import torch
@@ -156,10 +158,52 @@ def prefix_allocate(summaries, counts, descriptor, buffer, blocks_out, blocks, b
     ``compact_extra``).  ``summaries`` is int32[5*blocks + 1]."""
     _require_device(summaries, counts)
     meta = buffer.storage if buffer is not None else None
+    if buffered:
+        buffer._flush_frees()
     hip.call("lct_prefix_allocate", _ptr(summaries), _ptr(counts),
              _ptr(descriptor) if buffered else None, _ptr(meta) if buffered else None,
              _ptr(blocks_out), int(blocks), int(bool(buffered)), int(max_free_regions),
              _stream(summaries))
+
+
+MAX_PENDING_FREES = hip.MAX_PENDING_FREES
+
+# Values stored to the ready word of lct_allocate_compact: unique within the
+# process (a counter) and, in the high half, a per-process random salt, so no
+# earlier call's value (nor, in practice, stale memory) equals a new one.
+_EPOCHS = itertools.count((int.from_bytes(os.urandom(4), "little") | 1) << 32)
+
+# int32 entries of a summaries tensor for lct_allocate_compact: the 5*nb + 1
+# of lct_prefix_allocate, then an 8-byte aligned uint64 ready word.
+
+
+def summaries_length(blocks: int) -> int:
+    return 5 * blocks + 5
+
+
+def _ready_pointer(summaries: torch.Tensor, blocks: int) -> int:
+    return (summaries.data_ptr() + 4 * (5 * blocks + 1) + 7) & ~7
+
+
+def allocate_compact(source, summaries, counts, descriptor, buffer, blocks_out, extra_starts,
+                     frees, n_blocks, size, *, logical_numel, block_symbols, lanes, steps,
+                     precomputed) -> None:
+    """Buffered overflow bookkeeping in one launch: the deferred ``frees``
+    (device descriptors, at most ``hip.MAX_PENDING_FREES``), then what
+    ``prefix_allocate`` and ``compact_extra`` do for a shared buffer
+    (``dispatch.py:70-85, 113-130``).  ``summaries`` holds
+    ``summaries_length(n_blocks)`` entries."""
+    _require_device(source, summaries, counts)
+    pending = hip.PendingFrees()
+    pending.count = len(frees)
+    for i, freed in enumerate(frees):
+        pending.descriptor[i] = freed.data_ptr()
+    geometry = hip.Geometry(block_symbols, lanes, steps, 2)
+    hip.call("lct_allocate_compact", _ptr(source), _ptr(summaries), _ptr(counts),
+             _ptr(descriptor), _ptr(buffer.storage), int(buffer.max_free_regions),
+             _ptr(buffer.data), _ptr(blocks_out), _ptr(extra_starts), hip.ctypes.byref(pending),
+             _ready_pointer(summaries, n_blocks), next(_EPOCHS), int(size), int(logical_numel),
+             geometry, int(bool(precomputed)), _stream(source))
 
 
 def count_bad_streams(extra_starts, count, total, streams, steps) -> None:
@@ -420,6 +464,7 @@ def buffer_allocate(storage, max_free_regions, requested, item_count, item_bytes
              _ptr(item_count), int(item_bytes), _ptr(descriptor), _stream(storage))
 
 
-def buffer_free(storage, max_free_regions, descriptor, status) -> None:
+def buffer_free(storage, max_free_regions, descriptor, status, *, stream=None) -> None:
+    """``stream``: a raw stream handle; the current stream when None."""
     hip.call("lct_buffer_free", _ptr(storage), int(max_free_regions), _ptr(descriptor),
-             _ptr(status), _stream(storage))
+             _ptr(status), _stream(storage) if stream is None else stream)

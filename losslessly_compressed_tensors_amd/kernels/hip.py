@@ -48,6 +48,18 @@ class Overflow(ctypes.Structure):
     ]
 
 
+MAX_PENDING_FREES = 4   # LCT_MAX_PENDING_FREES
+
+
+class PendingFrees(ctypes.Structure):
+    """``lct_pending_frees``: descriptors whose frees ride on the next reservation."""
+
+    _fields_ = [
+        ("descriptor", _ptr * MAX_PENDING_FREES),
+        ("count", _c_int32),
+    ]
+
+
 # name -> argument types (all entry points return int32).
 _SIGNATURES = {
     "lct_estimate_and_shift_tables": [_ptr, _c_int32, _c_int64, _c_int64, _ptr, _ptr, _ptr, _ptr,
@@ -84,6 +96,9 @@ _SIGNATURES = {
                         _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _c_int64, _ptr, _ptr, _ptr,
                         _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64, _c_int64, Geometry,
                         _c_int32, _ptr],
+    "lct_allocate_compact": [_ptr, _ptr, _ptr, _ptr, _ptr, _c_int32, _ptr, _ptr, _ptr,
+                             ctypes.POINTER(PendingFrees), _ptr, ctypes.c_uint64, _c_int64,
+                             _c_int64, Geometry, _c_int32, _ptr],
     "lct_count_bad_streams": [_ptr, _ptr, _ptr, _c_int64, _c_int32, _ptr],
     "lct_compact_bad_streams": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64,
                                 _c_int32, _c_int64, _c_int32, _ptr],

@@ -6,6 +6,14 @@ generation`` (padded to 16 bytes) followed by the payload arena; allocation
 and free run on the device (``lct_buffer_allocate`` / ``lct_buffer_free``)
 and return ``[offset, size, status, generation]`` descriptors without a host
 sync.  ``reset()`` bumps the generation so older descriptors become stale.
+
+``CompressedTensor.free()`` (which reports no status) defers its free to the
+buffer's next reservation on the same stream: the compressed-output paths
+reserve and compact in one launch (``lct_allocate_compact``) that first
+applies the deferred frees, in order and under the same lock, so the arena
+holds exactly what an immediate free would have left.  Every other operation
+on the buffer (``allocate``, ``free``, ``reset``, the free-list snapshot
+helpers) and a change of stream first launch the deferred frees as they are.
 """
 from __future__ import annotations
 
@@ -43,9 +51,9 @@ class Allocation:
 
 
 def _free_now(storage: torch.Tensor, descriptor: torch.Tensor,
-              max_free_regions: int) -> torch.Tensor:
+              max_free_regions: int, stream: int | None = None) -> torch.Tensor:
     status = torch.empty(1, dtype=torch.int32, device=storage.device)
-    dispatch.buffer_free(storage, max_free_regions, descriptor, status)
+    dispatch.buffer_free(storage, max_free_regions, descriptor, status, stream=stream)
     return status
 
 
@@ -86,6 +94,10 @@ class TensorBuffer:
         self._lock = meta.narrow(0, 2 * regions + 1, 1)
         self._generation = meta.narrow(0, 2 * regions + 2, 1)
         self._data = self._storage.narrow(0, self._metadata_bytes, self.capacity_bytes)
+        # Descriptors whose free waits for the next reservation, and the raw
+        # handle of the stream they were freed on.
+        self._pending_frees: list[torch.Tensor] = []
+        self._pending_stream = 0
         self.reset()
 
     @staticmethod
@@ -102,8 +114,49 @@ class TensorBuffer:
         """Metadata followed by the arena; the allocator kernels take its base."""
         return self._storage
 
+    def _current_stream(self) -> int:
+        return torch._C._cuda_getCurrentRawStream(self._storage.get_device())
+
+    def _defer_free(self, descriptor: torch.Tensor) -> None:
+        """Free ``descriptor`` at the next reservation on the current stream."""
+        stream = self._current_stream()
+        if self._pending_frees and (stream != self._pending_stream
+                                    or len(self._pending_frees) == dispatch.MAX_PENDING_FREES):
+            self._flush_frees()
+        self._pending_frees.append(descriptor)
+        self._pending_stream = stream
+
+    def _take_frees(self) -> list[torch.Tensor]:
+        """The deferred frees for a reservation on the current stream (those
+        deferred on another stream are launched there first instead)."""
+        if not self._pending_frees:
+            return []
+        if self._pending_stream != self._current_stream():
+            self._flush_frees()
+            return []
+        frees, self._pending_frees = self._pending_frees, []
+        return frees
+
+    def _flush_frees(self) -> None:
+        """Launch the deferred frees, in order, on the stream they were made
+        on; when that is not the current stream, the current stream then
+        waits for them, so work enqueued on it from here on (after any
+        ``wait_stream`` the caller made since the frees) follows them, as it
+        would have followed an immediate free.  That stream must still exist."""
+        if not self._pending_frees:
+            return
+        frees, self._pending_frees = self._pending_frees, []
+        for descriptor in frees:
+            _free_now(self._storage, descriptor, self.max_free_regions,
+                      stream=self._pending_stream)
+        if self._pending_stream != self._current_stream():
+            done = torch.cuda.Event()
+            done.record(torch.cuda.ExternalStream(self._pending_stream, device=self.device))
+            torch.cuda.current_stream(self.device).wait_event(done)
+
     def allocate(self, nbytes: torch.Tensor) -> Allocation:
         """Reserve ``nbytes`` (a one-element device int32 tensor) without a sync."""
+        self._flush_frees()
         descriptor = torch.empty(4, dtype=torch.int32, device=self.device)
         dispatch.buffer_allocate(self._storage, self.max_free_regions, nbytes, None, 0,
                                  descriptor)
@@ -114,6 +167,7 @@ class TensorBuffer:
         """Reserve ``payload_bytes + item_count * item_bytes`` asynchronously."""
         if item_bytes <= 0:
             raise ValueError("item_bytes must be positive")
+        self._flush_frees()
         descriptor = torch.empty(4, dtype=torch.int32, device=self.device)
         dispatch.buffer_allocate(self._storage, self.max_free_regions, payload_bytes,
                                  item_count, int(item_bytes), descriptor)
@@ -129,15 +183,18 @@ class TensorBuffer:
             return tensor_buffer_free(self._storage, allocation.descriptor,
                                       self.max_free_regions)
         # Eager callers skip the operator dispatch (same kernel, same stream).
+        self._flush_frees()
         return _free_now(self._storage, allocation.descriptor, self.max_free_regions)
 
     def reset(self) -> None:
         """Reset asynchronously; previously returned descriptors become stale."""
+        self._flush_frees()
         dispatch.buffer_reset(self._storage, self.max_free_regions, self.capacity_bytes)
 
 
 def _free_regions_snapshot(buffer: TensorBuffer) -> list[tuple[int, int]]:
     """Synchronize and copy the free list as ``[(start, size), ...]``."""
+    buffer._flush_frees()
     regions = buffer.max_free_regions
     meta = buffer._storage.narrow(0, 0, buffer._metadata_bytes).view(torch.int32).cpu()
     count = int(meta[2 * regions].item())

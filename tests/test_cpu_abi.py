@@ -65,7 +65,7 @@ def _nulls(name):
     for argtype in hip._SIGNATURES[name]:
         if argtype is hip.Geometry:
             args.append(hip.Geometry(32768, 256, 128, 12))
-        elif argtype in (ctypes.c_int32, ctypes.c_int64):
+        elif argtype in (ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64):
             args.append(argtype(1))
         else:
             args.append(None)
@@ -91,3 +91,23 @@ def test_bad_geometry_is_rejected_before_launch(lib):
 def test_call_raises_on_error_code(lib):
     with pytest.raises(hip.LCTKernelError, match="lct_decode failed with code -1"):
         hip.call("lct_decode", *_nulls("lct_decode"))
+
+
+def test_allocate_compact_rejects_bad_frees_and_ready_before_launch(lib):
+    fake = ctypes.c_void_p(1 << 20)   # never dereferenced: the checks fail first
+    geometry = hip.Geometry(32768, 256, 128, 12)
+
+    def call(frees, ready=fake):
+        return lib.lct_allocate_compact(fake, fake, fake, fake, fake, 256, fake, fake, fake,
+                                        frees, ready, 1, 32768, 32768, geometry, 0, None)
+
+    too_many = hip.PendingFrees()
+    too_many.count = hip.MAX_PENDING_FREES + 1
+    assert call(ctypes.byref(too_many)) == -4          # LCT_E_ARG
+    missing = hip.PendingFrees()
+    missing.count = 1                                  # descriptor[0] is NULL
+    assert call(ctypes.byref(missing)) == LCT_E_NULL
+    assert call(None, ready=ctypes.c_void_p((1 << 20) + 4)) == -4   # ready not 8-byte aligned
+    bad_regions = lib.lct_allocate_compact(fake, fake, fake, fake, fake, 100, fake, fake, fake,
+                                           None, fake, 1, 32768, 32768, geometry, 0, None)
+    assert bad_regions == -4
