@@ -6,9 +6,15 @@
 // that fits the 16-byte-aligned request; free re-inserts a region, merging it
 // with its neighbours, and rejects stale or already-freed descriptors.
 //
-// The lock is taken with an agent-scope compare-and-swap by one thread; unlike
-// the reference's unbounded spin, the wait is bounded, and an allocator call
-// that cannot take the lock reports status LCT_STATUS_LOCK and changes nothing.
+// The lock word is versioned: even = free, odd = held; the holder that took
+// it at value v releases it with v + 2 (the reference's lock is 0/1,
+// LCT/kernels/tensor_buffer.py:7-15).  It is taken with an agent-scope
+// compare-and-swap by one thread; unlike the reference's unbounded spin, the
+// wait is bounded, and an allocator call that cannot take the lock reports
+// status LCT_STATUS_LOCK and changes nothing.  The version lets a caller read
+// the free list before it owns the lock: a snapshot read after the lock was
+// seen free at v is exactly current if the compare-and-swap v -> v + 1 then
+// succeeds (no holder came and went in between).
 #pragma once
 
 #include "lct_device.h"
@@ -38,33 +44,48 @@ struct AllocatorMeta {
           generation(meta + 2 * r + 2), regions(r) {}
 };
 
-// Returns true in every thread if the lock was taken.  Contains barriers.
-__device__ __forceinline__ bool allocator_lock(int32_t *lock, int32_t *flag) {
-    if (threadIdx.x == 0) {
-        int32_t got = 0;
-        for (int i = 0; i < kLockSpinLimit; ++i) {
-            int32_t expected = 0;
-            if (__hip_atomic_compare_exchange_strong(lock, &expected, 1, __ATOMIC_ACQUIRE,
-                                                     __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT)) {
-                got = 1;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-        }
-        *flag = got;
-    }
-    __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    return *flag != 0;
+// A value another workgroup wrote (or may be writing) in this launch: an
+// agent-scope load reads the coherent copy, where a plain load could hit a
+// stale line of this XCD's L2.
+__device__ __forceinline__ int32_t coherent_load(const int32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Publishes every thread's metadata writes, then releases.  Contains barriers.
-__device__ __forceinline__ void allocator_unlock(int32_t *lock) {
+// Thread 0's bounded wait for the lock; returns the version taken (even), or
+// -1.  `seen` is a value of the lock word already read, or -1.
+__device__ __forceinline__ int32_t take_lock_thread0(int32_t *lock, int32_t seen) {
+    int32_t v = seen;
+    for (int i = 0; i < kLockSpinLimit; ++i) {
+        if (v >= 0 && (v & 1) == 0) {
+            int32_t expected = v;
+            if (__hip_atomic_compare_exchange_strong(lock, &expected, v + 1, __ATOMIC_ACQUIRE,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                return v;
+            v = expected;
+            if ((v & 1) == 0) continue;
+        }
+        __builtin_amdgcn_s_sleep(2);
+        v = coherent_load(lock);
+    }
+    return -1;
+}
+
+// Returns the version taken (>= 0) in every thread, or -1 if the lock was not
+// taken.  flag: one LDS int.  Contains barriers.
+__device__ __forceinline__ int32_t allocator_lock(int32_t *lock, int32_t *flag) {
+    if (threadIdx.x == 0) *flag = take_lock_thread0(lock, coherent_load(lock));
+    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    return *flag;
+}
+
+// Publishes every thread's metadata writes, then releases the version `held`
+// took.  Contains barriers.
+__device__ __forceinline__ void allocator_unlock(int32_t *lock, int32_t held) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     if (threadIdx.x == 0)
-        __hip_atomic_store(lock, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(lock, held + 2, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Block-wide minimum; scratch holds kWavesPerBlock ints.  Contains barriers.
@@ -134,12 +155,14 @@ struct AllocatorSnapshot {
     RegionRegs r;
     int32_t generation;
     int32_t count;
+    int32_t held;   // version the lock was taken at
     bool locked;
 };
 
 __device__ __forceinline__ void allocator_begin(const AllocatorMeta &m, AllocatorSnapshot &snap,
                                                 int32_t *flag) {
-    snap.locked = allocator_lock(m.lock, flag);
+    snap.held = allocator_lock(m.lock, flag);
+    snap.locked = snap.held >= 0;
     snap.generation = 0;
     snap.count = 0;
     if (!snap.locked) return;
@@ -188,7 +211,7 @@ __device__ __forceinline__ void allocator_finish(const AllocatorMeta &m,
         descriptor[2] = request <= 0 ? kStatusEmpty : (success ? kStatusOk : kStatusNoFit);
         descriptor[3] = snap.generation;
     }
-    allocator_unlock(m.lock);
+    allocator_unlock(m.lock, snap.held);
 }
 
 __device__ __forceinline__ void allocator_allocate(const AllocatorMeta &m, int32_t request,
@@ -265,28 +288,144 @@ __device__ __forceinline__ int32_t allocator_free_locked(const AllocatorMeta &m,
 // tensor_buffer.py:94-179.  Returns the status in every thread.
 __device__ __forceinline__ int32_t allocator_free(const AllocatorMeta &m, int32_t *descriptor,
                                                   int32_t *scratch, int32_t *flag) {
-    if (!allocator_lock(m.lock, flag)) return kStatusLock;
+    const int32_t held = allocator_lock(m.lock, flag);
+    if (held < 0) return kStatusLock;
     const int32_t result = allocator_free_locked(m, descriptor, scratch);
-    allocator_unlock(m.lock);
+    allocator_unlock(m.lock, held);
     return result;
 }
 
-// allocator_begin that first returns the caller's deferred frees, in order,
-// under the same lock (each exactly as allocator_free would, its status
-// discarded), so the allocation that follows sees the free list those frees
-// leave.  Contains barriers.
-__device__ __forceinline__ void allocator_begin_after_frees(const AllocatorMeta &m,
-                                                            AllocatorSnapshot &snap,
-                                                            const lct_pending_frees &frees,
-                                                            int32_t *flag, int32_t *scratch) {
-    snap.locked = allocator_lock(m.lock, flag);
-    snap.generation = 0;
-    snap.count = 0;
-    if (!snap.locked) return;
-    for (int i = 0; i < frees.count; ++i) allocator_free_locked(m, frees.descriptor[i], scratch);
-    snap.generation = *m.generation;
-    snap.count = *m.count;
-    load_regions(m, snap.r);
+
+// ---- The free list on an LDS copy (one workgroup holding the lock): frees
+// and a first-fit reservation with no memory round trip, then one write-back.
+// The algorithms are those of allocator_free_locked and allocator_finish.
+struct LdsFreeList {
+    int32_t *start;   // LDS int32[regions]
+    int32_t *size;    // LDS int32[regions]
+    int32_t regions;
+    int32_t count;        // uniform in every thread
+    int32_t generation;   // uniform in every thread
+};
+
+// Entries [from, to) move by delta (+1 or -1).  Contains barriers.
+__device__ __forceinline__ void lds_shift(LdsFreeList &f, int32_t from, int32_t to,
+                                          int32_t delta) {
+    int32_t s[kRegionsPerThread], z[kRegionsPerThread];
+#pragma unroll
+    for (int k = 0; k < kRegionsPerThread; ++k) {
+        const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kLanes;
+        if (i >= from && i < to) {
+            s[k] = f.start[i];
+            z[k] = f.size[i];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kRegionsPerThread; ++k) {
+        const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kLanes;
+        if (i >= from && i < to) {
+            f.start[i + delta] = s[k];
+            f.size[i + delta] = z[k];
+        }
+    }
+    __syncthreads();
+}
+
+// tensor_buffer.py:94-179 on the LDS list for descriptor values d
+// {offset, size, status, generation}; returns the status in every thread.
+// Contains barriers.
+__device__ __forceinline__ int32_t lds_free(LdsFreeList &f, const int32_t (&d)[4],
+                                            int32_t *scratch) {
+    const int32_t offset = d[0], size = d[1];
+    if (!(d[2] == kStatusOk && d[3] == f.generation && offset >= 0 && size > 0))
+        return kStatusInvalid;
+    const int32_t count = f.count;
+    int32_t below = 0;
+#pragma unroll
+    for (int k = 0; k < kRegionsPerThread; ++k) {
+        const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kLanes;
+        below += (i < count && f.start[i] < offset) ? 1 : 0;
+    }
+    const int32_t insert = block_sum(below, scratch);
+    const bool has_prev = insert > 0, has_next = insert < count;
+    const int32_t prev_start = has_prev ? f.start[insert - 1] : 0;
+    const int32_t prev_size = has_prev ? f.size[insert - 1] : 0;
+    const int32_t next_start = has_next ? f.start[insert] : 0;
+    const int32_t next_size = has_next ? f.size[insert] : 0;
+    const bool merge_prev = has_prev && prev_start + prev_size == offset;
+    const bool merge_next = has_next && offset + size == next_start;
+    __syncthreads();   // every thread has read its neighbours before any write
+    if (merge_prev && merge_next) {
+        if (threadIdx.x == 0) f.size[insert - 1] = prev_size + size + next_size;
+        __syncthreads();
+        lds_shift(f, insert + 1, count, -1);
+        f.count = count - 1;
+    } else if (merge_prev) {
+        if (threadIdx.x == 0) f.size[insert - 1] = prev_size + size;
+        __syncthreads();
+    } else if (merge_next) {
+        if (threadIdx.x == 0) {
+            f.start[insert] = offset;
+            f.size[insert] = next_size + size;
+        }
+        __syncthreads();
+    } else if (count < f.regions) {
+        lds_shift(f, insert, count, +1);
+        if (threadIdx.x == 0) {
+            f.start[insert] = offset;
+            f.size[insert] = size;
+        }
+        __syncthreads();
+        f.count = count + 1;
+    } else {
+        return kStatusFreeListFull;
+    }
+    return kStatusOk;
+}
+
+// tensor_buffer.py:37-91 on the LDS list: the first region that holds the
+// 16-byte-aligned request.  Writes {offset, size, status} (uniform) to out.
+// Contains barriers.
+__device__ __forceinline__ void lds_reserve(LdsFreeList &f, int32_t request, int32_t *scratch,
+                                            int32_t (&out)[3]) {
+    const int32_t count = f.count;
+    const int32_t size = ((request + kAlignment - 1) / kAlignment) * kAlignment;
+    int32_t candidate = f.regions;
+#pragma unroll
+    for (int k = kRegionsPerThread - 1; k >= 0; --k) {
+        const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kLanes;
+        if (i < count && f.size[i] >= size) candidate = i;
+    }
+    const int32_t slot = block_min(candidate, scratch);
+    const bool success = request > 0 && slot < count;
+    int32_t start = 0;
+    if (success) {
+        start = f.start[slot];
+        const int32_t region = f.size[slot];
+        __syncthreads();
+        if (region == size) {
+            lds_shift(f, slot + 1, count, -1);
+            f.count = count - 1;
+        } else {
+            if (threadIdx.x == 0) {
+                f.start[slot] = start + size;
+                f.size[slot] = region - size;
+            }
+            __syncthreads();
+        }
+    }
+    out[0] = success ? start : -1;
+    out[1] = success ? size : 0;
+    out[2] = request <= 0 ? kStatusEmpty : (success ? kStatusOk : kStatusNoFit);
+}
+
+// Entries [0, count) and the count back to the buffer's metadata.
+__device__ __forceinline__ void lds_write_back(const LdsFreeList &f, const AllocatorMeta &m) {
+    for (int32_t i = threadIdx.x; i < f.count; i += kLanes) {
+        m.starts[i] = f.start[i];
+        m.sizes[i] = f.size[i];
+    }
+    if (threadIdx.x == 0) *m.count = f.count;
 }
 
 }  // namespace lct

@@ -58,20 +58,17 @@ __device__ __forceinline__ void block_exclusive_scan3(const int32_t (&v)[3], int
 // and reads its free list while the first pass's loads are in flight, and
 // before scanning, so those latencies overlap.
 //
-// A buffered call may first apply deferred frees (`frees`) under the same lock,
-// before the free list is read for the reservation.  Workgroup-wide; contains
-// barriers.
+// The reservation is a policy: `reserve.begin(scratch)` runs once the first
+// pass's loads are issued (a buffered call takes the arena lock and reads the
+// free list there, overlapping those latencies), `reserve.finish(request,
+// scratch)` at the end.  Workgroup-wide; contains barriers.
+template <class Reserve>
 __device__ __forceinline__ void scan_allocate(int32_t *__restrict__ summaries,
                                               int32_t *__restrict__ counts,
-                                              int32_t *__restrict__ descriptor,
-                                              int32_t *__restrict__ buffer_meta,
                                               int32_t *__restrict__ blocks, int32_t n_blocks,
-                                              int32_t buffered, int32_t max_free_regions,
-                                              const lct_pending_frees &frees) {
+                                              Reserve &reserve) {
     __shared__ int32_t scratch[3 * kWavesPerBlock];
-    __shared__ int32_t flag;
     const int t = threadIdx.x;
-    const AllocatorMeta meta(buffer_meta, max_free_regions);
     const int64_t nb = n_blocks;
     const uint32_t bytes = static_cast<uint32_t>(n_blocks) * 4u;
     const __amdgpu_buffer_rsrc_t count_in = make_rsrc(summaries, bytes);
@@ -112,8 +109,7 @@ __device__ __forceinline__ void scan_allocate(int32_t *__restrict__ summaries,
     // The first pass's loads are issued before the arena lock is requested,
     // so their latency and the lock's overlap.
     load_pass(0);
-    AllocatorSnapshot snap;
-    if (buffered) allocator_begin_after_frees(meta, snap, frees, &flag, scratch);
+    reserve.begin(scratch);
     for (int base = 0; base < n_blocks; base += kPrefixPass) {
         const int32_t first_block = base + t * kPrefixPer;
         const uint32_t off = static_cast<uint32_t>(first_block) * 4u;
@@ -182,17 +178,137 @@ __device__ __forceinline__ void scan_allocate(int32_t *__restrict__ summaries,
         summaries[5 * nb] = carry[2];
     }
     // Two metadata bytes per overflowing stream: lane, then start step.
-    if (buffered) allocator_finish(meta, snap, carry[1] + 2 * carry[0], descriptor, scratch);
+    reserve.finish(carry[1] + 2 * carry[0], scratch);
 }
+
+// lct_prefix_allocate's reservation: the lock, then the free list in
+// registers (allocator_begin / allocator_finish); nothing when not buffered.
+struct RegisterReserve {
+    AllocatorMeta meta;
+    int32_t *descriptor;
+    int32_t *flag;   // one LDS int
+    bool active;
+    AllocatorSnapshot snap;
+
+    __device__ void begin(int32_t *) {
+        if (active) allocator_begin(meta, snap, flag);
+    }
+    __device__ void finish(int32_t request, int32_t *scratch) {
+        if (active) allocator_finish(meta, snap, request, descriptor, scratch);
+    }
+};
+
+// lct_allocate_compact's reservation (workgroup 0).  begin: thread 0 reads
+// the lock word while the first pass's loads and the pending descriptors'
+// values are in flight; then, with the lock seen free at version v, thread 0
+// takes it (v -> v + 1) while every thread reads the free list into LDS with
+// agent-scope loads: the copy is current exactly when that compare-and-swap
+// succeeds (otherwise the lock is waited for and the list read again).  The
+// deferred frees then run on the LDS copy, in order.  finish: the first-fit
+// reservation on the LDS copy, the list written back, the descriptor, and one
+// agent-scope release that publishes every write of the workgroup before the
+// lock goes to v + 2.  Two memory round trips before the scan, where the
+// register path takes three (lock, fence, list) plus one per free.
+struct LdsReserve {
+    AllocatorMeta meta;
+    int32_t *descriptor;
+    lct_pending_frees frees;
+    int32_t *list;   // LDS int32[2 * regions]: starts, then sizes
+    LdsFreeList f;
+    int32_t held;
+
+    __device__ void read_list(int32_t *shared) {
+        const int32_t regions = meta.regions;
+        for (int32_t i = threadIdx.x; i < regions; i += kLanes) {
+            list[i] = coherent_load(meta.starts + i);
+            list[regions + i] = coherent_load(meta.sizes + i);
+        }
+        if (threadIdx.x == 0) {
+            shared[2] = coherent_load(meta.count);
+            shared[3] = coherent_load(meta.generation);
+        }
+    }
+
+    __device__ void begin(int32_t *scratch) {
+        __shared__ int32_t shared[4];   // seen version, held version, count, generation
+        __shared__ int32_t pending[LCT_MAX_PENDING_FREES][4];
+        const int t = threadIdx.x;
+        if (t == 0) shared[0] = coherent_load(meta.lock);
+#pragma unroll
+        for (int j = 0; j < LCT_MAX_PENDING_FREES; ++j)
+            if (j < frees.count && t < 4) pending[j][t] = frees.descriptor[j][t];
+        __syncthreads();
+        const int32_t seen = shared[0];
+        if ((seen & 1) == 0) {
+            if (t == 0) {
+                int32_t expected = seen;
+                shared[1] = __hip_atomic_compare_exchange_strong(
+                                meta.lock, &expected, seen + 1, __ATOMIC_ACQUIRE,
+                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                ? seen
+                                : -1;
+            }
+            read_list(shared);
+        } else if (t == 0) {
+            shared[1] = -1;
+        }
+        __syncthreads();
+        held = shared[1];
+        if (held < 0) {
+            if (t == 0) shared[1] = take_lock_thread0(meta.lock, -1);
+            __syncthreads();
+            held = shared[1];
+            if (held >= 0) read_list(shared);
+            __syncthreads();
+        }
+        f = LdsFreeList{list, list + meta.regions, meta.regions, shared[2], shared[3]};
+        if (held < 0) return;
+#pragma unroll
+        for (int j = 0; j < LCT_MAX_PENDING_FREES; ++j) {
+            if (j < frees.count) {
+                const int32_t d[4] = {pending[j][0], pending[j][1], pending[j][2], pending[j][3]};
+                if (lds_free(f, d, scratch) == kStatusOk && t == 0)
+                    frees.descriptor[j][2] = kStatusFreed;
+            }
+        }
+    }
+
+    __device__ void finish(int32_t request, int32_t *scratch) {
+        const int t = threadIdx.x;
+        if (held < 0) {
+            if (t == 0) {
+                descriptor[0] = -1;
+                descriptor[1] = 0;
+                descriptor[2] = kStatusLock;
+                descriptor[3] = -1;
+            }
+        } else {
+            int32_t out[3];
+            lds_reserve(f, request, scratch, out);
+            lds_write_back(f, meta);
+            if (t == 0) {
+                descriptor[0] = out[0];
+                descriptor[1] = out[1];
+                descriptor[2] = out[2];
+                descriptor[3] = f.generation;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __syncthreads();
+        if (held >= 0 && t == 0)
+            __hip_atomic_store(meta.lock, held + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+};
 
 __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     int32_t *__restrict__ summaries, int32_t *__restrict__ counts,
     int32_t *__restrict__ descriptor, int32_t *__restrict__ buffer_meta,
     int32_t *__restrict__ blocks, int32_t n_blocks, int32_t buffered,
     int32_t max_free_regions) {
-    const lct_pending_frees none{};
-    scan_allocate(summaries, counts, descriptor, buffer_meta, blocks, n_blocks, buffered,
-                  max_free_regions, none);
+    __shared__ int32_t flag;
+    RegisterReserve reserve{AllocatorMeta(buffer_meta, max_free_regions), descriptor, &flag,
+                            buffered != 0, {}};
+    scan_allocate(summaries, counts, blocks, n_blocks, reserve);
 }
 
 // One codec block's overflow entries and tails (compaction.py:137-228).  The
@@ -313,13 +429,14 @@ __global__ __launch_bounds__(kLanes) void allocate_compact_kernel(
     int32_t *__restrict__ blocks, const uint8_t *__restrict__ extra_starts,
     lct_pending_frees frees, uint64_t *__restrict__ ready, uint64_t epoch, int32_t n_blocks,
     int64_t logical_numel, int S, int precomputed) {
+    extern __shared__ int32_t free_list[];   // 2 * max_free_regions ints (workgroup 0)
     if (blockIdx.x == 0) {
-        scan_allocate(summaries, counts, descriptor, buffer_meta, blocks, n_blocks, 1,
-                      max_free_regions, frees);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __syncthreads();
+        LdsReserve reserve{AllocatorMeta(buffer_meta, max_free_regions), descriptor, frees,
+                           free_list, {}, -1};
+        scan_allocate(summaries, counts, blocks, n_blocks, reserve);
+        // finish() released every write of the workgroup at agent scope.
         if (threadIdx.x == 0)
-            __hip_atomic_store(ready, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ready, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     __shared__ int32_t go;
@@ -527,7 +644,8 @@ extern "C" int32_t lct_allocate_compact(const void *source, int32_t *summaries,
     // (every one fits on the device at once next to workgroup 0).
     const uint32_t grid = 1u + static_cast<uint32_t>(
         n_blocks < kAllocateCompactWaiters ? n_blocks : kAllocateCompactWaiters);
-    hipLaunchKernelGGL(allocate_compact_kernel, dim3(grid), dim3(kLanes), 0, stream, source,
+    const size_t lds = static_cast<size_t>(max_free_regions) * 8;
+    hipLaunchKernelGGL(allocate_compact_kernel, dim3(grid), dim3(kLanes), lds, stream, source,
                        summaries, counts, descriptor, buffer_meta, max_free_regions, arena,
                        blocks, extra_starts, pending, ready, epoch,
                        static_cast<int32_t>(n_blocks), logical_numel, g.steps, precomputed);

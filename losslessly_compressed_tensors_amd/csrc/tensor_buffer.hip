@@ -18,7 +18,10 @@ __global__ __launch_bounds__(kLanes) void buffer_reset_kernel(int32_t *__restric
     }
     if (threadIdx.x == 0) {
         *m.count = 1;
-        *m.lock = 0;
+        // The next free version (the reference stores 0): a free-list snapshot
+        // taken before the reset cannot validate against the lock afterwards.
+        const int32_t version = coherent_load(m.lock);
+        __hip_atomic_store(m.lock, (version | 1) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *m.generation = *m.generation + 1;
     }
 }
