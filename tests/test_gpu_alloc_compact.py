@@ -253,3 +253,43 @@ def test_deferred_free_then_explicit_allocate_and_stream_change():
     torch.cuda.synchronize()
     assert int(cts[2][1].fallback_descriptor[2].item()) == 5
     assert _free_regions_snapshot(buf_b) == [(0, 1 << 20)]
+
+
+def test_one_launch_free_list_full():
+    """A deferred free that needs a new region when the list is full (status 3
+    in the reference) changes nothing, as an immediate free would."""
+    require_gpu()
+    print("case allocate_compact free list full", flush=True)
+    x = _patterns(41, 65536)
+    src, extra, summaries, (B, L, S, W), nb, size, n = _encode(x, SPARSE)
+    buffers = []
+    for _ in range(2):
+        buffer = TensorBuffer(1 << 20, max_free_regions=4, device="cuda")
+        allocations = [buffer.allocate(torch.tensor([4096], dtype=torch.int32, device="cuda"))
+                       for _ in range(8)]
+        for i in (0, 2, 4):
+            buffer.free(allocations[i])   # three holes + the tail: the list is full
+        buffers.append((buffer, allocations))
+    (buf_a, alloc_a), (buf_b, alloc_b) = buffers
+    status = buf_a.free(alloc_a[6])
+    sum_a, sum_b = summaries.clone(), summaries.clone()
+    outs = [tuple(torch.empty(k, dtype=torch.int32, device="cuda") for k in (4, 4, 3 * nb))
+            for _ in range(2)]
+    dispatch.prefix_allocate(sum_a, outs[0][0], outs[0][1], buf_a, outs[0][2], nb, True,
+                             buf_a.max_free_regions)
+    arena_a = buf_a.data
+    storage = FallbackStorage(tail=arena_a, count=outs[0][0][:1], lanes=arena_a, starts=arena_a,
+                              blocks=outs[0][2], descriptor=outs[0][1], allocation=outs[0][1])
+    dispatch.compact_extra(src, storage, nb, size, precomputed=False, buffered=True,
+                           logical_numel=n, block_symbols=B, lanes=L, steps=S,
+                           extra_starts=extra, summaries=sum_a)
+    dispatch.allocate_compact(src, sum_b, outs[1][0], outs[1][1], buf_b, outs[1][2], extra,
+                              [alloc_b[6].descriptor], nb, size, logical_numel=n,
+                              block_symbols=B, lanes=L, steps=S, precomputed=False)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 3
+    assert int(alloc_b[6].descriptor[2].item()) == 0   # not freed
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
+    assert _free_regions_snapshot(buf_a) == _free_regions_snapshot(buf_b)
+    assert torch.equal(buf_a.data, buf_b.data)
