@@ -177,3 +177,94 @@ def test_reference_module_paths_resolve_to_this_package(name):
     assert importlib.import_module(f"LCT.{name}") is ours
     from LCT.operations import compress as lct_compress
     assert lct_compress is compress
+
+
+class _FakeEvent:
+    def __init__(self, log):
+        self.log = log
+
+    def record(self, stream):
+        self.log.append(("record", stream))
+
+
+class _FakeStream:
+    def __init__(self, log):
+        self.log = log
+
+    def wait_event(self, event):
+        self.log.append(("wait",))
+
+
+@pytest.fixture
+def deferral(monkeypatch):
+    """A TensorBuffer whose device calls are recorded instead of launched:
+    ``state.stream`` is the current raw stream; ``log`` collects the frees
+    (descriptor, stream), event records and stream waits in order."""
+    from losslessly_compressed_tensors_amd import tensor_buffer as tb
+
+    log = []
+    state = type("State", (), {"stream": 11})()
+    buf = object.__new__(tb.TensorBuffer)
+    buf._storage = torch.zeros(64, dtype=torch.uint8)
+    buf.max_free_regions = 4
+    buf.capacity_bytes = 16
+    buf._metadata_bytes = 48
+    buf.device = torch.device("cpu")
+    buf._pending_frees = []
+    buf._pending_stream = 0
+    monkeypatch.setattr(tb.TensorBuffer, "_current_stream", lambda self: state.stream)
+    monkeypatch.setattr(tb, "_free_now",
+                        lambda storage, d, regions, stream=None: log.append(("free", d, stream)))
+    monkeypatch.setattr(tb.torch.cuda, "Event", lambda: _FakeEvent(log))
+    monkeypatch.setattr(tb.torch.cuda, "ExternalStream", lambda handle, device=None: handle)
+    monkeypatch.setattr(tb.torch.cuda, "current_stream", lambda device=None: _FakeStream(log))
+    monkeypatch.setattr(tb.dispatch, "buffer_reset", lambda *a: log.append(("reset",)))
+    return buf, state, log
+
+
+def test_deferred_frees_ride_on_the_next_reservation_in_order(deferral):
+    buf, state, log = deferral
+    buf._defer_free("d1")
+    buf._defer_free("d2")
+    buf._defer_free("d3")
+    assert log == []                                  # nothing launched yet
+    assert buf._take_frees() == ["d1", "d2", "d3"]    # one reservation takes them in order
+    assert buf._take_frees() == [] and log == []
+
+
+def test_a_full_pending_list_is_launched_before_the_next_free(deferral):
+    from losslessly_compressed_tensors_amd.kernels import dispatch
+    buf, state, log = deferral
+    names = [f"d{i}" for i in range(dispatch.MAX_PENDING_FREES + 1)]
+    for name in names:
+        buf._defer_free(name)
+    launched = [entry[1] for entry in log if entry[0] == "free"]
+    assert launched == names[:dispatch.MAX_PENDING_FREES]   # launched on their own stream
+    assert all(entry[2] == 11 for entry in log if entry[0] == "free")
+    assert buf._take_frees() == names[dispatch.MAX_PENDING_FREES:]
+
+
+def test_a_change_of_stream_launches_pending_frees_and_orders_the_new_stream(deferral):
+    buf, state, log = deferral
+    buf._defer_free("d1")
+    state.stream = 22
+    assert buf._take_frees() == []                    # not taken on another stream
+    assert log == [("free", "d1", 11), ("record", 11), ("wait",)]
+    log.clear()
+    buf._defer_free("d2")                             # now deferred on stream 22
+    state.stream = 33
+    buf._defer_free("d3")                             # a free on a third stream flushes d2 first
+    assert log == [("free", "d2", 22), ("record", 22), ("wait",)]
+    assert buf._take_frees() == ["d3"]
+
+
+def test_every_other_buffer_operation_launches_pending_frees_first(deferral):
+    buf, state, log = deferral
+    buf._defer_free("d1")
+    buf.reset()
+    assert log == [("free", "d1", 11), ("reset",)]    # same stream: no wait needed
+    log.clear()
+    buf._defer_free("d2")
+    buf._flush_frees()
+    buf._flush_frees()                                # idempotent
+    assert log == [("free", "d2", 11)]
