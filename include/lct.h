@@ -178,7 +178,8 @@ int32_t lct_prefix_allocate(int32_t *summaries, int32_t *counts,
  * stores `epoch` to *ready.  Every other workgroup waits (bounded) until
  * *ready == epoch and then writes the entries and tails of the listed blocks,
  * as lct_compact_extra with buffered = 1 (lanes, starts and tails in `arena`).
- * summaries: int32[5*nb + 1] as for lct_prefix_allocate.  ready: a device
+ * summaries: int32[5*nb + 1] as for lct_prefix_allocate, except that the
+ * exclusive scans [2*nb, 4*nb) are not written (blocks holds them).  ready: a device
  * uint64 whose value before the launch differs from `epoch` (use a value no
  * earlier call used).  The result (counts, descriptor, blocks, arena bytes)
  * equals lct_buffer_free on each pending descriptor followed by

@@ -61,8 +61,10 @@ __device__ __forceinline__ void block_exclusive_scan3(const int32_t (&v)[3], int
 // The reservation is a policy: `reserve.begin(scratch)` runs once the first
 // pass's loads are issued (a buffered call takes the arena lock and reads the
 // free list there, overlapping those latencies), `reserve.finish(request,
-// scratch)` at the end.  Workgroup-wide; contains barriers.
-template <class Reserve>
+// scratch)` at the end.  kWriteScans = false leaves the exclusive scans of
+// summaries[2nb, 4nb) unwritten (the block metadata holds the same values).
+// Workgroup-wide; contains barriers.
+template <bool kWriteScans, class Reserve>
 __device__ __forceinline__ void scan_allocate(int32_t *__restrict__ summaries,
                                               int32_t *__restrict__ counts,
                                               int32_t *__restrict__ blocks, int32_t n_blocks,
@@ -140,8 +142,10 @@ __device__ __forceinline__ void scan_allocate(int32_t *__restrict__ summaries,
 #pragma unroll
             for (int k = 0; k < kPrefixPer; ++k) {
                 const uint32_t o = off + 4 * k;
-                __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(firsts[k]), first_out, o, 0, 0);
-                __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(bases[k]), base_out, o, 0, 0);
+                if (kWriteScans) {
+                    __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(firsts[k]), first_out, o, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(bases[k]), base_out, o, 0, 0);
+                }
                 __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(c[k]), meta_count, o, 0, 0);
                 __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(firsts[k]), meta_first, o, 0, 0);
                 __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(bases[k]), meta_base, o, 0, 0);
@@ -161,8 +165,10 @@ __device__ __forceinline__ void scan_allocate(int32_t *__restrict__ summaries,
             const u32x4 cq = {static_cast<uint32_t>(c[4 * q]), static_cast<uint32_t>(c[4 * q + 1]),
                               static_cast<uint32_t>(c[4 * q + 2]),
                               static_cast<uint32_t>(c[4 * q + 3])};
-            __builtin_amdgcn_raw_buffer_store_b128(fq, first_out, off + 16 * q, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(bq, base_out, off + 16 * q, 0, 0);
+            if (kWriteScans) {
+                __builtin_amdgcn_raw_buffer_store_b128(fq, first_out, off + 16 * q, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(bq, base_out, off + 16 * q, 0, 0);
+            }
             __builtin_amdgcn_raw_buffer_store_b128(cq, meta_count, off + 16 * q, 0, 0);
             __builtin_amdgcn_raw_buffer_store_b128(fq, meta_first, off + 16 * q, 0, 0);
             __builtin_amdgcn_raw_buffer_store_b128(bq, meta_base, off + 16 * q, 0, 0);
@@ -308,7 +314,7 @@ __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     __shared__ int32_t flag;
     RegisterReserve reserve{AllocatorMeta(buffer_meta, max_free_regions), descriptor, &flag,
                             buffered != 0, {}};
-    scan_allocate(summaries, counts, blocks, n_blocks, reserve);
+    scan_allocate<true>(summaries, counts, blocks, n_blocks, reserve);
 }
 
 // One codec block's overflow entries and tails (compaction.py:137-228).  The
@@ -433,7 +439,7 @@ __global__ __launch_bounds__(kLanes) void allocate_compact_kernel(
     if (blockIdx.x == 0) {
         LdsReserve reserve{AllocatorMeta(buffer_meta, max_free_regions), descriptor, frees,
                            free_list, {}, -1};
-        scan_allocate(summaries, counts, blocks, n_blocks, reserve);
+        scan_allocate<false>(summaries, counts, blocks, n_blocks, reserve);
         // finish() released every write of the workgroup at agent scope.
         if (threadIdx.x == 0)
             __hip_atomic_store(ready, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
