@@ -317,37 +317,55 @@ __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     scan_allocate<true>(summaries, counts, blocks, n_blocks, reserve);
 }
 
-// One codec block's overflow entries and tails (compaction.py:137-228).  The
-// block's tail bytes are produced one per thread: tail byte i belongs to the
-// overflowing lane whose local byte range holds i (binary search over the
-// lanes' offsets in LDS), so every byte is an independent load and the tail
-// stores are contiguous.
-__device__ __forceinline__ void compact_block(
-    const void *__restrict__ source, uint8_t *__restrict__ lanes, uint8_t *__restrict__ starts,
-    uint8_t *__restrict__ tail, int64_t lane_off, int64_t start_off, int64_t tail_off,
-    int32_t count, int32_t first, int32_t byte_base,
-    const uint8_t *__restrict__ extra_starts, int64_t block, int64_t logical_numel, int S,
-    int precomputed, int32_t *scratch, int32_t *entry_offset, int32_t *entry_start,
-    int32_t *entry_lane) {
+// One codec block's overflow entries and tails (compaction.py:137-228), in
+// two halves.  rank_block needs nothing from the reservation: it ranks the
+// block's overflowing lanes (ascending) and puts each one's tail offset, start
+// and lane in LDS.  write_block then stores the entries at `first` and the
+// tails at `byte_base`: tail byte i belongs to the overflowing lane whose local
+// byte range holds i (binary search over the offsets in LDS), so every byte is
+// an independent load and the tail stores are contiguous.
+struct BlockEntries {
+    int32_t start;   // this lane's first overflow step (255: none)
+    int32_t rank;    // this lane's entry index in the block, if it overflows
+    int32_t count;   // entries of the block (uniform)
+    int32_t bytes;   // tail bytes of the block (uniform)
+};
+
+__device__ __forceinline__ BlockEntries rank_block(const uint8_t *__restrict__ extra_starts,
+                                                   int64_t block, int S, int32_t *scratch,
+                                                   int32_t *entry_offset, int32_t *entry_start,
+                                                   int32_t *entry_lane) {
     const int t = threadIdx.x;
-    const int32_t start = extra_starts[block * kLanes + t];
-    const bool bad = start != 255;
-    int32_t block_bytes, ignored;
-    const int32_t local = block_exclusive_scan(bad ? S - start : 0, scratch, &block_bytes);
-    const int32_t rank = block_exclusive_scan(bad ? 1 : 0, scratch, &ignored);
+    BlockEntries e;
+    e.start = extra_starts[block * kLanes + t];
+    const bool bad = e.start != 255;
+    const int32_t local = block_exclusive_scan(bad ? S - e.start : 0, scratch, &e.bytes);
+    e.rank = block_exclusive_scan(bad ? 1 : 0, scratch, &e.count);
     if (bad) {
-        lanes[lane_off + first + rank] = static_cast<uint8_t>(t);
-        starts[start_off + first + rank] = static_cast<uint8_t>(start);
-        entry_offset[rank] = local;
-        entry_start[rank] = start;
-        entry_lane[rank] = t;
+        entry_offset[e.rank] = local;
+        entry_start[e.rank] = e.start;
+        entry_lane[e.rank] = t;
     }
     __syncthreads();
+    return e;
+}
+
+__device__ __forceinline__ void write_block(
+    const void *__restrict__ source, uint8_t *__restrict__ lanes, uint8_t *__restrict__ starts,
+    uint8_t *__restrict__ tail, int64_t lane_off, int64_t start_off, int64_t tail_off,
+    int32_t first, int32_t byte_base, const BlockEntries &e, int64_t block,
+    int64_t logical_numel, int S, int precomputed, const int32_t *entry_offset,
+    const int32_t *entry_start, const int32_t *entry_lane) {
+    const int t = threadIdx.x;
+    if (e.start != 255) {
+        lanes[lane_off + first + e.rank] = static_cast<uint8_t>(t);
+        starts[start_off + first + e.rank] = static_cast<uint8_t>(e.start);
+    }
     uint8_t *out = tail + tail_off + byte_base;
     const int64_t row_base = block * S;
-    for (int32_t i = t; i < block_bytes; i += kLanes) {
+    for (int32_t i = t; i < e.bytes; i += kLanes) {
         // Last entry whose offset is <= i.
-        int32_t lo = 0, hi = count - 1;
+        int32_t lo = 0, hi = e.count - 1;
         while (lo < hi) {
             const int32_t mid = (lo + hi + 1) >> 1;
             if (entry_offset[mid] <= i) lo = mid;
@@ -356,18 +374,18 @@ __device__ __forceinline__ void compact_block(
         const int32_t row = entry_start[lo] + (i - entry_offset[lo]);
         const int64_t logical = (row_base + row) * kLanes
             + (entry_lane[lo] ^ static_cast<int32_t>((row_base + row) & 254));
-        int32_t e = -127;
+        int32_t x = -127;
         if (logical < logical_numel) {
             if (precomputed) {
-                e = static_cast<int32_t>(static_cast<const uint8_t *>(source)[logical]) - 127;
+                x = static_cast<int32_t>(static_cast<const uint8_t *>(source)[logical]) - 127;
             } else {
                 const int32_t bits = static_cast<const uint16_t *>(source)[logical];
-                e = ((bits >> 7) & 255) - 127;
+                x = ((bits >> 7) & 255) - 127;
             }
         }
-        out[i] = static_cast<uint8_t>(e);
+        out[i] = static_cast<uint8_t>(x);
     }
-    __syncthreads();   // entry arrays are reused by the next listed block
+    __syncthreads();   // the entry arrays are reused by the next block
 }
 
 __global__ __launch_bounds__(kLanes) void compact_extra_kernel(
@@ -395,10 +413,11 @@ __global__ __launch_bounds__(kLanes) void compact_extra_kernel(
     for (int64_t i = blockIdx.x; i < listed; i += gridDim.x) {
         const int64_t block = list != nullptr ? list[i] : i;
         if (list == nullptr && blocks[block] == 0) continue;   // uniform
-        compact_block(source, lanes, starts, tail, lane_off, start_off, tail_off,
-                      blocks[block], blocks[n_blocks + block], blocks[2 * n_blocks + block],
-                      extra_starts, block, logical_numel, S, precomputed, scratch,
-                      entry_offset, entry_start, entry_lane);
+        const BlockEntries e = rank_block(extra_starts, block, S, scratch, entry_offset,
+                                          entry_start, entry_lane);
+        write_block(source, lanes, starts, tail, lane_off, start_off, tail_off,
+                    blocks[n_blocks + block], blocks[2 * n_blocks + block], e, block,
+                    logical_numel, S, precomputed, entry_offset, entry_start, entry_lane);
     }
 }
 
@@ -407,10 +426,13 @@ __global__ __launch_bounds__(kLanes) void compact_extra_kernel(
 // own wait for the arena lock is bounded well below that, and it publishes
 // in every case).  A workgroup that gives up writes nothing.
 constexpr int kReadySpinLimit = 1 << 22;
-// Compacting workgroups of one launch: 511 measured best on gfx950 at 4096
-// blocks (694 with overflow) and at 1024 blocks (all with overflow), against
-// 255, 1023 and 2047.
-constexpr int64_t kAllocateCompactWaiters = 511;
+// Compacting workgroups of one launch (each owns every 2047th block): 2047
+// measured best on gfx950 at 4096 blocks (694 with overflow: 12.6 us with a
+// pending free) and at 1024 blocks (all with overflow: 11.9 us), against 511
+// (16.3, 14.7 us), 1023 and 4095.  Workgroups that do not fit on the device
+// at once start as others leave; those whose blocks have no overflow leave
+// at once.
+constexpr int64_t kAllocateCompactWaiters = 2047;
 
 // A value workgroup 0 wrote in this launch: an agent-scope load, which reads
 // the coherent copy (workgroup 0 released its writes before the ready word).
@@ -421,11 +443,13 @@ __device__ __forceinline__ int32_t published(const int32_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Scan + reservation (workgroup 0, deferred frees first) and compaction of
-// the listed blocks (workgroups 1..G-1) in one launch.  Workgroup 0 publishes
-// its writes with an agent-scope release and then stores `epoch` to *ready;
-// the others poll *ready, read what workgroup 0 wrote with agent-scope loads
-// and walk the overflow-block list with stride G - 1.  Workgroup 0 is
+// Scan + reservation (workgroup 0, deferred frees first) and compaction
+// (workgroups 1..G-1) in one launch.  Workgroup 0 publishes its writes with an
+// agent-scope release and then stores `epoch` to *ready.  Compacting
+// workgroup w owns blocks w - 1 + k (G - 1): it ranks its first overflowing
+// block's lanes before waiting, then polls *ready, reads the offsets workgroup
+// 0 wrote with agent-scope loads and writes its blocks' entries and tails; a
+// workgroup whose blocks have no overflow exits at once.  Workgroup 0 is
 // dispatched first and waits for nothing but the arena lock, so every wait
 // ends.
 __global__ __launch_bounds__(kLanes) void allocate_compact_kernel(
@@ -448,7 +472,38 @@ __global__ __launch_bounds__(kLanes) void allocate_compact_kernel(
     __shared__ int32_t go;
     __shared__ int32_t scratch[kWavesPerBlock];
     __shared__ int32_t entry_offset[kLanes], entry_start[kLanes], entry_lane[kLanes];
-    if (threadIdx.x == 0) {
+    __shared__ uint64_t mine[kWavesPerBlock];
+    // This workgroup's blocks are blockIdx.x - 1 + k * stride; the encoder's
+    // per-block counts (summaries[0, nb), written before this launch) say which
+    // of them overflow, one load per thread (at most 33 blocks per workgroup:
+    // n_blocks <= 65535 and stride = min(n_blocks, 2047)).
+    const int64_t nb = n_blocks;
+    const int64_t stride = gridDim.x - 1;
+    const int64_t own = blockIdx.x - 1;
+    const int64_t k_count = (nb - own + stride - 1) / stride;
+    const int t = threadIdx.x;
+    const bool has = t < k_count && summaries[own + t * stride] > 0;
+    const uint64_t has_mask = __ballot(has);
+    if ((t & (kWave - 1)) == 0) mine[t / kWave] = has_mask;
+    __syncthreads();
+    int wave = 0;
+    uint64_t pending = mine[0];
+    auto next_block = [&]() -> int64_t {   // uniform; -1 when none is left
+        while (pending == 0) {
+            if (++wave == kWavesPerBlock) return -1;
+            pending = mine[wave];
+        }
+        const int k = __builtin_ctzll(pending);
+        pending &= pending - 1;
+        return own + static_cast<int64_t>(wave * kWave + k) * stride;
+    };
+    int64_t block = next_block();
+    if (block < 0) return;   // no overflow here: nothing to wait for
+    // Ranking needs nothing from workgroup 0, so the first block's is done
+    // while workgroup 0 works.
+    BlockEntries e = rank_block(extra_starts, block, S, scratch, entry_offset, entry_start,
+                                entry_lane);
+    if (t == 0) {
         int32_t seen = 0;
         for (int i = 0; i < kReadySpinLimit; ++i) {
             if (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch) {
@@ -461,21 +516,18 @@ __global__ __launch_bounds__(kLanes) void allocate_compact_kernel(
     }
     __syncthreads();
     if (go == 0) return;
-    const int64_t nb = n_blocks;
-    const int64_t listed = published(summaries + 5 * nb);
-    if (static_cast<int64_t>(blockIdx.x) - 1 >= listed) return;   // nothing for this workgroup
     if (published(descriptor + 2) != kStatusOk) return;   // failed reservation: write nothing
     const int64_t total = published(counts);
     const int64_t lane_off = published(descriptor);
     const int64_t start_off = lane_off + total;
     const int64_t tail_off = lane_off + 2 * total;
-    const int32_t *list = summaries + 4 * nb;
-    for (int64_t i = blockIdx.x - 1; i < listed; i += gridDim.x - 1) {
-        const int64_t block = published(list + i);
-        compact_block(source, arena, arena, arena, lane_off, start_off, tail_off,
-                      published(blocks + block), published(blocks + nb + block),
-                      published(blocks + 2 * nb + block), extra_starts, block, logical_numel,
-                      S, precomputed, scratch, entry_offset, entry_start, entry_lane);
+    for (;;) {
+        write_block(source, arena, arena, arena, lane_off, start_off, tail_off,
+                    published(blocks + nb + block), published(blocks + 2 * nb + block), e, block,
+                    logical_numel, S, precomputed, entry_offset, entry_start, entry_lane);
+        block = next_block();
+        if (block < 0) break;
+        e = rank_block(extra_starts, block, S, scratch, entry_offset, entry_start, entry_lane);
     }
 }
 
@@ -646,8 +698,7 @@ extern "C" int32_t lct_allocate_compact(const void *source, int32_t *summaries,
             if (frees->descriptor[i] == nullptr) return LCT_E_NULL;
         pending = *frees;
     }
-    // Workgroup 0 plus up to kAllocateCompactWaiters compacting workgroups
-    // (every one fits on the device at once next to workgroup 0).
+    // Workgroup 0 plus up to kAllocateCompactWaiters compacting workgroups.
     const uint32_t grid = 1u + static_cast<uint32_t>(
         n_blocks < kAllocateCompactWaiters ? n_blocks : kAllocateCompactWaiters);
     const size_t lds = static_cast<size_t>(max_free_regions) * 8;
