@@ -295,3 +295,63 @@ def test_one_launch_free_list_full():
         assert torch.equal(a, b)
     assert _free_regions_snapshot(buf_a) == _free_regions_snapshot(buf_b)
     assert torch.equal(buf_a.data, buf_b.data)
+
+
+def test_two_streams_share_one_buffer():
+    """Compress + free on two streams at once into one TensorBuffer: the
+    versioned lock serialises the reservations (a snapshot taken while the
+    other stream holds or changes the list is read again), so the free list
+    stays valid, every tensor decodes to its input and all space comes back."""
+    require_gpu()
+    print("case two streams, one buffer", flush=True)
+    inputs = [(x.cuda(), d) for x, d in _inputs()]
+    buffer = TensorBuffer(16 << 20, max_free_regions=64, device="cuda")
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    kept = [[], []]
+    for round_ in range(12):
+        for k, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                x, dist = inputs[(round_ + k) % len(inputs)]
+                ct = compress(x, dist, buffer=buffer)
+                if round_ % 3 == 2:
+                    ct.free()
+                else:
+                    kept[k].append((ct, x))
+    for s in streams:
+        torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    verify_buffer(buffer)
+    for k in range(2):
+        for ct, x in kept[k]:
+            assert int(ct.fallback_descriptor[2].item()) == 0
+            assert torch.equal(decompress(ct).view(torch.int16).reshape(-1),
+                               x.view(torch.int16).reshape(-1))
+    for k in range(2):
+        for ct, _ in kept[k]:
+            ct.free()
+    torch.cuda.synchronize()
+    assert _free_regions_snapshot(buffer) == [(0, 16 << 20)]
+
+
+def test_deferred_frees_with_the_largest_free_list():
+    """4096 free regions: the LDS copy of the list is 32 KiB and every thread
+    holds 16 entries in the shifts; many small holes are freed and refilled."""
+    require_gpu()
+    print("case 4096-region buffer", flush=True)
+    x, dist = _patterns(51, 65536), SPARSE
+    x = x.cuda()
+    bufs = [TensorBuffer(4 << 20, max_free_regions=4096, device="cuda") for _ in range(2)]
+    cts = [[compress(x, dist, buffer=b) for _ in range(40)] for b in bufs]
+    for i in range(0, 40, 2):   # every other tensor: twenty holes
+        bufs[0].free(Allocation(cts[0][i].fallback_descriptor, bufs[0]))
+        cts[1][i].free()
+    again = [[compress(x, dist, buffer=b) for _ in range(10)] for b in bufs]
+    for a, b in zip(again[0], again[1]):
+        _assert_same_allocation(a, b)
+    torch.cuda.synchronize()
+    assert _free_regions_snapshot(bufs[0]) == _free_regions_snapshot(bufs[1])
+    assert len(_free_regions_snapshot(bufs[1])) > 5
+    verify_buffer(bufs[1])
+    assert torch.equal(decompress(again[1][-1]).view(torch.int16), x.view(torch.int16))
