@@ -273,8 +273,19 @@ struct LdsReserve {
         for (int j = 0; j < LCT_MAX_PENDING_FREES; ++j) {
             if (j < frees.count) {
                 const int32_t d[4] = {pending[j][0], pending[j][1], pending[j][2], pending[j][3]};
-                if (lds_free(f, d, scratch) == kStatusOk && t == 0)
-                    frees.descriptor[j][2] = kStatusFreed;
+                if (lds_free(f, d, scratch) == kStatusOk) {
+                    if (t == 0) {
+                        frees.descriptor[j][2] = kStatusFreed;
+                        // A later copy of the same descriptor now reads as
+                        // freed, so a second free of it is rejected, as the
+                        // immediate free would reject it (status 4).
+#pragma unroll
+                        for (int k = j + 1; k < LCT_MAX_PENDING_FREES; ++k)
+                            if (k < frees.count && frees.descriptor[k] == frees.descriptor[j])
+                                pending[k][2] = kStatusFreed;
+                    }
+                    __syncthreads();
+                }
             }
         }
     }

@@ -103,7 +103,7 @@ CASES = [
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-@pytest.mark.parametrize("frees", ["one", "double-free", "none"])
+@pytest.mark.parametrize("frees", ["one", "double-free", "same-twice", "none"])
 def test_one_launch_equals_free_scan_compact(case, frees):
     require_gpu()
     name, dist, make, capacity = case
@@ -112,7 +112,7 @@ def test_one_launch_equals_free_scan_compact(case, frees):
     src, extra, summaries, (B, L, S, W), nb, size, n = _encode(x, dist)
     buf_a, alloc_a = _fragmented(capacity)
     buf_b, alloc_b = _fragmented(capacity)
-    pending = {"one": [2], "double-free": [2, 1], "none": []}[frees]
+    pending = {"one": [2], "double-free": [2, 1], "same-twice": [2, 2], "none": []}[frees]
 
     # Reference-shaped sequence: immediate frees, scan + reservation, compaction.
     statuses = [buf_a.free(alloc_a[i]) for i in pending]
@@ -140,7 +140,7 @@ def test_one_launch_equals_free_scan_compact(case, frees):
                               precomputed=False)
     torch.cuda.synchronize()
 
-    if frees == "double-free":
+    if frees in ("double-free", "same-twice"):
         assert [int(s.item()) for s in statuses] == [0, 4]
     assert torch.equal(counts_a, counts_b)
     assert torch.equal(desc_a, desc_b)
@@ -355,3 +355,26 @@ def test_deferred_frees_with_the_largest_free_list():
     assert len(_free_regions_snapshot(bufs[1])) > 5
     verify_buffer(bufs[1])
     assert torch.equal(decompress(again[1][-1]).view(torch.int16), x.view(torch.int16))
+
+
+def test_freeing_one_tensor_twice_changes_nothing_the_second_time():
+    """CompressedTensor.free() twice: both frees ride on one reservation; the
+    second is rejected as the immediate second free is (status 4)."""
+    require_gpu()
+    print("case double CompressedTensor.free()", flush=True)
+    x, dist = _patterns(61, 65536), SPARSE
+    x = x.cuda()
+    buf_a = TensorBuffer(1 << 20, device="cuda")
+    buf_b = TensorBuffer(1 << 20, device="cuda")
+    cts = [(compress(x, dist, buffer=buf_a), compress(x, dist, buffer=buf_b)) for _ in range(3)]
+    first = buf_a.free(Allocation(cts[1][0].fallback_descriptor, buf_a))
+    second = buf_a.free(Allocation(cts[1][0].fallback_descriptor, buf_a))
+    cts[1][1].free()
+    cts[1][1].free()
+    ct_a, ct_b = compress(x, dist, buffer=buf_a), compress(x, dist, buffer=buf_b)
+    torch.cuda.synchronize()
+    assert (int(first.item()), int(second.item())) == (0, 4)
+    _assert_same_allocation(ct_a, ct_b)
+    assert torch.equal(cts[1][0].fallback_descriptor, cts[1][1].fallback_descriptor)
+    assert _free_regions_snapshot(buf_a) == _free_regions_snapshot(buf_b)
+    verify_buffer(buf_b)
