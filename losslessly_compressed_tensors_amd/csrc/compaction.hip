@@ -340,12 +340,43 @@ struct BlockEntries {
     int32_t rank;    // this lane's entry index in the block, if it overflows
     int32_t count;   // entries of the block (uniform)
     int32_t bytes;   // tail bytes of the block (uniform)
+    int32_t first_tail;   // tail byte threadIdx.x of the block (if < bytes)
 };
 
+// Tail byte i of `block`: int8(e - 127) of the exponent at its logical
+// position (-127 past the tensor's end), from the entries in LDS.
+__device__ __forceinline__ int32_t tail_byte(const void *__restrict__ source, int32_t i,
+                                             int32_t count, int64_t block, int64_t logical_numel,
+                                             int S, int precomputed,
+                                             const int32_t *entry_offset,
+                                             const int32_t *entry_start,
+                                             const int32_t *entry_lane) {
+    // Last entry whose offset is <= i.
+    int32_t lo = 0, hi = count - 1;
+    while (lo < hi) {
+        const int32_t mid = (lo + hi + 1) >> 1;
+        if (entry_offset[mid] <= i) lo = mid;
+        else hi = mid - 1;
+    }
+    const int64_t row_base = block * S;
+    const int32_t row = entry_start[lo] + (i - entry_offset[lo]);
+    const int64_t logical = (row_base + row) * kLanes
+        + (entry_lane[lo] ^ static_cast<int32_t>((row_base + row) & 254));
+    if (logical >= logical_numel) return -127;
+    if (precomputed) return static_cast<int32_t>(static_cast<const uint8_t *>(source)[logical]) - 127;
+    const int32_t bits = static_cast<const uint16_t *>(source)[logical];
+    return ((bits >> 7) & 255) - 127;
+}
+
+// With `source` given, the block's first 256 tail bytes are also read here
+// (they depend on the ranking only), one per thread.
 __device__ __forceinline__ BlockEntries rank_block(const uint8_t *__restrict__ extra_starts,
                                                    int64_t block, int S, int32_t *scratch,
                                                    int32_t *entry_offset, int32_t *entry_start,
-                                                   int32_t *entry_lane) {
+                                                   int32_t *entry_lane,
+                                                   const void *__restrict__ source = nullptr,
+                                                   int64_t logical_numel = 0,
+                                                   int precomputed = 0) {
     const int t = threadIdx.x;
     BlockEntries e;
     e.start = extra_starts[block * kLanes + t];
@@ -358,6 +389,10 @@ __device__ __forceinline__ BlockEntries rank_block(const uint8_t *__restrict__ e
         entry_lane[e.rank] = t;
     }
     __syncthreads();
+    e.first_tail = source != nullptr && t < e.bytes
+                       ? tail_byte(source, t, e.count, block, logical_numel, S, precomputed,
+                                   entry_offset, entry_start, entry_lane)
+                       : 0;
     return e;
 }
 
@@ -366,34 +401,19 @@ __device__ __forceinline__ void write_block(
     uint8_t *__restrict__ tail, int64_t lane_off, int64_t start_off, int64_t tail_off,
     int32_t first, int32_t byte_base, const BlockEntries &e, int64_t block,
     int64_t logical_numel, int S, int precomputed, const int32_t *entry_offset,
-    const int32_t *entry_start, const int32_t *entry_lane) {
+    const int32_t *entry_start, const int32_t *entry_lane, bool prefetched = false) {
     const int t = threadIdx.x;
     if (e.start != 255) {
         lanes[lane_off + first + e.rank] = static_cast<uint8_t>(t);
         starts[start_off + first + e.rank] = static_cast<uint8_t>(e.start);
     }
     uint8_t *out = tail + tail_off + byte_base;
-    const int64_t row_base = block * S;
+    // Byte t may have been read by rank_block already (prefetched).
     for (int32_t i = t; i < e.bytes; i += kLanes) {
-        // Last entry whose offset is <= i.
-        int32_t lo = 0, hi = e.count - 1;
-        while (lo < hi) {
-            const int32_t mid = (lo + hi + 1) >> 1;
-            if (entry_offset[mid] <= i) lo = mid;
-            else hi = mid - 1;
-        }
-        const int32_t row = entry_start[lo] + (i - entry_offset[lo]);
-        const int64_t logical = (row_base + row) * kLanes
-            + (entry_lane[lo] ^ static_cast<int32_t>((row_base + row) & 254));
-        int32_t x = -127;
-        if (logical < logical_numel) {
-            if (precomputed) {
-                x = static_cast<int32_t>(static_cast<const uint8_t *>(source)[logical]) - 127;
-            } else {
-                const int32_t bits = static_cast<const uint16_t *>(source)[logical];
-                x = ((bits >> 7) & 255) - 127;
-            }
-        }
+        const int32_t x = prefetched && i == t
+                              ? e.first_tail
+                              : tail_byte(source, i, e.count, block, logical_numel, S,
+                                          precomputed, entry_offset, entry_start, entry_lane);
         out[i] = static_cast<uint8_t>(x);
     }
     __syncthreads();   // the entry arrays are reused by the next block
@@ -513,7 +533,7 @@ __global__ __launch_bounds__(kLanes) void allocate_compact_kernel(
     // Ranking needs nothing from workgroup 0, so the first block's is done
     // while workgroup 0 works.
     BlockEntries e = rank_block(extra_starts, block, S, scratch, entry_offset, entry_start,
-                                entry_lane);
+                                entry_lane, source, logical_numel, precomputed);
     if (t == 0) {
         int32_t seen = 0;
         for (int i = 0; i < kReadySpinLimit; ++i) {
@@ -527,18 +547,27 @@ __global__ __launch_bounds__(kLanes) void allocate_compact_kernel(
     }
     __syncthreads();
     if (go == 0) return;
-    if (published(descriptor + 2) != kStatusOk) return;   // failed reservation: write nothing
+    // All of the reservation's values at once (reading them is harmless when
+    // it failed), then the status.
+    const int32_t status = published(descriptor + 2);
     const int64_t total = published(counts);
     const int64_t lane_off = published(descriptor);
+    int32_t first = published(blocks + nb + block);
+    int32_t byte_base = published(blocks + 2 * nb + block);
+    if (status != kStatusOk) return;   // failed reservation: write nothing
     const int64_t start_off = lane_off + total;
     const int64_t tail_off = lane_off + 2 * total;
+    bool prefetched = true;
     for (;;) {
-        write_block(source, arena, arena, arena, lane_off, start_off, tail_off,
-                    published(blocks + nb + block), published(blocks + 2 * nb + block), e, block,
-                    logical_numel, S, precomputed, entry_offset, entry_start, entry_lane);
+        write_block(source, arena, arena, arena, lane_off, start_off, tail_off, first,
+                    byte_base, e, block, logical_numel, S, precomputed, entry_offset,
+                    entry_start, entry_lane, prefetched);
         block = next_block();
         if (block < 0) break;
         e = rank_block(extra_starts, block, S, scratch, entry_offset, entry_start, entry_lane);
+        first = published(blocks + nb + block);
+        byte_base = published(blocks + 2 * nb + block);
+        prefetched = false;
     }
 }
 
