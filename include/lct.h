@@ -180,10 +180,14 @@ int32_t lct_prefix_allocate(int32_t *summaries, int32_t *counts,
  * as lct_compact_extra with buffered = 1 (lanes, starts and tails in `arena`).
  * summaries: int32[5*nb + 1] as for lct_prefix_allocate, except that the
  * exclusive scans [2*nb, 4*nb) are not written (blocks holds them).  ready: a device
- * uint64 whose value before the launch differs from `epoch` (use a value no
- * earlier call used).  The result (counts, descriptor, blocks, arena bytes)
- * equals lct_buffer_free on each pending descriptor followed by
- * lct_prefix_allocate and lct_compact_extra. */
+ * uint64 whose value before the launch differs from `epoch` and from ~epoch
+ * (use a value no earlier call used).  The result (counts, descriptor, blocks,
+ * arena bytes) equals lct_buffer_free on each pending descriptor followed by
+ * lct_prefix_allocate and lct_compact_extra.  A compacting workgroup whose
+ * bounded wait ends first writes nothing and leaves ~epoch in *ready; the
+ * reservation then gets status 7 (LCT_STATUS_INCOMPLETE).  A failed reservation
+ * of a non-empty request (status 1, 6 or 7) also sets a bit of the buffer's
+ * failure word (LCT_FAIL_*). */
 int32_t lct_allocate_compact(const void *source, int32_t *summaries, int32_t *counts,
                              int32_t *descriptor, int32_t *buffer_meta,
                              int32_t max_free_regions, uint8_t *arena, int32_t *blocks,
@@ -425,12 +429,22 @@ int32_t lct_dual_encode(const int32_t *a_encoded, const uint8_t *a_side,
 /* ---- TensorBuffer allocator kernels: replace LCT/tensor_buffer.py:130-136
  * (_reset_kernel launch), :93-120 (_allocate_kernel launches) and
  * LCT/kernels/tensor_buffer_ops.py:5-15 (_free_storage_kernel launch).
- * meta: the int32 metadata block at the start of the buffer's storage.
+ * meta: the int32 metadata block at the start of the buffer's storage,
+ * free_starts[R] | free_sizes[R] | count | lock | generation | failures (the
+ * failure word sits in the padding the reference leaves after generation).
  * requested/item_count: device int32[1]; item_count may be NULL when
  * item_bytes == 0.  descriptor: int32[4] {offset, size, status, generation};
- * status 0 ok, 1 no fit, 2 empty request, 5 freed, 6 lock not acquired.
+ * status 0 ok, 1 no fit, 2 empty request, 5 freed, 6 lock not acquired,
+ * 7 reserved but the compaction into it did not complete (freeable).
  * free writes status_out[0]: 0 ok, 3 free list full, 4 invalid descriptor,
- * 6 lock not acquired. */
+ * 6 lock not acquired.  reset also clears the failure word. */
+#define LCT_STATUS_INCOMPLETE 7
+/* Bits of the failure word: a codec reservation (lct_prefix_allocate buffered,
+ * lct_allocate_compact) of a non-empty request found no fit, could not take
+ * the lock, or its compaction did not complete.  Sticky until reset. */
+#define LCT_FAIL_NO_FIT 1
+#define LCT_FAIL_LOCK 2
+#define LCT_FAIL_INCOMPLETE 4
 int32_t lct_buffer_reset(int32_t *meta, int32_t max_free_regions,
                          int32_t capacity_bytes, hipStream_t stream);
 int32_t lct_buffer_allocate(int32_t *meta, int32_t max_free_regions,
@@ -440,6 +454,14 @@ int32_t lct_buffer_allocate(int32_t *meta, int32_t max_free_regions,
 int32_t lct_buffer_free(int32_t *meta, int32_t max_free_regions,
                         int32_t *descriptor, int32_t *status_out,
                         hipStream_t stream);
+
+/* ---- bounds of the device-side waits, in polls: the arena lock (every
+ * allocator entry point, default 2^20) and lct_allocate_compact's wait for its
+ * reservation (default 2^22); 0 restores a default.  Applies to launches made
+ * after the call.  No counterpart in the reference (its lock wait is
+ * unbounded, LCT/kernels/tensor_buffer.py:7-15): tests lower the bounds to
+ * drive the give-up paths from the host without long waits. */
+int32_t lct_set_wait_limits(int32_t lock_polls, int32_t ready_polls);
 
 #ifdef __cplusplus
 }

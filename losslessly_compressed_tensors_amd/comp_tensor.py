@@ -64,6 +64,19 @@ class CompressedTensor:
             return 65536, 256, 256, 24
         return geometry(self.distribution)
 
+    def _reserved_bytes(self) -> int:
+        """Arena bytes of this tensor's reservation (syncs).  Raises
+        ``BufferReservationError`` when the tensor has overflow entries whose
+        reservation failed (no fit, lock not taken, or a compaction that did
+        not complete): its overflow tails were never stored, so it cannot be
+        decoded."""
+        from .tensor_buffer import check_reservation
+
+        size, status, count = (int(v) for v in torch.cat(
+            (self.fallback_descriptor[1:3], self.fallback_count[:1])).tolist())
+        check_reservation(status, count)
+        return size
+
     def memory_size(self) -> int:
         """Device bytes owned by this tensor (syncs when buffer-backed)."""
         allocations: dict[tuple[torch.device, int], int] = {}
@@ -79,14 +92,14 @@ class CompressedTensor:
             allocations[(value.device, storage.data_ptr())] = storage.nbytes()
         total = sum(allocations.values())
         if self.fallback_descriptor is not None:
-            total += int(self.fallback_descriptor[1].item())
+            total += self._reserved_bytes()
         return total
 
     def memory_buffer_size(self) -> int:
         """Arena bytes reserved by this tensor (syncs)."""
         if self.fallback_descriptor is None:
             return 0
-        return int(self.fallback_descriptor[1].item())
+        return self._reserved_bytes()
 
     def free(self) -> None:
         """Release this tensor's arena reservation, if buffer-backed

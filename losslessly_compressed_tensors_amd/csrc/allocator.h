@@ -29,7 +29,33 @@ constexpr int32_t kStatusFreeListFull = 3;
 constexpr int32_t kStatusInvalid = 4;
 constexpr int32_t kStatusFreed = 5;
 constexpr int32_t kStatusLock = 6;
+// A codec reservation that succeeded but whose compaction did not complete
+// (a compacting workgroup stopped waiting for the reservation and wrote none
+// of its blocks' entries or tails).  The region is held like a status-0 one
+// and is freed the same way; decoding treats the tensor as failed.
+constexpr int32_t kStatusIncomplete = 7;
+// Bounded waits: polls of the arena lock, and of lct_allocate_compact's ready
+// word.  The host passes the limits to every kernel that waits
+// (lct_set_wait_limits lowers them for tests of the give-up paths).
 constexpr int kLockSpinLimit = 1 << 20;
+constexpr int kReadyPollLimit = 1 << 22;
+
+// The limits in force (host side; tensor_buffer.hip).
+int32_t lock_spins();
+int32_t ready_polls();
+
+// Bits of the buffer's failure word (int32 at metadata index 2R + 3, in the
+// padding after the generation): set, and kept until the next reset, when a
+// compressed tensor's overflow reservation fails (no fit, lock not taken) or
+// its compaction does not complete.  The host reads it at its sync points.
+constexpr int32_t kFailNoFit = 1;
+constexpr int32_t kFailLock = 2;
+constexpr int32_t kFailIncomplete = 4;
+
+// Whether a descriptor holds a live region (freeable).
+__device__ __forceinline__ bool holds_region(int32_t status) {
+    return status == kStatusOk || status == kStatusIncomplete;
+}
 
 struct AllocatorMeta {
     int32_t *starts;
@@ -37,12 +63,26 @@ struct AllocatorMeta {
     int32_t *count;
     int32_t *lock;
     int32_t *generation;
+    int32_t *failures;
     int32_t regions;
+    int32_t spins;   // bound of the lock wait, in polls
 
-    __device__ explicit AllocatorMeta(int32_t *meta, int32_t r)
+    __device__ explicit AllocatorMeta(int32_t *meta, int32_t r, int32_t lock_spins)
         : starts(meta), sizes(meta + r), count(meta + 2 * r), lock(meta + 2 * r + 1),
-          generation(meta + 2 * r + 2), regions(r) {}
+          generation(meta + 2 * r + 2), failures(meta + 2 * r + 3), regions(r),
+          spins(lock_spins) {}
 };
+
+// Records a codec reservation's failure (status 1 or 6 for a non-empty
+// request, or an incomplete compaction) in the buffer's failure word.
+__device__ __forceinline__ void record_failure(const AllocatorMeta &m, int32_t bits) {
+    __hip_atomic_fetch_or(m.failures, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ int32_t failure_bits(int32_t status, int32_t request) {
+    if (request <= 0) return 0;
+    return status == kStatusNoFit ? kFailNoFit : status == kStatusLock ? kFailLock : 0;
+}
 
 // A value another workgroup wrote (or may be writing) in this launch: an
 // agent-scope load reads the coherent copy, where a plain load could hit a
@@ -53,9 +93,10 @@ __device__ __forceinline__ int32_t coherent_load(const int32_t *p) {
 
 // Thread 0's bounded wait for the lock; returns the version taken (even), or
 // -1.  `seen` is a value of the lock word already read, or -1.
-__device__ __forceinline__ int32_t take_lock_thread0(int32_t *lock, int32_t seen) {
+__device__ __forceinline__ int32_t take_lock_thread0(int32_t *lock, int32_t seen,
+                                                     int32_t spins) {
     int32_t v = seen;
-    for (int i = 0; i < kLockSpinLimit; ++i) {
+    for (int i = 0; i < spins; ++i) {
         if (v >= 0 && (v & 1) == 0) {
             int32_t expected = v;
             if (__hip_atomic_compare_exchange_strong(lock, &expected, v + 1, __ATOMIC_ACQUIRE,
@@ -72,8 +113,8 @@ __device__ __forceinline__ int32_t take_lock_thread0(int32_t *lock, int32_t seen
 
 // Returns the version taken (>= 0) in every thread, or -1 if the lock was not
 // taken.  flag: one LDS int.  Contains barriers.
-__device__ __forceinline__ int32_t allocator_lock(int32_t *lock, int32_t *flag) {
-    if (threadIdx.x == 0) *flag = take_lock_thread0(lock, coherent_load(lock));
+__device__ __forceinline__ int32_t allocator_lock(int32_t *lock, int32_t *flag, int32_t spins) {
+    if (threadIdx.x == 0) *flag = take_lock_thread0(lock, coherent_load(lock), spins);
     __syncthreads();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     return *flag;
@@ -161,7 +202,7 @@ struct AllocatorSnapshot {
 
 __device__ __forceinline__ void allocator_begin(const AllocatorMeta &m, AllocatorSnapshot &snap,
                                                 int32_t *flag) {
-    snap.held = allocator_lock(m.lock, flag);
+    snap.held = allocator_lock(m.lock, flag, m.spins);
     snap.locked = snap.held >= 0;
     snap.generation = 0;
     snap.count = 0;
@@ -171,10 +212,12 @@ __device__ __forceinline__ void allocator_begin(const AllocatorMeta &m, Allocato
     load_regions(m, snap.r);
 }
 
-// tensor_buffer.py:37-91.  `request` already includes item bytes.
+// tensor_buffer.py:37-91.  `request` already includes item bytes.  A codec
+// reservation (`codec`) records its failure in the buffer's failure word.
 __device__ __forceinline__ void allocator_finish(const AllocatorMeta &m,
                                                  const AllocatorSnapshot &snap, int32_t request,
-                                                 int32_t *descriptor, int32_t *scratch) {
+                                                 int32_t *descriptor, int32_t *scratch,
+                                                 bool codec = false) {
     __shared__ int32_t shared2[2];
     if (!snap.locked) {
         if (threadIdx.x == 0) {
@@ -182,6 +225,7 @@ __device__ __forceinline__ void allocator_finish(const AllocatorMeta &m,
             descriptor[1] = 0;
             descriptor[2] = kStatusLock;
             descriptor[3] = -1;
+            if (codec && request > 0) record_failure(m, kFailLock);
         }
         return;
     }
@@ -210,6 +254,7 @@ __device__ __forceinline__ void allocator_finish(const AllocatorMeta &m,
         descriptor[1] = success ? size : 0;
         descriptor[2] = request <= 0 ? kStatusEmpty : (success ? kStatusOk : kStatusNoFit);
         descriptor[3] = snap.generation;
+        if (codec && request > 0 && !success) record_failure(m, kFailNoFit);
     }
     allocator_unlock(m.lock, snap.held);
 }
@@ -236,7 +281,7 @@ __device__ __forceinline__ int32_t allocator_free_locked(const AllocatorMeta &m,
     const int32_t current_generation = *m.generation;
     RegionRegs r;
     load_regions(m, r);
-    const bool valid = status == kStatusOk && generation == current_generation && offset >= 0
+    const bool valid = holds_region(status) && generation == current_generation && offset >= 0
         && size > 0;
     int32_t result = kStatusInvalid;
     if (valid) {
@@ -288,7 +333,7 @@ __device__ __forceinline__ int32_t allocator_free_locked(const AllocatorMeta &m,
 // tensor_buffer.py:94-179.  Returns the status in every thread.
 __device__ __forceinline__ int32_t allocator_free(const AllocatorMeta &m, int32_t *descriptor,
                                                   int32_t *scratch, int32_t *flag) {
-    const int32_t held = allocator_lock(m.lock, flag);
+    const int32_t held = allocator_lock(m.lock, flag, m.spins);
     if (held < 0) return kStatusLock;
     const int32_t result = allocator_free_locked(m, descriptor, scratch);
     allocator_unlock(m.lock, held);
@@ -337,7 +382,7 @@ __device__ __forceinline__ void lds_shift(LdsFreeList &f, int32_t from, int32_t 
 __device__ __forceinline__ int32_t lds_free(LdsFreeList &f, const int32_t (&d)[4],
                                             int32_t *scratch) {
     const int32_t offset = d[0], size = d[1];
-    if (!(d[2] == kStatusOk && d[3] == f.generation && offset >= 0 && size > 0))
+    if (!(holds_region(d[2]) && d[3] == f.generation && offset >= 0 && size > 0))
         return kStatusInvalid;
     const int32_t count = f.count;
     int32_t below = 0;

@@ -200,7 +200,7 @@ struct RegisterReserve {
         if (active) allocator_begin(meta, snap, flag);
     }
     __device__ void finish(int32_t request, int32_t *scratch) {
-        if (active) allocator_finish(meta, snap, request, descriptor, scratch);
+        if (active) allocator_finish(meta, snap, request, descriptor, scratch, true);
     }
 };
 
@@ -261,7 +261,7 @@ struct LdsReserve {
         __syncthreads();
         held = shared[1];
         if (held < 0) {
-            if (t == 0) shared[1] = take_lock_thread0(meta.lock, -1);
+            if (t == 0) shared[1] = take_lock_thread0(meta.lock, -1, meta.spins);
             __syncthreads();
             held = shared[1];
             if (held >= 0) read_list(shared);
@@ -290,9 +290,12 @@ struct LdsReserve {
         }
     }
 
+    int32_t status;   // the reservation's status (uniform after finish)
+
     __device__ void finish(int32_t request, int32_t *scratch) {
         const int t = threadIdx.x;
         if (held < 0) {
+            status = kStatusLock;
             if (t == 0) {
                 descriptor[0] = -1;
                 descriptor[1] = 0;
@@ -303,6 +306,7 @@ struct LdsReserve {
             int32_t out[3];
             lds_reserve(f, request, scratch, out);
             lds_write_back(f, meta);
+            status = out[2];
             if (t == 0) {
                 descriptor[0] = out[0];
                 descriptor[1] = out[1];
@@ -310,6 +314,8 @@ struct LdsReserve {
                 descriptor[3] = f.generation;
             }
         }
+        if (t == 0 && failure_bits(status, request) != 0)
+            record_failure(meta, failure_bits(status, request));
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         __syncthreads();
         if (held >= 0 && t == 0)
@@ -321,10 +327,10 @@ __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     int32_t *__restrict__ summaries, int32_t *__restrict__ counts,
     int32_t *__restrict__ descriptor, int32_t *__restrict__ buffer_meta,
     int32_t *__restrict__ blocks, int32_t n_blocks, int32_t buffered,
-    int32_t max_free_regions) {
+    int32_t max_free_regions, int32_t lock_spins) {
     __shared__ int32_t flag;
-    RegisterReserve reserve{AllocatorMeta(buffer_meta, max_free_regions), descriptor, &flag,
-                            buffered != 0, {}};
+    RegisterReserve reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins), descriptor,
+                            &flag, buffered != 0, {}};
     scan_allocate<true>(summaries, counts, blocks, n_blocks, reserve);
 }
 
@@ -453,10 +459,13 @@ __global__ __launch_bounds__(kLanes) void compact_extra_kernel(
 }
 
 // Waits of the compacting workgroups for workgroup 0's reservation: polls of
-// the ready word with a sleep between them, about 4 s at most (workgroup 0's
-// own wait for the arena lock is bounded well below that, and it publishes
-// in every case).  A workgroup that gives up writes nothing.
-constexpr int kReadySpinLimit = 1 << 22;
+// the ready word with a sleep between them, about 4 s at most with the default
+// limit (workgroup 0's own wait for the arena lock is bounded well below that,
+// and it publishes in every case).  A workgroup that gives up writes nothing:
+// it replaces the ready word's old value with ~epoch, and workgroup 0, which
+// publishes with an exchange, then finds ~epoch and marks the reservation
+// incomplete (status 7, failure bit 4).  Had workgroup 0 published first, the
+// replacement fails, the waiter sees epoch and goes on as usual.
 // Compacting workgroups of one launch (each owns every 2047th block): 2047
 // measured best on gfx950 at 4096 blocks (694 with overflow: 12.6 us with a
 // pending free) and at 1024 blocks (all with overflow: 11.9 us), against 511
@@ -489,15 +498,24 @@ __global__ __launch_bounds__(kLanes) void allocate_compact_kernel(
     int32_t *__restrict__ buffer_meta, int32_t max_free_regions, uint8_t *__restrict__ arena,
     int32_t *__restrict__ blocks, const uint8_t *__restrict__ extra_starts,
     lct_pending_frees frees, uint64_t *__restrict__ ready, uint64_t epoch, int32_t n_blocks,
-    int64_t logical_numel, int S, int precomputed) {
+    int64_t logical_numel, int S, int precomputed, int32_t lock_spins, int32_t ready_limit) {
     extern __shared__ int32_t free_list[];   // 2 * max_free_regions ints (workgroup 0)
+    const uint64_t gave_up = ~epoch;
     if (blockIdx.x == 0) {
-        LdsReserve reserve{AllocatorMeta(buffer_meta, max_free_regions), descriptor, frees,
-                           free_list, {}, -1};
+        LdsReserve reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins), descriptor,
+                           frees, free_list, {}, -1, kStatusOk};
         scan_allocate<false>(summaries, counts, blocks, n_blocks, reserve);
         // finish() released every write of the workgroup at agent scope.
-        if (threadIdx.x == 0)
-            __hip_atomic_store(ready, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) {
+            const uint64_t before = __hip_atomic_exchange(ready, epoch, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT);
+            if (before == gave_up && reserve.status == kStatusOk) {
+                // Some compacting workgroup left without writing its blocks.
+                __hip_atomic_store(descriptor + 2, kStatusIncomplete, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                record_failure(reserve.meta, kFailIncomplete);
+            }
+        }
         return;
     }
     __shared__ int32_t go;
@@ -535,15 +553,25 @@ __global__ __launch_bounds__(kLanes) void allocate_compact_kernel(
     BlockEntries e = rank_block(extra_starts, block, S, scratch, entry_offset, entry_start,
                                 entry_lane, source, logical_numel, precomputed);
     if (t == 0) {
-        int32_t seen = 0;
-        for (int i = 0; i < kReadySpinLimit; ++i) {
-            if (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch) {
-                seen = 1;
-                break;
-            }
+        uint64_t value = 0;
+        for (int i = 0; i < ready_limit; ++i) {
+            value = __hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (value == epoch) break;
             __builtin_amdgcn_s_sleep(8);
         }
-        go = seen;
+        // Giving up: leave ~epoch in the ready word for workgroup 0 to find,
+        // unless it published meanwhile (the value can change at most twice:
+        // to epoch, or to ~epoch by another waiter).
+        while (value != epoch && value != gave_up) {
+            uint64_t expected = value;
+            if (__hip_atomic_compare_exchange_strong(ready, &expected, gave_up,
+                                                     __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT))
+                value = gave_up;
+            else
+                value = expected;
+        }
+        go = value == epoch ? 1 : 0;
     }
     __syncthreads();
     if (go == 0) return;
@@ -685,7 +713,7 @@ extern "C" int32_t lct_prefix_allocate(int32_t *summaries, int32_t *counts,
         return LCT_E_ARG;
     hipLaunchKernelGGL(prefix_allocate_kernel, dim3(1), dim3(kLanes), 0, stream, summaries,
                        counts, descriptor, buffer_meta, blocks, static_cast<int32_t>(n_blocks),
-                       buffered, max_free_regions);
+                       buffered, max_free_regions, lock_spins());
     return static_cast<int32_t>(hipGetLastError());
 }
 
@@ -745,7 +773,8 @@ extern "C" int32_t lct_allocate_compact(const void *source, int32_t *summaries,
     hipLaunchKernelGGL(allocate_compact_kernel, dim3(grid), dim3(kLanes), lds, stream, source,
                        summaries, counts, descriptor, buffer_meta, max_free_regions, arena,
                        blocks, extra_starts, pending, ready, epoch,
-                       static_cast<int32_t>(n_blocks), logical_numel, g.steps, precomputed);
+                       static_cast<int32_t>(n_blocks), logical_numel, g.steps, precomputed,
+                       lock_spins(), ready_polls());
     return static_cast<int32_t>(hipGetLastError());
 }
 

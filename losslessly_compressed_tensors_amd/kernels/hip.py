@@ -117,6 +117,7 @@ _SIGNATURES = {
     "lct_buffer_reset": [_ptr, _c_int32, _c_int32, _ptr],
     "lct_buffer_allocate": [_ptr, _c_int32, _ptr, _ptr, _c_int32, _ptr, _ptr],
     "lct_buffer_free": [_ptr, _c_int32, _ptr, _ptr, _ptr],
+    "lct_set_wait_limits": [_c_int32, _c_int32],
 }
 
 EXPORTED = tuple(_SIGNATURES) + ("lct_version", "lct_error_string")

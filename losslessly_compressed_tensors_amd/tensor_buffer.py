@@ -7,6 +7,13 @@ and free run on the device (``lct_buffer_allocate`` / ``lct_buffer_free``)
 and return ``[offset, size, status, generation]`` descriptors without a host
 sync.  ``reset()`` bumps the generation so older descriptors become stale.
 
+A compressed tensor whose overflow reservation fails (no fit, lock not taken,
+or an incomplete compaction) also sets a bit of a failure word kept in the
+metadata's padding; ``verify_buffer``, ``TensorBuffer.check`` and the
+tensor's own ``memory_size()`` raise ``BufferReservationError`` at their
+synchronisation.  The reference never reports this case
+(``LCT/kernels/tensor_buffer.py:84-89``).
+
 ``CompressedTensor.free()`` (which reports no status) defers its free to the
 buffer's next reservation on the same stream: the compressed-output paths
 reserve and compact in one launch (``lct_allocate_compact``) that first
@@ -24,6 +31,45 @@ import torch
 from .kernels import dispatch
 
 _ALIGNMENT = 16
+
+# Descriptor statuses (LCT/kernels/tensor_buffer.py:37-192; 7 is this
+# build's: a reservation whose compaction did not complete).
+STATUS_OK, STATUS_NO_FIT, STATUS_EMPTY, STATUS_FREE_LIST_FULL = 0, 1, 2, 3
+STATUS_INVALID, STATUS_FREED, STATUS_LOCK, STATUS_INCOMPLETE = 4, 5, 6, 7
+
+# Bits of the buffer's failure word (int32 after the generation): a compressed
+# tensor's overflow reservation found no fit, could not take the arena lock, or
+# its compaction did not complete.  Kept until reset().
+FAIL_NO_FIT, FAIL_LOCK, FAIL_INCOMPLETE = 1, 2, 4
+_FAILURE_TEXT = {
+    FAIL_NO_FIT: "no free region was large enough",
+    FAIL_LOCK: "the arena lock could not be taken",
+    FAIL_INCOMPLETE: "the compaction into the reservation did not complete",
+}
+_STATUS_FAILURE = {STATUS_NO_FIT: FAIL_NO_FIT, STATUS_LOCK: FAIL_LOCK,
+                   STATUS_INCOMPLETE: FAIL_INCOMPLETE}
+
+
+class BufferReservationError(RuntimeError):
+    """A compressed tensor's overflow data could not be stored in its
+    ``TensorBuffer``; the tensor does not decode to its input.  The reference
+    leaves such a tensor unflagged (``LCT/kernels/tensor_buffer.py:84-89``)."""
+
+
+def _describe(bits: int) -> str:
+    return "; ".join(text for bit, text in _FAILURE_TEXT.items() if bits & bit)
+
+
+def check_reservation(status: int, count: int) -> None:
+    """Raise ``BufferReservationError`` for a codec reservation with ``count``
+    overflow entries whose descriptor status says the entries were not
+    stored."""
+    if count > 0 and status in _STATUS_FAILURE:
+        raise BufferReservationError(
+            f"compressed tensor's overflow reservation failed (status {status}: "
+            f"{_describe(_STATUS_FAILURE[status])}); its {count} overflow streams were not "
+            "stored and it does not decode to its input. Size the TensorBuffer for all "
+            "live compressed tensors.")
 
 
 @dataclass(frozen=True)
@@ -87,12 +133,14 @@ class TensorBuffer:
                                     dtype=torch.uint8, device=torch.device(device or "cuda"))
         self.device = self._storage.device
         regions = self.max_free_regions
-        meta = self._storage.narrow(0, 0, 8 * regions + 12).view(torch.int32)
+        meta = self._storage.narrow(0, 0, 8 * regions + 16).view(torch.int32)
         self._free_starts = meta.narrow(0, 0, regions)
         self._free_sizes = meta.narrow(0, regions, regions)
         self._free_count = meta.narrow(0, 2 * regions, 1)
         self._lock = meta.narrow(0, 2 * regions + 1, 1)
         self._generation = meta.narrow(0, 2 * regions + 2, 1)
+        # In the metadata's alignment padding (8R + 12 rounded up to 16).
+        self._failures = meta.narrow(0, 2 * regions + 3, 1)
         self._data = self._storage.narrow(0, self._metadata_bytes, self.capacity_bytes)
         # Descriptors whose free waits for the next reservation, and the raw
         # handle of the stream they were freed on.
@@ -125,6 +173,10 @@ class TensorBuffer:
             self._flush_frees()
         self._pending_frees.append(descriptor)
         self._pending_stream = stream
+
+    def _restore_frees(self, frees: list[torch.Tensor]) -> None:
+        """Put back frees taken for a reservation that was not launched."""
+        self._pending_frees = [*frees, *self._pending_frees]
 
     def _take_frees(self) -> list[torch.Tensor]:
         """The deferred frees for a reservation on the current stream (those
@@ -187,9 +239,27 @@ class TensorBuffer:
         return _free_now(self._storage, allocation.descriptor, self.max_free_regions)
 
     def reset(self) -> None:
-        """Reset asynchronously; previously returned descriptors become stale."""
+        """Reset asynchronously; previously returned descriptors become stale
+        and the failure word is cleared."""
         self._flush_frees()
         dispatch.buffer_reset(self._storage, self.max_free_regions, self.capacity_bytes)
+
+    def failures(self) -> int:
+        """Synchronize and return the failure word: ``FAIL_*`` bits of the
+        compressed tensors whose overflow reservation failed since the last
+        reset (0 if none)."""
+        self._flush_frees()
+        return int(self._failures.item())
+
+    def check(self) -> None:
+        """Synchronize and raise ``BufferReservationError`` if a compressed
+        tensor's overflow reservation failed since the last reset."""
+        bits = self.failures()
+        if bits:
+            raise BufferReservationError(
+                f"a compressed tensor's overflow reservation in this TensorBuffer failed "
+                f"({_describe(bits)}); that tensor does not decode to its input. Size the "
+                "buffer for all live compressed tensors, then reset() it.")
 
 
 def _free_regions_snapshot(buffer: TensorBuffer) -> list[tuple[int, int]]:
@@ -204,7 +274,10 @@ def _free_regions_snapshot(buffer: TensorBuffer) -> list[tuple[int, int]]:
 
 
 def verify_buffer(buffer: TensorBuffer) -> None:
-    """Synchronize and check the free-list invariants (``tensor_buffer.py:158-170``)."""
+    """Synchronize and check the free-list invariants (``tensor_buffer.py:158-170``),
+    and that no compressed tensor's overflow reservation failed since the last
+    reset (``BufferReservationError``)."""
+    buffer.check()
     previous_end = 0
     free_bytes = 0
     for start, size in _free_regions_snapshot(buffer):

@@ -72,9 +72,20 @@ def _nulls(name):
     return args
 
 
-@pytest.mark.parametrize("name", sorted(hip._SIGNATURES))
+# Entry points that take no pointer.
+_NO_POINTERS = {"lct_set_wait_limits"}
+
+
+@pytest.mark.parametrize("name", sorted(set(hip._SIGNATURES) - _NO_POINTERS))
 def test_null_pointers_are_rejected(lib, name):
     assert getattr(lib, name)(*_nulls(name)) == LCT_E_NULL
+
+
+def test_wait_limits_reject_negative_bounds_and_restore_defaults(lib):
+    assert lib.lct_set_wait_limits(-1, 0) == LCT_E_ARG
+    assert lib.lct_set_wait_limits(0, -1) == LCT_E_ARG
+    assert lib.lct_set_wait_limits(16, 16) == 0
+    assert lib.lct_set_wait_limits(0, 0) == 0   # the defaults again
 
 
 def test_bad_geometry_is_rejected_before_launch(lib):

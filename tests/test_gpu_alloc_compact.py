@@ -27,7 +27,8 @@ from losslessly_compressed_tensors_amd.kernels import dispatch
 from losslessly_compressed_tensors_amd.kernels.dispatch import FallbackStorage
 from losslessly_compressed_tensors_amd.operations import compress, decompress
 from losslessly_compressed_tensors_amd.tensor_buffer import (
-    Allocation, TensorBuffer, _free_regions_snapshot, verify_buffer,
+    FAIL_NO_FIT, Allocation, BufferReservationError, TensorBuffer, _free_regions_snapshot,
+    verify_buffer,
 )
 
 pytestmark = pytest.mark.gpu
@@ -151,13 +152,17 @@ def test_one_launch_equals_free_scan_compact(case, frees):
     for a, b in zip(alloc_a, alloc_b):
         assert torch.equal(a.descriptor, b.descriptor)
     assert _free_regions_snapshot(buf_a) == _free_regions_snapshot(buf_b)
-    verify_buffer(buf_b)
     assert torch.equal(buf_a.data, buf_b.data), "arena bytes differ"
     status = int(desc_b[2].item())
     if name == "no-fit":
         assert status == 1
+        # Both paths record the failed codec reservation in the buffer.
+        assert buf_a.failures() == buf_b.failures() == FAIL_NO_FIT
+        with pytest.raises(BufferReservationError):
+            verify_buffer(buf_b)
     else:
         assert status == 0 and int(counts_b[0].item()) > 0
+        verify_buffer(buf_b)
 
 
 def _inputs():
