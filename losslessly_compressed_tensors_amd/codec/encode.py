@@ -142,10 +142,16 @@ def finish_encode(
     buffered = buffer is not None
     descriptor = torch.empty(4, dtype=torch.int32, device=device) if buffered else counts
     if blocks > 0 and buffered:
-        dispatch.allocate_compact(
-            tail_source, summaries, counts, descriptor, buffer, blocks_out, extra_starts,
-            buffer._take_frees(), blocks, size, logical_numel=logical_numel,
-            block_symbols=block_symbols, lanes=lanes, steps=steps, precomputed=precomputed)
+        frees = buffer._take_frees()
+        try:
+            dispatch.allocate_compact(
+                tail_source, summaries, counts, descriptor, buffer, blocks_out, extra_starts,
+                frees, blocks, size, logical_numel=logical_numel, block_symbols=block_symbols,
+                lanes=lanes, steps=steps, precomputed=precomputed)
+        except BaseException:
+            # Nothing was launched: the deferred frees wait for the next call.
+            buffer._restore_frees(frees)
+            raise
     elif blocks > 0:
         dispatch.prefix_allocate(summaries, counts, descriptor, buffer, blocks_out, blocks,
                                  False, 256)

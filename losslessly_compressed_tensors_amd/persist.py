@@ -32,14 +32,18 @@ reserves a region and copies them back in.
 from __future__ import annotations
 
 import json
+import math
 from pathlib import Path
 from typing import BinaryIO, Union
 
+import numpy as np
 import torch
 
+from .codec.geometry import geometry as layout_geometry
 from .comp_format import Distribution, DistType, NoiseLevel, StorageLayout
 from .comp_tensor import CompressedTensor
-from .tensor_buffer import TensorBuffer
+from .compression.huffman_tables import distribution_codebook
+from .tensor_buffer import TensorBuffer, check_reservation
 
 FORMAT = "lct-v1"
 
@@ -71,6 +75,7 @@ def _overflow_arrays(ct: CompressedTensor):
         return empty, empty, empty.clone(), 0, nbytes
     if ct.fallback_descriptor is not None:
         descriptor = ct.fallback_descriptor.cpu()
+        check_reservation(int(descriptor[2]), count)
         if int(descriptor[2]) != 0:
             raise ValueError("buffer-backed tensor has no overflow storage "
                              f"(allocation status {int(descriptor[2])})")
@@ -114,6 +119,97 @@ def state_of(ct: CompressedTensor) -> tuple[dict[str, torch.Tensor], dict[str, s
     return tensors, meta
 
 
+def _shifted_decode(base: np.ndarray, center: int) -> np.ndarray:
+    """The center-shifted decode table (``LCT/kernels/common/tables.py:102-118``):
+    ``len | exponent << 8`` per entry, 0 for continuation entries."""
+    base = base.astype(np.int64)
+    length = base & 255
+    symbol = (base >> 8) & 255
+    zero_delta = (-127 - center) & 255
+    delta = symbol - (symbol <= zero_delta)
+    delta = np.where(delta >= 128, delta - 256, delta)
+    exponent = np.where(symbol == 0, -127, delta + center)
+    entry = np.where(length == 0, 0, (length | (exponent << 8)) & 0xFFFFFFFF)
+    return entry.astype(np.uint32).view(np.int32)
+
+
+def _validate(tensors: dict[str, torch.Tensor], meta: dict[str, str],
+              distribution: Distribution, shape: tuple[int, ...]):
+    """Check every field the device kernels index with before anything is
+    uploaded: geometry, sizes, the per-block overflow metadata against the
+    entries it describes, the center and the tables.  Returns (size, (B, L,
+    S, W), count, nbytes); raises ``ValueError`` on any mismatch.  A record
+    that passes cannot make a kernel read or write outside its arrays."""
+    def fail(what: str):
+        raise ValueError(f"corrupt {FORMAT} record: {what}")
+
+    def tensor(name: str, dtype: torch.dtype) -> np.ndarray:
+        value = tensors.get(name)
+        if value is None:
+            fail(f"missing field {name!r}")
+        if value.dtype != dtype or value.dim() != 1:
+            fail(f"field {name!r} is not a 1-D {dtype} tensor")
+        return value.numpy()
+
+    try:
+        size = int(meta["size"])
+        stored = tuple(int(v) for v in json.loads(meta["geometry"]))
+        count = int(meta["overflow_count"])
+        nbytes = int(meta["overflow_bytes"])
+        center = int(meta["center"])
+    except (KeyError, TypeError, ValueError) as error:
+        fail(f"metadata {error}")
+    if len(stored) != 4 or stored != tuple(layout_geometry(distribution)):
+        fail(f"geometry {list(stored)} is not the layout of {distribution}")
+    B, L, S, W = stored
+    n = math.prod(shape)
+    if any(d < 0 for d in shape) or size <= 0 or size % B or not size - B < n <= size:
+        fail(f"{size} storage elements do not hold shape {list(shape)} in blocks of {B}")
+    if not -128 <= center <= 127:
+        fail(f"center {center} outside [-128, 127]")
+    nb = size // B
+    payload = tensor("payload", torch.int32)
+    side = tensor("side", torch.uint8)
+    blocks = tensor("blocks", torch.int32)
+    lanes = tensor("lanes", torch.uint8)
+    starts = tensor("starts", torch.uint8)
+    tails = tensor("tails", torch.uint8)
+    if payload.size != nb * L * W + 4 or side.size != size or blocks.size != 3 * nb:
+        fail("payload, side or block metadata size does not match the geometry")
+    if lanes.size != count or starts.size != count or tails.size != nbytes:
+        fail("overflow entry or tail sizes do not match the counts")
+    per_count = blocks[:nb].astype(np.int64)
+    if np.any(per_count < 0) or np.any(per_count > L) or int(per_count.sum()) != count:
+        fail("per-block overflow counts")
+    first = np.concatenate(([0], np.cumsum(per_count)[:-1])) if nb else per_count
+    if not np.array_equal(blocks[nb:2 * nb], first):
+        fail("per-block first entries are not the scan of the counts")
+    starts64 = starts.astype(np.int64)
+    if np.any(starts64 >= S) or np.any(starts64 & 1):
+        fail("an overflow start step is odd or past the block")
+    entry_block = np.repeat(np.arange(nb), per_count)
+    per_bytes = np.bincount(entry_block, weights=S - starts64, minlength=nb).astype(np.int64)
+    if int(per_bytes.sum()) != nbytes:
+        fail("tail bytes do not match the overflow starts")
+    base = np.concatenate(([0], np.cumsum(per_bytes)[:-1])) if nb else per_bytes
+    if not np.array_equal(blocks[2 * nb:], base):
+        fail("per-block tail bases are not the scan of the tail bytes")
+    if count > 1:
+        same_block = entry_block[1:] == entry_block[:-1]
+        if np.any(same_block & (lanes[1:].astype(np.int64) <= lanes[:-1])):
+            fail("overflow lanes do not ascend within a block")
+    table = tensors.get("decode_table")
+    if table is not None:
+        expect = _shifted_decode(distribution_codebook(distribution).decode, center)
+        if table.dtype != torch.int32 or not np.array_equal(table.numpy(), expect):
+            fail("decode table is not the distribution's table shifted by the center")
+    samples = tensors.get("sample_values")
+    if samples is not None and (samples.dtype != torch.int16
+                                or samples.numel() != min(n, 4096)):
+        fail("sample values are not one int16 per center sample")
+    return size, stored, count, nbytes
+
+
 def from_state(tensors: dict[str, torch.Tensor], meta: dict[str, str],
                device: Union[str, torch.device] = "cuda",
                buffer: TensorBuffer | None = None) -> CompressedTensor:
@@ -124,26 +220,20 @@ def from_state(tensors: dict[str, torch.Tensor], meta: dict[str, str],
     if meta.get("format") != FORMAT:
         raise ValueError(f"not an {FORMAT} record (format={meta.get('format')!r})")
     device = torch.device(device)
-    shape = tuple(json.loads(meta["shape"]))
-    distribution = _distribution_from(meta)
+    try:
+        shape = tuple(int(d) for d in json.loads(meta["shape"]))
+        distribution = _distribution_from(meta)
+    except (KeyError, TypeError, ValueError) as error:
+        raise ValueError(f"corrupt {FORMAT} record: metadata {error}") from None
     if meta["layout"] == "raw":
         data = tensors["data"].to(device)
         return CompressedTensor(data, data.numel(), distribution=distribution, shape=shape,
                                 layout=StorageLayout.RAW)
     if meta["layout"] != "compressed":
         raise ValueError(f"unknown layout {meta['layout']!r}")
-    size = int(meta["size"])
-    B, L, S, W = (int(v) for v in json.loads(meta["geometry"]))
-    nb = size // B
-    count = int(meta["overflow_count"])
-    nbytes = int(meta["overflow_bytes"])
+    tensors = {name: value.cpu() for name, value in tensors.items()}
+    size, (B, L, S, W), count, nbytes = _validate(tensors, meta, distribution, shape)
     payload, side, blocks = tensors["payload"], tensors["side"], tensors["blocks"]
-    if (size % B or payload.dtype != torch.int32 or payload.numel() != nb * L * W + 4
-            or side.dtype != torch.uint8 or side.numel() != size
-            or blocks.dtype != torch.int32 or blocks.numel() != 3 * nb
-            or tensors["lanes"].numel() != count or tensors["starts"].numel() != count
-            or tensors["tails"].numel() != nbytes):
-        raise ValueError("lct-v1 record fields do not match its geometry and counts")
     # One 4-entry counts array, as the encoder's host sequence allocates it
     # (memory_size() counts its 16 bytes).
     counts = torch.tensor([count, nbytes, 0, 0], dtype=torch.int32, device=device)

@@ -268,3 +268,27 @@ def test_every_other_buffer_operation_launches_pending_frees_first(deferral):
     buf._flush_frees()
     buf._flush_frees()                                # idempotent
     assert log == [("free", "d2", 11)]
+
+
+def test_frees_taken_by_a_reservation_that_fails_to_launch_stay_pending(deferral, monkeypatch):
+    """A reservation whose launch raises (bad arguments, a launch error)
+    launches nothing, so the deferred frees it took wait for the next one."""
+    from losslessly_compressed_tensors_amd.codec import encode as enc
+    from losslessly_compressed_tensors_amd.comp_format import Distribution
+    from losslessly_compressed_tensors_amd.kernels import hip
+
+    buf, state, log = deferral
+
+    def failing_launch(*args, **kwargs):
+        raise hip.LCTKernelError("lct_allocate_compact failed with code -4")
+
+    monkeypatch.setattr(enc.dispatch, "allocate_compact", failing_launch)
+    buf._defer_free("d1")
+    buf._defer_free("d2")
+    dummy = torch.zeros(8, dtype=torch.int32)
+    with pytest.raises(hip.LCTKernelError):
+        enc.finish_encode(dummy, dummy, dummy, dummy, dummy, 32768, Distribution(), buf, (32768,),
+                          precomputed=False, center=dummy, shifted_decode=dummy,
+                          logical_numel=32768)
+    assert log == []
+    assert buf._take_frees() == ["d1", "d2"]
