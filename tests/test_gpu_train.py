@@ -397,3 +397,110 @@ def test_gpt_all_compressed_trains():
     assert all(torch.isfinite(l) for l in losses)
     assert float(losses[-1]) < float(losses[0])
     verify_buffer(model.tensor_buffer)
+
+
+# ---------------------------------------------------------------------------
+# Config 5 at its stated shape: 12 layers, width 768, 12 heads, vocabulary
+# 50304 (ids below 50257), sequence 1024, batch 8
+# (examples/nanogpt/train_gpt_lct.py:86-303 of the reference).
+# ---------------------------------------------------------------------------
+
+
+def _full(compress_weights, compress_activations, compress_optimizer):
+    from examples.nanogpt import train_gpt_lct as gpt
+    model, optimizers = gpt.build(torch.device(DEV), compress_weights=compress_weights,
+                                  compress_activations=compress_activations,
+                                  compress_optimizer=compress_optimizer, seed=0)
+    assert (len(model.blocks), model.embed.weight.shape) == (12, (50304, 768))
+    assert model.blocks[0].attn.num_heads == 12
+    return gpt, model, optimizers
+
+
+def _full_steps(gpt, model, optimizers, steps):
+    losses = []
+    for step in range(steps):
+        inputs, targets = gpt.random_tokens(gpt.BATCH, gpt.SEQ_LEN, DEV, seed=500 + step)
+        assert inputs.shape == (8, 1024) and int(inputs.max()) < 50257
+        losses.append(gpt.train_step(model, optimizers, inputs, targets))
+        print(f"config 5 step {step}: loss {float(losses[-1]):.1f}", flush=True)
+    return losses
+
+
+def test_config5_full_shape_compressed_activations_and_momentum_bit_identical(
+        layers_counting):
+    """Two GPT-2-small steps with activations and Muon momentum compressed give
+    every loss and every final weight of the uncompressed run, bit for bit."""
+    require_gpu()
+    print("case config 5 dense", flush=True)
+    gpt, model, optimizers = _full(False, False, False)
+    dense_losses = _full_steps(gpt, model, optimizers, 2)
+    dense_weights = _weights(model)
+    del model, optimizers
+    torch.cuda.empty_cache()
+    print("case config 5 activations + momentum compressed", flush=True)
+    _, calls = layers_counting
+    gpt, model, optimizers = _full(False, True, True)
+    losses = _full_steps(gpt, model, optimizers, 2)
+    weights = _weights(model)
+    from losslessly_compressed_tensors_amd.LCTensor import LCTTensor
+    from losslessly_compressed_tensors_amd.tensor_buffer import verify_buffer
+    assert len(calls) > 100, "the layers' compressed branch did not run"
+    assert all(isinstance(m, LCTTensor) for m in optimizers[1].momentums)
+    for a, b in zip(dense_losses, losses):
+        assert torch.equal(a, b)
+    assert dense_weights.keys() == weights.keys()
+    for name in dense_weights:
+        _assert_identical([dense_weights[name]], [weights[name]])
+    verify_buffer(model.tensor_buffer)
+
+
+def test_config5_full_shape_all_compressed_weight_update_matches_oracle(monkeypatch):
+    """Weights, activations and momentum compressed: the first loss equals the
+    dense run's (the weights decode losslessly), and the fused Muon update of
+    a block matrix, p <- fma(p, 1 - lr wd, fl(-lr u)) rounded once, equals
+    the oracle's arithmetic element by element."""
+    require_gpu()
+    from losslessly_compressed_tensors_amd.components import sparse_utils
+    from losslessly_compressed_tensors_amd.LCTensor import LCTTensor
+    from losslessly_compressed_tensors_amd.tensor_buffer import verify_buffer
+    print("case config 5 dense first loss", flush=True)
+    gpt, model, optimizers = _full(False, False, False)
+    dense_first = _full_steps(gpt, model, optimizers, 1)[0]
+    del model, optimizers
+    torch.cuda.empty_cache()
+    print("case config 5 all compressed", flush=True)
+    gpt, model, optimizers = _full(True, True, True)
+    # Every projection (the head's included) starts at zero, so the first
+    # step's gradients reach no block matrix; on the second step the output
+    # projections take a full update, while q and fc (behind the still-zero
+    # projections) take only the decay, which rounds away in BF16.  The tall
+    # fc matrix is transposed into the wide group.
+    losses = _full_steps(gpt, model, optimizers, 1)
+    assert torch.equal(losses[0], dense_first)
+    watched = {"blocks.0.mlp.proj.weight": model.blocks[0].mlp.proj.weight,
+               "blocks.11.attn.proj.weight": model.blocks[11].attn.proj.weight,
+               "blocks.5.mlp.fc.weight": model.blocks[5].mlp.fc.weight,
+               "blocks.3.attn.q.weight": model.blocks[3].attn.q.weight}
+    assert all(isinstance(p, LCTTensor) for p in watched.values())
+    before = {name: bits_of(p.decompress()) for name, p in watched.items()}
+    seen = {}
+    real_apply = sparse_utils.SparseMuon._apply
+
+    def recording_apply(self, param, update):
+        for name, p in watched.items():
+            if param is p:
+                seen[name] = bits_of(update)
+        return real_apply(self, param, update)
+
+    monkeypatch.setattr(sparse_utils.SparseMuon, "_apply", recording_apply)
+    _full_steps(gpt, model, optimizers, 1)
+    muon = optimizers[1]
+    decay = float(np.float32(1 - muon.lr * muon.weight_decay))
+    neg_lr = float(np.float32(-muon.lr))
+    for name, p in watched.items():
+        expect = oracle.apply_array(oracle.OP_SCALAR_MUL_ADD, before[name], seen[name], decay,
+                                    neg_lr, False, False)
+        np.testing.assert_array_equal(bits_of(p.decompress()), expect, err_msg=name)
+        if name.endswith("proj.weight"):
+            assert not np.array_equal(expect, before[name]), name
+    verify_buffer(model.tensor_buffer)
