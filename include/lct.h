@@ -34,6 +34,7 @@ extern "C" {
 #define LCT_E_GEOMETRY (-2)    /* geometry not (B, 256, B/256, W) with even S, 2 <= W <= 64 */
 #define LCT_E_SIZE (-3)        /* sizes inconsistent or out of the supported range */
 #define LCT_E_ARG (-4)         /* another argument out of range */
+#define LCT_E_SCRATCH (-5)     /* larger than lct_compress_buffered_noalloc's working array */
 
 /* Stream geometry (B, L, S, W): LCT/codec/geometry.py:13-39. */
 typedef struct {
@@ -454,6 +455,32 @@ int32_t lct_buffer_allocate(int32_t *meta, int32_t max_free_regions,
 int32_t lct_buffer_free(int32_t *meta, int32_t max_free_regions,
                         int32_t *descriptor, int32_t *status_out,
                         hipStream_t stream);
+
+/* ---- buffered compress that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * It enqueues what compress() with a shared TensorBuffer enqueues --
+ * lct_sample_center, lct_encode_sampled and lct_allocate_compact -- and its
+ * outputs are theirs, byte for byte: side, encoded, center_out,
+ * shifted_decode_out, sample_values (NULL: not recorded), blocks, counts,
+ * descriptor, the TensorBuffer's free list and the arena region, with `frees`
+ * (NULL or pending frees) applied first.  The working arrays (partial sums,
+ * block summaries, extra starts, ready word) live in a file-scope device array
+ * of 2.2 MiB that each GPU holds until the process ends; the call allocates
+ * nothing.  Tensors of more than 8192 codec blocks are rejected with
+ * LCT_E_SCRATCH before anything is launched.  Every call on a GPU uses that
+ * GPU's one array: calls that overlap on one GPU (different streams without
+ * ordering) race; calls ordered on one stream do not.  The current device must
+ * be the stream's. */
+int32_t lct_compress_buffered_noalloc(const void *source, int64_t logical_numel, int64_t size,
+                                      lct_geometry geometry, const int32_t *base_encode,
+                                      const int32_t *base_decode, uint8_t *side,
+                                      int32_t *encoded, int32_t *center_out,
+                                      int32_t *shifted_decode_out, uint16_t *sample_values,
+                                      int32_t *blocks, int32_t *counts, int32_t *descriptor,
+                                      int32_t *buffer_meta, int32_t max_free_regions,
+                                      uint8_t *arena, const lct_pending_frees *frees,
+                                      hipStream_t stream);
 
 /* ---- bounds of the device-side waits, in polls: the arena lock (every
  * allocator entry point, default 2^20) and lct_allocate_compact's wait for its

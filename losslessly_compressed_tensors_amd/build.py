@@ -26,6 +26,7 @@ SOURCES = [
     "decode.hip",
     "pointwise.hip",
     "update.hip",
+    "noalloc.hip",
 ]
 
 # Packed FP32 instructions are kept out of the device code: the feature is

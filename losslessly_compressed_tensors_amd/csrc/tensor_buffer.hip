@@ -118,6 +118,8 @@ extern "C" const char *lct_error_string(int32_t code) {
         case LCT_E_GEOMETRY: return "unsupported stream geometry";
         case LCT_E_SIZE: return "sizes inconsistent or out of range";
         case LCT_E_ARG: return "argument out of range";
+        case LCT_E_SCRATCH:
+            return "tensor larger than the no-allocation entry point serves (8192 codec blocks)";
         default: break;
     }
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

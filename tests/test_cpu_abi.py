@@ -122,3 +122,23 @@ def test_allocate_compact_rejects_bad_frees_and_ready_before_launch(lib):
     bad_regions = lib.lct_allocate_compact(fake, fake, fake, fake, fake, 100, fake, fake, fake,
                                            None, fake, 1, 32768, 32768, geometry, 0, None)
     assert bad_regions == -4
+
+
+def test_no_alloc_compress_rejects_tensors_beyond_its_array(lib):
+    """More than 8192 codec blocks exceed the file-scope working array: rejected
+    before anything is launched (the fake pointers are never dereferenced)."""
+    fake = ctypes.c_void_p(1 << 20)
+    geometry = hip.Geometry(32768, 256, 128, 12)
+
+    def call(blocks):
+        size = blocks * 32768
+        return lib.lct_compress_buffered_noalloc(fake, size, size, geometry, fake, fake, fake,
+                                                 fake, fake, fake, None, fake, fake, fake, fake,
+                                                 256, fake, None, None)
+
+    assert call(8193) == -5   # LCT_E_SCRATCH
+    assert lib.lct_error_string(-5).decode().startswith("tensor larger than")
+    bad_size = lib.lct_compress_buffered_noalloc(fake, 10, 32768 * 2, geometry, fake, fake, fake,
+                                                 fake, fake, fake, None, fake, fake, fake, fake,
+                                                 256, fake, None, None)
+    assert bad_size == LCT_E_SIZE   # a whole empty block of padding
