@@ -7,7 +7,7 @@ weights, so near-ties could flip lengths in a restatement.  This script is run
 by hand in the build container, where the reference is mounted read-only at
 ``/root/reference``; it imports only the pure NumPy/SciPy modules
 ``LCT.compression.probabilities`` and ``LCT.compression.huffman_tables``
-(``huffman_tables.py:196-242`` and ``probabilities.py:329-372``) and never
+(``huffman_tables.py:196-242`` and ``probabilities.py:43-158``) and never
 touches a GPU.  Only the resulting vectors are committed
 (``tests/golden/tables.json``); the reference never travels.
 

@@ -33,6 +33,26 @@ def _randn(shape, seed, scale=1.0):
     return torch.randn(*shape, generator=g) * scale
 
 
+@pytest.mark.parametrize("buffered", [False, True], ids=["private", "buffered"])
+def test_headline_tensor_matches_oracle(buffered):
+    """The benchmark's own input: randn(16384, 8192) with CPU seed 0 in BF16
+    (256 MiB), GAUSSIAN CLEAN.  Every field equals the oracle's, the ratio is
+    the bench's 1.45409 and decompression restores the input."""
+    require_gpu()
+    print(f"case headline tensor buffered={buffered}", flush=True)
+    x = _randn((16384, 8192), 0).to(torch.bfloat16)
+    dist = Distribution(DistType.GAUSSIAN)
+    capacity = 64 << 20
+    buffer = TensorBuffer(capacity, device="cuda") if buffered else None
+    ct = compress(x.cuda(), dist, buffer=buffer)
+    o = oracle_compress(x, dist, buffer=oracle.Buffer(capacity, 256) if buffered else None)
+    assert int(o.counts[0]) == 771, "771 streams of the headline tensor overflow"
+    assert_matches_oracle(ct, o)
+    if not buffered:
+        assert round(2 * x.numel() / ct.memory_size(), 5) == 1.45409
+    assert np.array_equal(bits_of(decompress(ct)), bits_of(x))
+
+
 def test_c2_weight_medium():
     """8192x8192 from N(0, 0.02^2), seed 1; GAUSSIAN, MEDIUM layout."""
     require_gpu()
