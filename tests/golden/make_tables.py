@@ -86,7 +86,7 @@ def main() -> None:
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tables.json")
     with open(path, "w") as handle:
         json.dump({"source": "LCT/compression/huffman_tables.py:196-242 via "
-                             "probabilities.py:329-437", "cases": tables},
+                             "probabilities.py:43-158", "cases": tables},
                   handle, indent=0)
     print(f"wrote {len(tables)} cases to {path}")
 
