@@ -253,13 +253,33 @@ struct StreamCursorT {
     // Decode the next two symbols into entries f0/f1 (length | field << 7) and
     // return len0 + len1.  Also starts the read of the word a crossing needs.
     __device__ __forceinline__ uint32_t next_fields(uint32_t &f0, uint32_t &f1) {
+        uint32_t bits, t0;
+        first_lookup(bits, t0);
+        uint32_t t1 = second_lookup(bits, t0);
+        const uint32_t sum = resolve(bits, t0, t1);
+        f0 = t0;
+        f1 = t1;
+        return sum;
+    }
+
+    // next_fields in three stages, for callers that interleave other work
+    // between them: the word a crossing needs and the first symbol's entry ...
+    __device__ __forceinline__ void first_lookup(uint32_t &bits, uint32_t &t0) {
         pending = stage[next_row * kStride];
         // Keep the read ahead of the lookups, so its latency overlaps theirs.
         __builtin_amdgcn_sched_barrier(0);
-        const uint32_t bits = __builtin_amdgcn_alignbit(hi, lo, pos);
-        uint32_t t0 = tb->entry[bits & 255u];
-        // ubfe reads its offset from t0[4:0], the first code's length.
-        uint32_t t1 = tb->entry[__builtin_amdgcn_ubfe(bits, t0, 8)];
+        bits = __builtin_amdgcn_alignbit(hi, lo, pos);
+        t0 = tb->entry[bits & 255u];
+    }
+
+    // ... the second symbol's entry (ubfe reads its offset from t0[4:0], the
+    // first code's length) ...
+    __device__ __forceinline__ uint32_t second_lookup(uint32_t bits, uint32_t t0) const {
+        return tb->entry[__builtin_amdgcn_ubfe(bits, t0, 8)];
+    }
+
+    // ... and escaped symbols; returns len0 + len1.
+    __device__ __forceinline__ uint32_t resolve(uint32_t bits, uint32_t &t0, uint32_t &t1) const {
         uint32_t sum = (t0 + t1) & 127u;
         if (__any(sum >= 32u)) {
             // ESC + 8-bit literal table index (primitives.py:29-35).
@@ -274,8 +294,6 @@ struct StreamCursorT {
                 t1 = tb->escape[(bits >> (l0 + static_cast<uint32_t>(rare))) & 255u] | escaped;
             sum = (t0 + t1) & 127u;
         }
-        f0 = t0;
-        f1 = t1;
         return sum;
     }
 
@@ -293,6 +311,74 @@ struct StreamCursorT {
 
 // The codec kernels' cursor: one lane per stream of a block, rows of 256 words.
 using StreamCursor = StreamCursorT<kLanes>;
+
+// A cursor that keeps no window in registers: each pair reads the two words at
+// its bit position (rows pos/32 and pos/32 + 1, 1 KiB apart: one
+// ds_read2st64) and extracts 32 bits with alignbit.  Fewer instructions per
+// pair than StreamCursorT (no window shifting) at the cost of one more LDS
+// round trip on the pair's dependency chain; for kernels bounded by
+// instruction issue rather than by that chain.  Needs the block's W rows and
+// two zero pad rows staged (window_stage_bytes); the row is clamped to W, so
+// no read leaves the stage whatever the payload holds.
+__host__ __device__ constexpr int32_t window_stage_bytes(int W) { return (W + 2) * kLanes * 4; }
+
+struct WindowCursor {
+    const uint32_t *stage;   // stage + lane; row r at stage[r * kLanes]
+    const DecodeTables *tb;
+    uint32_t pos;            // bits consumed
+    uint32_t last_row;       // W: the first pad row
+    int32_t rare;
+
+    __device__ __forceinline__ void init(const uint32_t *stage_lane, const DecodeTables *tables,
+                                         uint32_t words, int32_t rare_length) {
+        stage = stage_lane;
+        tb = tables;
+        pos = 0;
+        last_row = words;
+        rare = rare_length;
+    }
+
+    __device__ __forceinline__ void first_lookup(uint32_t &bits, uint32_t &t0) {
+        const uint32_t row = min(pos >> 5, last_row);
+        const uint32_t *at = stage + row * kLanes;
+        bits = __builtin_amdgcn_alignbit(at[kLanes], at[0], pos);
+        t0 = tb->entry[bits & 255u];
+    }
+
+    __device__ __forceinline__ uint32_t second_lookup(uint32_t bits, uint32_t t0) const {
+        return tb->entry[__builtin_amdgcn_ubfe(bits, t0, 8)];
+    }
+
+    // Escaped symbols (as StreamCursorT::resolve); returns len0 + len1.
+    __device__ __forceinline__ uint32_t resolve(uint32_t bits, uint32_t &t0, uint32_t &t1) const {
+        uint32_t sum = (t0 + t1) & 127u;
+        if (__any(sum >= 32u)) {
+            const uint32_t escaped = static_cast<uint32_t>(rare) + 8u;
+            uint32_t l0 = t0 & 31u;
+            if (l0 == kEscapeLength) {
+                l0 = escaped;
+                t0 = tb->escape[(bits >> rare) & 255u] | escaped;
+                t1 = tb->entry[(bits >> l0) & 255u];
+            }
+            if ((t1 & 31u) == kEscapeLength)
+                t1 = tb->escape[(bits >> (l0 + static_cast<uint32_t>(rare))) & 255u] | escaped;
+            sum = (t0 + t1) & 127u;
+        }
+        return sum;
+    }
+
+    __device__ __forceinline__ uint32_t next_fields(uint32_t &f0, uint32_t &f1) {
+        uint32_t bits, t0;
+        first_lookup(bits, t0);
+        uint32_t t1 = second_lookup(bits, t0);
+        const uint32_t sum = resolve(bits, t0, t1);
+        f0 = t0;
+        f1 = t1;
+        return sum;
+    }
+
+    __device__ __forceinline__ void advance(uint32_t bits) { pos += bits; }
+};
 
 // BF16 bits of a decoded entry (exponent field at bits 7..14, nothing at bit 15
 // or above) and its side byte: one multiply and one bit-field insert
@@ -382,8 +468,8 @@ enum Overlay { kNoOverlay, kLdsOverlay, kHbmOverlay };
 constexpr int kHalfSteps = kChunkSteps / 2;
 
 // The entries of steps `step` and `step + 1` of this lane's stream.
-template <bool kFull, Overlay kOverlay>
-__device__ __forceinline__ void decode_pair(StreamCursor &cursor, const LaneOverlay &lane,
+template <bool kFull, Overlay kOverlay, class Cursor>
+__device__ __forceinline__ void decode_pair(Cursor &cursor, const LaneOverlay &lane,
                                             const uint8_t *tail_lds, int step, int64_t row_base,
                                             uint32_t valid_in_block, uint32_t &f0,
                                             uint32_t &f1) {
@@ -401,8 +487,8 @@ __device__ __forceinline__ void decode_pair(StreamCursor &cursor, const LaneOver
     cursor.advance(sum);
 }
 
-template <bool kFull, Overlay kOverlay>
-__device__ __forceinline__ void decode_fields(StreamCursor &cursor, const LaneOverlay &lane,
+template <bool kFull, Overlay kOverlay, class Cursor>
+__device__ __forceinline__ void decode_fields(Cursor &cursor, const LaneOverlay &lane,
                                               const uint8_t *tail_lds, int first_step,
                                               int64_t row_base, uint32_t valid_in_block,
                                               uint32_t (&f)[kHalfSteps]) {

@@ -75,6 +75,25 @@ __device__ __forceinline__ uint32_t round_bf16_high(float value) {
 
 __device__ __forceinline__ uint32_t high_exponent_byte(uint32_t h) { return (h >> 23) & 0xFFu; }
 
+// Two results rounded to BF16 at once: x0's bits in the low half, x1's in the
+// high half.  gfx950's v_cvt_pk_bf16_f32 rounds to nearest even exactly as
+// float_to_bf16 does for every FP32 pattern that is not a NaN (checked over all
+// 2^32 patterns on the device); a NaN becomes the canonical 0x7FFF, in a branch
+// the whole wave skips unless one of its results is a NaN.
+typedef float lct_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 lct_bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t round_pair_bf16(float x0, float x1) {
+    const lct_f32x2 v = {x0, x1};
+    uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, lct_bf16x2));
+    const bool nan0 = __builtin_isnan(x0), nan1 = __builtin_isnan(x1);
+    if (__builtin_expect(__any(nan0 || nan1), 0)) {
+        r = nan0 ? ((r & 0xFFFF0000u) | 0x7FFFu) : r;
+        r = nan1 ? ((r & 0x0000FFFFu) | 0x7FFF0000u) : r;
+    }
+    return r;
+}
+
 // Side byte of a high-half BF16 in bits 0..7 (higher bits are not meaningful).
 __device__ __forceinline__ uint32_t high_side_byte(uint32_t h) {
     return __builtin_amdgcn_ubfe(h, 16, 7) | ((h >> 24) & 0x80u);

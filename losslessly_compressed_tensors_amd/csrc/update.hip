@@ -240,6 +240,30 @@ struct StreamWriter {
         return !ok;
     }
 
+    // Append a pair that is known to fit (its chunk passed fits_chunk): the
+    // same bits and stores as put() without the overflow bookkeeping; the
+    // chunk's caller adds its pairs to `fits` at the end.
+    __device__ __forceinline__ void put_fast(uint2 e0, uint2 e1) {
+        const uint32_t code = e0.x | (e1.x << e0.y);
+        const uint32_t len = e0.y + e1.y;
+        const uint32_t shift = pos & 31u;
+        const uint64_t placed = static_cast<uint64_t>(code) << shift;
+        const uint32_t new_word = word | static_cast<uint32_t>(placed);
+        const bool completes = shift + len >= 32u;
+        __builtin_amdgcn_raw_buffer_store_b32(new_word, out, completes ? row_off : kOutOfRange,
+                                              0, 0);
+        row_off += completes ? row_bytes : 0u;
+        word = completes ? static_cast<uint32_t>(placed >> 32) : new_word;
+        pos += len;
+    }
+
+    // Whether every pair of the next `steps` steps fits for every lane of the
+    // wave (a symbol's code is at most 16 bits: ESC of at most 8 bits and an
+    // 8-bit literal).  Wave-uniform.
+    __device__ __forceinline__ bool fits_chunk(int steps) const {
+        return __all(pos + 16u * static_cast<uint32_t>(steps) <= limit);
+    }
+
     // After the last pair: the word being filled (the bits before the first
     // pair that did not fit, for an overflowing stream), then zero words up to
     // row W-1.
@@ -377,6 +401,225 @@ __device__ __forceinline__ void update_chunks(StreamCursor &cursor, const LaneOv
     }
 }
 
+// ---- the pipelined full-block path
+//
+// Each stream's decode is a chain of dependent LDS lookups, and only about 2.7
+// waves per SIMD exist at C4's 688 blocks, so the chains' latency used to go
+// unhidden.  Here the wave interleaves, pair by pair, the arithmetic and
+// encoding of one 8-step half with the decoding of the next half: the two are
+// independent, so the compiler fills each lookup's wait with the other half's
+// work.  A chunk in which no lane of the wave can overflow (fits_chunk) also
+// skips the overflow bookkeeping and the exponent stores, which only overflow
+// rows need.
+
+// The arithmetic and encoding of this lane's pair at chunk step s0 (absolute
+// step c + s0), in stages that the caller interleaves with a decode's lookups:
+// A's entries f0/f1 joined with A's side bytes from the slice and B from the
+// pair's word (emit_operands), the operation, BF16 rounding, the result's side
+// bytes into the slice and the encode-table reads (emit_result), and the
+// exponent codes into the stream (emit_codes).
+struct EmitState {
+    uint32_t sa0, sa1;   // A's side bytes
+    float b0, b1;        // B
+    uint32_t r;          // the results' BF16 bits (step s0 low, s0 + 1 high)
+    uint2 e0, e1;        // their encode entries
+};
+
+__device__ __forceinline__ void emit_operands(EmitState &st, const uint8_t *slice, int s0,
+                                              uint32_t b_word, const LanePair &lp) {
+    st.sa0 = side_byte(slice, s0);
+    st.sa1 = side_byte(slice, s0 + 1);
+    pair_unpack16(lp, b_word, st.b0, st.b1);
+}
+
+template <int kForm>
+__device__ __forceinline__ void emit_result(EmitState &st, const uint2 *enc, uint8_t *slice,
+                                            int s0, uint32_t f0, uint32_t f1,
+                                            const OpParams &p) {
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const uint32_t a0 = join_entry(f0, st.sa0);
+    const uint32_t a1 = join_entry(f1, st.sa1);
+    const uint32_t r = round_pair_bf16(apply_form<kForm>(p, bf16_to_float(a0), st.b0),
+                                       apply_form<kForm>(p, bf16_to_float(a1), st.b1));
+    // Side bytes: the mantissa and, from r >> 8, the sign of each half.
+    const uint32_t sign_down = r >> 8;
+    uint32_t side0, side1;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(side0) : "s"(0x7Fu), "v"(r), "v"(sign_down));
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(side1) : "s"(0x007F0000u), "v"(r), "v"(sign_down));
+    slice[s0 * kWave + lane] = static_cast<uint8_t>(side0);
+    slice[(s0 + 1) * kWave + lane] = static_cast<uint8_t>(side1 >> 16);
+    // Encode entries are 8 bytes: byte offset exponent * 8.
+    const uint8_t *table = reinterpret_cast<const uint8_t *>(enc);
+    st.e0 = *reinterpret_cast<const uint2 *>(table + ((r >> 4) & 0x7F8u));
+    st.e1 = *reinterpret_cast<const uint2 *>(table + ((r >> 20) & 0x7F8u));
+    st.r = r;
+}
+
+template <bool kFast>
+__device__ __forceinline__ void emit_codes(const EmitState &st, StreamWriter &writer,
+                                           uint32_t off0, const UpdateIo &io) {
+    if (kFast) {
+        writer.put_fast(st.e0, st.e1);
+    } else {
+        const bool over = writer.put(st.e0, st.e1);
+        const uint32_t exp_off = over ? off0 : kOutOfRange;
+        __builtin_amdgcn_raw_buffer_store_b8(st.r >> 7, io.exponents, exp_off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b8(st.r >> 23, io.exponents, exp_off + kLanes, 0, 0);
+    }
+}
+
+// One half (8 steps from chunk step `half` * 8) of emitting f, interleaved pair
+// by pair with decoding the 8 steps from `next_step` into g (kDecode).  The
+// order within a pair is pinned with scheduling barriers: each of the
+// decode's two dependent lookups is followed by independent emit work that
+// fills its latency.
+template <Overlay kOverlay, int kForm, bool kFast, bool kDecode, class Cursor>
+__device__ __forceinline__ void pipelined_half(Cursor &cursor, const LaneOverlay &lane,
+                                               const uint8_t *tail_lds, uint8_t *slice,
+                                               StreamWriter &writer, const uint2 *enc,
+                                               const UpdateIo &io, const LanePair &lp,
+                                               const OpParams &p, int64_t row_base, int c,
+                                               int half, uint32_t mask,
+                                               const uint32_t (&b_cur)[kChunkSteps / 2],
+                                               const uint32_t (&f)[kHalfSteps],
+                                               uint32_t (&g)[kHalfSteps], int next_step) {
+#pragma unroll
+    for (int j = 0; j < kHalfSteps; j += 2) {
+        const int s0 = half * kHalfSteps + j;
+        const uint32_t off0 = static_cast<uint32_t>(c + s0) * kLanes
+            + (threadIdx.x ^ mask ^ static_cast<uint32_t>(s0));
+        EmitState st;
+        uint32_t bits = 0, t0 = 0, t1 = 0;
+        if (kDecode) cursor.first_lookup(bits, t0);
+        __builtin_amdgcn_sched_barrier(0);
+        emit_operands(st, slice, s0, b_cur[s0 / 2], lp);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kDecode) t1 = cursor.second_lookup(bits, t0);
+        __builtin_amdgcn_sched_barrier(0);
+        emit_result<kForm>(st, enc, slice, s0, f[j], f[j + 1], p);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kDecode) {
+            uint32_t sum = cursor.resolve(bits, t0, t1);
+            if (kOverlay != kNoOverlay) {
+                overlay_pair<kOverlay == kLdsOverlay>(lane, tail_lds, next_step + j, t0, t1);
+                sum = (t0 + t1) & 127u;
+            }
+            cursor.advance(sum);
+            g[j] = t0;
+            g[j + 1] = t1;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        emit_codes<kFast>(st, writer, off0, io);
+    }
+}
+
+// Both halves of the chunk at c; f holds the first half's entries on entry and
+// the next chunk's first half's on exit (when kDecodeNext).
+template <Overlay kOverlay, int kForm, bool kFast, bool kDecodeNext, class Cursor>
+__device__ __forceinline__ void pipelined_chunk(Cursor &cursor, const LaneOverlay &lane,
+                                                const uint8_t *tail_lds, uint8_t *slice,
+                                                StreamWriter &writer, const uint2 *enc,
+                                                const UpdateIo &io, const LanePair &lp,
+                                                const OpParams &p, int64_t row_base, int c,
+                                                uint32_t mask,
+                                                const uint32_t (&b_cur)[kChunkSteps / 2],
+                                                uint32_t (&f)[kHalfSteps]) {
+    uint32_t g[kHalfSteps];
+    pipelined_half<kOverlay, kForm, kFast, true>(cursor, lane, tail_lds, slice, writer, enc, io,
+                                                 lp, p, row_base, c, 0, mask, b_cur, f, g,
+                                                 c + kHalfSteps);
+    pipelined_half<kOverlay, kForm, kFast, kDecodeNext>(cursor, lane, tail_lds, slice, writer,
+                                                        enc, io, lp, p, row_base, c, 1, mask,
+                                                        b_cur, g, f, c + kChunkSteps);
+    if (kFast) writer.fits += kChunkSteps / 2;
+}
+
+// Chunks [c_begin, c_end) of a full block with one overlay variant of A; as
+// update_chunks<true, ...>.  The segment's first half is decoded before the
+// loop and its last chunk decodes nothing further, so no step outside the
+// segment is decoded with this variant.
+// A's side bytes and B's words of the next two chunks (fetched two chunks
+// ahead: one chunk of work is shorter than HBM's latency under load).
+struct Prefetch {
+    SideChunk side1, side2;
+    uint32_t b1[kChunkSteps / 2], b2[kChunkSteps / 2];
+};
+
+// One chunk at c using the side bytes and B words in (side, b) -- the copy of
+// the two that holds chunk c -- and refilling them with chunk c + 32.  The two
+// copies alternate, so a chunk's loads are issued two chunks before use and no
+// register copy of an in-flight load (which would wait for it) is made.
+template <Overlay kOverlay, int S, int kForm, class Cursor>
+__device__ __forceinline__ void pipelined_step(Cursor &cursor, const LaneOverlay &lane,
+                                               const uint8_t *tail_lds, uint8_t *slice,
+                                               SideChunk &side, uint32_t (&b)[kChunkSteps / 2],
+                                               StreamWriter &writer, const uint2 *enc,
+                                               const UpdateIo &io, const LanePair &lp,
+                                               int64_t row_base, int c, int c_end,
+                                               const OpParams &p, uint32_t (&f)[kHalfSteps]) {
+    const uint32_t voffset = side_fetch_offset();
+    store_side_chunk(slice, side);
+    uint32_t b_cur[kChunkSteps / 2];
+#pragma unroll
+    for (int k = 0; k < kChunkSteps / 2; ++k) b_cur[k] = b[k];
+    const bool more = c + 2 * kChunkSteps < S;
+    side = fetch_side_chunk(io.side, more ? voffset : kOutOfRange, c + 2 * kChunkSteps);
+    fetch_b_chunk(b, io, lp, row_base, c + 2 * kChunkSteps, more);
+    const uint32_t mask = static_cast<uint32_t>((row_base + c) & 254);
+    const bool fast = writer.fits_chunk(kChunkSteps);
+    const bool next = c + kChunkSteps < c_end;
+#define LCT_CHUNK(FAST, NEXT)                                                                 \
+    pipelined_chunk<kOverlay, kForm, FAST, NEXT>(cursor, lane, tail_lds, slice, writer, enc, \
+                                                 io, lp, p, row_base, c, mask, b_cur, f)
+    if (fast) {
+        if (next) LCT_CHUNK(true, true);
+        else LCT_CHUNK(true, false);
+    } else {
+        if (next) LCT_CHUNK(false, true);
+        else LCT_CHUNK(false, false);
+    }
+#undef LCT_CHUNK
+    // The slice now holds the chunk's result side bytes.
+    const uint4 q = reinterpret_cast<const uint4 *>(slice)[threadIdx.x & (kWave - 1)];
+    store_b128<kStreaming>(q, io.side_out, voffset + static_cast<uint32_t>(c) * kLanes);
+}
+
+// Chunks [c_begin, c_end); pf.side1/b1 hold chunk c_begin's data and
+// side2/b2 chunk c_begin + 16's.  On exit the same holds for c_end.
+template <Overlay kOverlay, int S, int kForm, class Cursor>
+__device__ __forceinline__ void update_chunks_pipelined(
+    Cursor &cursor, const LaneOverlay &lane, const uint8_t *tail_lds, uint8_t *slice,
+    Prefetch &pf, StreamWriter &writer, const uint2 *enc, const UpdateIo &io,
+    const LanePair &lp, int64_t row_base, int c_begin, int c_end, const OpParams &p) {
+    if (c_begin >= c_end) return;
+    uint32_t f[kHalfSteps];
+    decode_fields<true, kOverlay>(cursor, lane, tail_lds, c_begin, row_base, 0u, f);
+    int c = c_begin;
+#pragma unroll 1
+    for (; c + kChunkSteps < c_end; c += 2 * kChunkSteps) {
+        pipelined_step<kOverlay, S, kForm>(cursor, lane, tail_lds, slice, pf.side1, pf.b1,
+                                           writer, enc, io, lp, row_base, c, c_end, p, f);
+        pipelined_step<kOverlay, S, kForm>(cursor, lane, tail_lds, slice, pf.side2, pf.b2,
+                                           writer, enc, io, lp, row_base, c + kChunkSteps, c_end,
+                                           p, f);
+    }
+    if (c < c_end) {
+        pipelined_step<kOverlay, S, kForm>(cursor, lane, tail_lds, slice, pf.side1, pf.b1,
+                                           writer, enc, io, lp, row_base, c, c_end, p, f);
+        // An odd number of chunks: the next chunk's data is in the second copy.
+        // Swapping waits for its loads, once per block at most.
+        const SideChunk side = pf.side1;
+        pf.side1 = pf.side2;
+        pf.side2 = side;
+#pragma unroll
+        for (int k = 0; k < kChunkSteps / 2; ++k) {
+            const uint32_t b = pf.b1[k];
+            pf.b1[k] = pf.b2[k];
+            pf.b2[k] = b;
+        }
+    }
+}
+
 template <bool kFull, int S, int kForm>
 __device__ __forceinline__ void update_rows(StreamCursor cursor, const LaneOverlay &lane,
                                             const uint8_t *tail_lds, uint8_t *slice,
@@ -385,9 +628,31 @@ __device__ __forceinline__ void update_rows(StreamCursor cursor, const LaneOverl
                                             int64_t row_base, uint32_t valid_in_block,
                                             const OpParams &p) {
     const LanePair lp;
-    uint32_t b_next[kChunkSteps / 2];
-    if (kFull) fetch_b_chunk(b_next, io, lp, row_base, 0, true);
     const int split = min(S, lane.wave_start & ~(kChunkSteps - 1));
+    if (kFull) {
+        // Full blocks decode with the LDS-window cursor (the stage has two pad
+        // rows); the partial block keeps the register window.
+        WindowCursor wc;
+        wc.init(cursor.stage, cursor.tb, cursor.pad_row, cursor.rare);
+        Prefetch pf;
+        pf.side1 = side_next;
+        pf.side2 = fetch_side_chunk(io.side, side_fetch_offset(), kChunkSteps);
+        fetch_b_chunk(pf.b1, io, lp, row_base, 0, true);
+        fetch_b_chunk(pf.b2, io, lp, row_base, kChunkSteps, true);
+        update_chunks_pipelined<kNoOverlay, S, kForm>(wc, lane, tail_lds, slice, pf, writer,
+                                                      enc, io, lp, row_base, 0, split, p);
+        if (split == S) return;
+        if (lane.lds)
+            update_chunks_pipelined<kLdsOverlay, S, kForm>(wc, lane, tail_lds, slice, pf,
+                                                           writer, enc, io, lp, row_base, split,
+                                                           S, p);
+        else
+            update_chunks_pipelined<kHbmOverlay, S, kForm>(wc, lane, tail_lds, slice, pf,
+                                                           writer, enc, io, lp, row_base, split,
+                                                           S, p);
+        return;
+    }
+    uint32_t b_next[kChunkSteps / 2];
     update_chunks<kFull, kNoOverlay, S, kForm>(cursor, lane, tail_lds, slice, side_next, b_next,
                                                writer, enc, io, lp, row_base, valid_in_block, 0,
                                                split, p);
@@ -445,7 +710,7 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
     uint8_t *__restrict__ exponents, int64_t n_blocks, int64_t logical_numel, int S, int W,
     int rare) {
-    extern __shared__ uint32_t stage[];   // A's payload: stage_bytes(W)
+    extern __shared__ uint32_t stage[];   // A's payload: window_stage_bytes(W)
     __shared__ DecodeTables tb;
     __shared__ uint2 enc[256];
     __shared__ int32_t scratch[kWavesPerBlock];
@@ -476,6 +741,7 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     center_from_partials(partials, n_groups, &shared_center);
     build_decode_tables(tb, a.shifted_decode, a.center[0]);
     stage_payload(stage, a.encoded, n_blocks * kLanes, block, W);
+    stage[(W + 1) * kLanes + t] = 0u;   // the window cursor's second pad row
     __syncthreads();   // center and raw encode table
     const int32_t center = shared_center;
     enc[t] = repack_encode_entry(static_cast<uint32_t>(raw_encode[byte_to_index(t, center)]));
@@ -719,6 +985,162 @@ __device__ __forceinline__ void dual_halves(StreamCursor &ca, const LaneOverlay 
     }
 }
 
+// ---- the pipelined full-block path of the two-operand kernel: as for one
+// operand, the arithmetic and encoding of one 8-step half are interleaved pair
+// by pair with decoding the next half, here of both operands (two independent
+// lookup chains), and chunks that cannot overflow use the lean writer.
+
+struct DualEmit {
+    uint32_t sa0, sa1, sb0, sb1;   // A's and B's side bytes
+    uint32_t r;                    // the results' BF16 bits (step s0 low, s0 + 1 high)
+    uint2 e0, e1;                  // their encode entries
+};
+
+__device__ __forceinline__ void dual_emit_operands(DualEmit &st, const uint8_t *half_a,
+                                                   const uint8_t *half_b, int j) {
+    st.sa0 = side_byte(half_a, j);
+    st.sa1 = side_byte(half_a, j + 1);
+    st.sb0 = side_byte(half_b, j);
+    st.sb1 = side_byte(half_b, j + 1);
+}
+
+// fma(a, alpha, b) (pointwise_scalar_dual.py:226) rounded to BF16, the result's
+// side bytes over A's in the half slice and the encode-table reads.
+__device__ __forceinline__ void dual_emit_result(DualEmit &st, const uint2 *enc, uint8_t *half_a,
+                                                 int j, uint32_t fa0, uint32_t fa1, uint32_t fb0,
+                                                 uint32_t fb1, float alpha) {
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const float a0 = bf16_to_float(join_entry(fa0, st.sa0));
+    const float a1 = bf16_to_float(join_entry(fa1, st.sa1));
+    const float b0 = bf16_to_float(join_entry(fb0, st.sb0));
+    const float b1 = bf16_to_float(join_entry(fb1, st.sb1));
+    const uint32_t r = round_pair_bf16(__builtin_fmaf(a0, alpha, b0), __builtin_fmaf(a1, alpha, b1));
+    const uint32_t sign_down = r >> 8;
+    uint32_t side0, side1;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(side0) : "s"(0x7Fu), "v"(r), "v"(sign_down));
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(side1) : "s"(0x007F0000u), "v"(r), "v"(sign_down));
+    half_a[j * kWave + lane] = static_cast<uint8_t>(side0);
+    half_a[(j + 1) * kWave + lane] = static_cast<uint8_t>(side1 >> 16);
+    const uint8_t *table = reinterpret_cast<const uint8_t *>(enc);
+    st.e0 = *reinterpret_cast<const uint2 *>(table + ((r >> 4) & 0x7F8u));
+    st.e1 = *reinterpret_cast<const uint2 *>(table + ((r >> 20) & 0x7F8u));
+    st.r = r;
+}
+
+// One operand's staged lookups for the pair at `step` (kOverlay: tails from HBM).
+template <Overlay kOverlay>
+__device__ __forceinline__ void finish_pair(StreamCursor &cursor, const LaneOverlay &lane,
+                                            int step, uint32_t bits, uint32_t &t0,
+                                            uint32_t &t1) {
+    uint32_t sum = cursor.resolve(bits, t0, t1);
+    if (kOverlay != kNoOverlay) {
+        overlay_pair<false>(lane, nullptr, step, t0, t1);
+        sum = (t0 + t1) & 127u;
+    }
+    cursor.advance(sum);
+}
+
+// The half at c: emit from fa/fb while decoding the half at c + 8 into them
+// (kDecode).
+template <Overlay kOverlay, bool kFast, bool kDecode>
+__device__ __forceinline__ void dual_pipelined_half(StreamCursor &ca, const LaneOverlay &lane_a,
+                                                    StreamCursor &cb, const LaneOverlay &lane_b,
+                                                    uint8_t *half_a, const uint8_t *half_b,
+                                                    StreamWriter &writer, const uint2 *enc,
+                                                    const UpdateIo &io, int c, uint32_t mask,
+                                                    float alpha, uint32_t (&fa)[kHalfSteps],
+                                                    uint32_t (&fb)[kHalfSteps]) {
+    uint32_t ga[kHalfSteps], gb[kHalfSteps];
+#pragma unroll
+    for (int j = 0; j < kHalfSteps; j += 2) {
+        const uint32_t off0 = static_cast<uint32_t>(c + j) * kLanes
+            + (threadIdx.x ^ mask ^ static_cast<uint32_t>(j));
+        DualEmit st;
+        uint32_t bits_a = 0, ta0 = 0, ta1 = 0, bits_b = 0, tb0 = 0, tb1 = 0;
+        if (kDecode) {
+            ca.first_lookup(bits_a, ta0);
+            cb.first_lookup(bits_b, tb0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        dual_emit_operands(st, half_a, half_b, j);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kDecode) {
+            ta1 = ca.second_lookup(bits_a, ta0);
+            tb1 = cb.second_lookup(bits_b, tb0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        dual_emit_result(st, enc, half_a, j, fa[j], fa[j + 1], fb[j], fb[j + 1], alpha);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kDecode) {
+            finish_pair<kOverlay>(ca, lane_a, c + kHalfSteps + j, bits_a, ta0, ta1);
+            finish_pair<kOverlay>(cb, lane_b, c + kHalfSteps + j, bits_b, tb0, tb1);
+            ga[j] = ta0;
+            ga[j + 1] = ta1;
+            gb[j] = tb0;
+            gb[j + 1] = tb1;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (kFast) {
+            writer.put_fast(st.e0, st.e1);
+        } else {
+            const bool over = writer.put(st.e0, st.e1);
+            const uint32_t exp_off = over ? off0 : kOutOfRange;
+            __builtin_amdgcn_raw_buffer_store_b8(st.r >> 7, io.exponents, exp_off, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b8(st.r >> 23, io.exponents, exp_off + kLanes, 0, 0);
+        }
+    }
+    if (kDecode) {
+#pragma unroll
+        for (int k = 0; k < kHalfSteps; ++k) {
+            fa[k] = ga[k];
+            fb[k] = gb[k];
+        }
+    }
+    if (kFast) writer.fits += kHalfSteps / 2;
+}
+
+// Halves [c_begin, c_end) of a full block with one overlay variant of both
+// operands (tails from HBM); as dual_halves<true, ...>.
+template <Overlay kOverlay, int S>
+__device__ __forceinline__ void dual_halves_pipelined(
+    StreamCursor &ca, const LaneOverlay &lane_a, StreamCursor &cb, const LaneOverlay &lane_b,
+    uint8_t *slice, u32x2 &side_a, u32x2 &side_b, __amdgpu_buffer_rsrc_t b_side,
+    StreamWriter &writer, const uint2 *enc, const UpdateIo &io, int64_t row_base, int c_begin,
+    int c_end, float alpha) {
+    if (c_begin >= c_end) return;
+    const uint32_t voffset = half_side_offset();
+    uint8_t *half_a = slice;
+    uint8_t *half_b = slice + kHalfSlice;
+    uint32_t fa[kHalfSteps], fb[kHalfSteps];
+    decode_fields<true, kOverlay>(ca, lane_a, nullptr, c_begin, row_base, 0u, fa);
+    decode_fields<true, kOverlay>(cb, lane_b, nullptr, c_begin, row_base, 0u, fb);
+#pragma unroll 1
+    for (int c = c_begin; c < c_end; c += kHalfSteps) {
+        store_half_side(half_a, side_a);
+        store_half_side(half_b, side_b);
+        const bool more = c + kHalfSteps < S;
+        side_a = fetch_half_side(io.side, more ? voffset : kOutOfRange, c + kHalfSteps);
+        side_b = fetch_half_side(b_side, more ? voffset : kOutOfRange, c + kHalfSteps);
+        const uint32_t mask = static_cast<uint32_t>((row_base + c) & 254);
+        const bool fast = writer.fits_chunk(kHalfSteps);
+        const bool next = c + kHalfSteps < c_end;
+#define LCT_HALF(FAST, NEXT)                                                                   \
+    dual_pipelined_half<kOverlay, FAST, NEXT>(ca, lane_a, cb, lane_b, half_a, half_b, writer, \
+                                              enc, io, c, mask, alpha, fa, fb)
+        if (fast) {
+            if (next) LCT_HALF(true, true);
+            else LCT_HALF(true, false);
+        } else {
+            if (next) LCT_HALF(false, true);
+            else LCT_HALF(false, false);
+        }
+#undef LCT_HALF
+        // A's half now holds the result's side bytes.
+        const u32x2 q = reinterpret_cast<const u32x2 *>(half_a)[threadIdx.x & (kWave - 1)];
+        __builtin_amdgcn_raw_buffer_store_b64(q, io.side_out, voffset, c * kLanes, kStreaming);
+    }
+}
+
 template <bool kFull, int S>
 __device__ __forceinline__ void dual_rows(StreamCursor ca, const LaneOverlay &lane_a,
                                           StreamCursor cb, const LaneOverlay &lane_b,
@@ -727,6 +1149,13 @@ __device__ __forceinline__ void dual_rows(StreamCursor ca, const LaneOverlay &la
                                           const uint2 *enc, const UpdateIo &io,
                                           int64_t row_base, uint32_t valid_in_block, float alpha) {
     const int split = min(S, min(lane_a.wave_start, lane_b.wave_start) & ~(kHalfSteps - 1));
+    if (kFull) {
+        dual_halves_pipelined<kNoOverlay, S>(ca, lane_a, cb, lane_b, slice, side_a, side_b,
+                                             b_side, writer, enc, io, row_base, 0, split, alpha);
+        dual_halves_pipelined<kHbmOverlay, S>(ca, lane_a, cb, lane_b, slice, side_a, side_b,
+                                              b_side, writer, enc, io, row_base, split, S, alpha);
+        return;
+    }
     dual_halves<kFull, kNoOverlay, S>(ca, lane_a, cb, lane_b, slice, side_a, side_b, b_side,
                                       writer, enc, io, row_base, valid_in_block, 0, split, alpha);
     if (split < S)
@@ -933,7 +1362,7 @@ extern "C" int32_t lct_pointwise_encode(
                      overflow ? *overflow : lct_overflow{}, overflow != nullptr};
     const OpArgs args{alpha, beta, op, alpha_is_one, beta_is_one};
     const int32_t groups = sample_groups(sample_size);
-    const size_t lds = static_cast<size_t>(stage_bytes(g.fixed_words));
+    const size_t lds = static_cast<size_t>(window_stage_bytes(g.fixed_words));
     if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&pointwise_encode_kernel),
                                            lds))
         return static_cast<int32_t>(e);
