@@ -10,14 +10,16 @@
 // Memory traffic is organised per wave and per 16-step chunk:
 //  * input: a wave's lanes read one aligned 64-column group (128 bytes of
 //    BF16, or 64 exponent bytes) per row, so a chunk is 2 KiB (1 KiB) per
-//    wave; it is fetched with 16-byte non-temporal buffer loads one chunk
+//    wave; it is fetched with 16-byte non-temporal buffer loads two chunks
 //    ahead of use and staged in a wave-private LDS slice;
-//  * side bytes: written as one 16-byte store per lane per chunk (16 rows x
-//    the wave's 64 bytes, half a cache line per row) with the default cache
-//    policy: four waves complete each row's lines in L2.  Non-temporal side
-//    stores wrote 10 % more bytes to HBM and took 89 us instead of 78 us at
-//    4096 blocks on gfx950; the input loads and the payload copy-out, which
-//    move whole lines, are non-temporal (each is touched once);
+//  * side bytes: written as one 16-byte non-temporal store per lane per chunk
+//    (16 rows x the wave's 64 bytes, half a cache line per row).  With each
+//    call's outputs in fresh memory (as in use) the non-temporal stores time
+//    as the default policy in the kernel (89.4 us at 4096 blocks) and leave
+//    the caches to the next launches: the public compress is 2 us shorter.
+//    (Rewriting one output block over and over, the default policy lets the
+//    256 MB Infinity Cache absorb the writes: 78 us, a figure no real caller
+//    sees.)  The input loads and the payload copy-out are non-temporal too;
 //  * payload: built in a zeroed LDS stage -- each pair ORs its code, placed at
 //    the lane's bit position, into stage rows pos/32 and pos/32 + 1 (two
 //    ds_or_b32, conflict-free: row stride 256 words), so no partial word is
@@ -151,11 +153,13 @@ __device__ __forceinline__ void encode_block(
     // Pairs that fit.  pos only grows, so they are exactly the pairs before the
     // first one that does not, and that pair's even step is 2 * fits.
     uint32_t fits = 0;
-#pragma unroll 1
-    for (int c = 0; c < S; c += kEncChunk) {
-        store_input<kPrecomputed>(in_slice, next);
-        if (c + kEncChunk < S)
-            next = fetch_input<kFull, kPrecomputed>(src, row_base, c + kEncChunk, valid_bytes);
+    // Input chunks are fetched two ahead, alternating between `next` and
+    // `later` (no copy of a register that a load is still filling); a fetch
+    // past the block reads zeros from the range check, without memory traffic.
+    InputChunk later = fetch_input<kFull, kPrecomputed>(src, row_base, kEncChunk, valid_bytes);
+    auto chunk = [&](int c, InputChunk &held) {
+        store_input<kPrecomputed>(in_slice, held);
+        held = fetch_input<kFull, kPrecomputed>(src, row_base, c + 2 * kEncChunk, valid_bytes);
         // Column of this lane inside its wave's 64-column group: the row mask's
         // low six bits.  The chunk's first row is a multiple of 16, so row c+p
         // has mask ^ p (rows p and p+1 share it).
@@ -205,8 +209,13 @@ __device__ __forceinline__ void encode_block(
         if (!kPrecomputed) {
             const u32x4 sides = *reinterpret_cast<const u32x4 *>(in_slice + side_read);
             __builtin_amdgcn_raw_buffer_store_b128(sides, side, side_store_offset + c * kLanes, 0,
-                                                   0);
+                                                   kStreaming);
         }
+    };
+#pragma unroll 1
+    for (int c = 0; c < S; c += 2 * kEncChunk) {
+        chunk(c, next);
+        chunk(c + kEncChunk, later);
     }
     overflow_out = pos > limit;
     extra_out = static_cast<int>(2 * fits);
