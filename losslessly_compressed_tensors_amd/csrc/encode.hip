@@ -112,10 +112,11 @@ __device__ __forceinline__ void store_input(uint8_t *slice, const InputChunk &c)
     if (!kPrecomputed) reinterpret_cast<u32x4 *>(slice + 1024)[j] = c.q1;
 }
 
-// OR `value` into the LDS word at byte address `addr` (ds_or_b32).
-__device__ __forceinline__ void lds_or(uint32_t addr, uint32_t value) {
-    __hip_atomic_fetch_or(reinterpret_cast<__attribute__((address_space(3))) uint32_t *>(addr),
-                          value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+// OR `value` into the stage word at `word` (ds_or_b32).  The pointer keeps
+// its provenance (the dynamic stage, not the static input slices), so the
+// compiler may move later pairs' slice and table reads above these writes.
+__device__ __forceinline__ void lds_or(uint32_t *word, uint32_t value) {
+    __hip_atomic_fetch_or(word, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Side byte of BF16 bits v in bits 0..7 (higher bits are not meaningful):
@@ -140,9 +141,9 @@ __device__ __forceinline__ void encode_block(
     const uint32_t j = lane & (kWave - 1);
     const uint32_t limit = static_cast<uint32_t>(W) * 32u;
     // Stage rows are 1 KiB apart; rows W and W+1 are pad rows that take the
-    // words of pairs that do not fit.  Addresses are LDS byte addresses.
-    const uint32_t lane_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(stage)) + lane * 4u;
-    const uint32_t pad_addr = lane_addr + static_cast<uint32_t>(W) * kLanes * 4u;
+    // words of pairs that do not fit.
+    uint32_t *const lane_word = stage + lane;
+    uint32_t *const pad_word = lane_word + W * kLanes;
     const uint32_t valid_bytes = valid_in_block * (kPrecomputed ? 1u : 2u);
     // Side bytes of a chunk leave as one 16-byte store per lane: row j/4 of
     // the chunk, bytes (j%4)*16.. of the wave's 64-byte segment.
@@ -200,9 +201,9 @@ __device__ __forceinline__ void encode_block(
             // overflowing pair (encode.py:73-90).
             const uint64_t placed = static_cast<uint64_t>(code) << (pos & 31u);
             const bool over = after > limit;
-            const uint32_t addr = over ? pad_addr : ((pos >> 5) << 10) + lane_addr;
-            lds_or(addr, static_cast<uint32_t>(placed));
-            lds_or(addr + kLanes * 4, static_cast<uint32_t>(placed >> 32));
+            uint32_t *const word = over ? pad_word : lane_word + (pos >> 5) * kLanes;
+            lds_or(word, static_cast<uint32_t>(placed));
+            lds_or(word + kLanes, static_cast<uint32_t>(placed >> 32));
             fits += over ? 0u : 1u;
             pos = after;
         }
