@@ -38,7 +38,49 @@ constexpr int kChunkSteps = 16;   // steps per prefetched side-byte chunk
 struct DecodeTables {
     uint16_t entry[256];
     uint16_t escape[256];
+
+    // Entry of an escaped symbol's 8-bit literal (a table index).
+    __device__ __forceinline__ uint32_t escaped(uint32_t literal, int32_t) const {
+        return escape[literal];
+    }
+    // Entry of an overflow tail byte int8(e - 127) (length 0).
+    static __device__ __forceinline__ uint32_t tail(uint32_t byte) {
+        return ((byte + 127u) & 255u) << 7;
+    }
 };
+
+// Tables of the fused update kernels: the same entries with the exponent in
+// FP32 position (len | e_raw << 23), one dword each, so a decoded value is one
+// bit-field insert away from its FP32 bits (join_float) and the entry needs no
+// masking before that.  Lengths stay in bits 0..4, so (t0 + t1) & 127 still
+// adds two lengths.  An escaped literal's exponent is computed from the
+// center (index_to_exponent) instead of read from a second table: escapes are
+// rare, and the 1 KiB this saves keeps the two-operand kernel's LDS at three
+// workgroups per CU.
+struct FloatDecodeTables {
+    uint32_t entry[256];
+
+    __device__ __forceinline__ uint32_t escaped(uint32_t literal, int32_t center) const {
+        return static_cast<uint32_t>(
+                   (index_to_exponent(static_cast<int32_t>(literal), center) + 127) & 255)
+            << 23;
+    }
+    static __device__ __forceinline__ uint32_t tail(uint32_t byte) {
+        return ((byte + 127u) & 255u) << 23;
+    }
+};
+
+// FloatDecodeTables from the 1024-entry shifted decode table, one entry per
+// thread of a 256-thread block.
+__device__ __forceinline__ void build_float_decode_tables(
+    FloatDecodeTables &tb, const int32_t *__restrict__ shifted_decode) {
+    const int32_t packed = shifted_decode[threadIdx.x];
+    const int32_t length = packed & 255;
+    const uint32_t field = static_cast<uint32_t>(((packed >> 8) + 127) & 255) << 23;
+    tb.entry[threadIdx.x] = (length >= 1 && length <= 8)
+                                ? (static_cast<uint32_t>(length) | field)
+                                : static_cast<uint32_t>(kEscapeLength);
+}
 
 // Entry `t` of both tables from entry t of the 1024-entry shifted decode
 // table (len | exp << 8).
@@ -204,19 +246,22 @@ __device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, boo
 // without masking first: (t0 + t1) & 127 = len0 + len1, since each length is at
 // most 31 and the exponent fields start at bit 7.  Direct codes are 1..8 bits,
 // so the sum reaches 32 only when an entry holds the escape marker.
-template <int kStride>
+template <int kStride, class Tables = DecodeTables>
 struct StreamCursorT {
+    using TablesT = Tables;
     const uint32_t *stage;    // stage + lane; row r at stage[r * kStride]
-    const DecodeTables *tb;
+    const Tables *tb;
     uint32_t pos;             // bit offset within lo
     uint32_t lo, hi, nx;      // stream words w, w+1, w+2
     uint32_t next_row;        // row of word w+3 (clamped to the pad row)
     uint32_t pad_row;         // W: the zero row after the payload
     uint32_t pending;         // word next_row, read at the start of a pair
     int32_t rare;
+    int32_t center;           // the tensor's center (escaped literals of FloatDecodeTables)
 
-    __device__ __forceinline__ void init(const uint32_t *stage_lane, const DecodeTables *tables,
-                                         uint32_t words, int32_t rare_length) {
+    __device__ __forceinline__ void init(const uint32_t *stage_lane, const Tables *tables,
+                                         uint32_t words, int32_t rare_length,
+                                         int32_t center_value = 0) {
         stage = stage_lane;
         tb = tables;
         pos = 0;
@@ -227,6 +272,7 @@ struct StreamCursorT {
         next_row = min(3u, words);
         pending = 0;
         rare = rare_length;
+        center = center_value;
     }
 
     // Start with the stream's words 0..2 in registers and rows 3..W-1 staged
@@ -235,9 +281,9 @@ struct StreamCursorT {
     // stream's end never reach a decoded value (a code's table entries do not
     // depend on the bits after it).  Needs W >= 4.
     __device__ __forceinline__ void init_registers(const uint32_t *stage_rows,
-                                                   const DecodeTables *tables, uint32_t words,
+                                                   const Tables *tables, uint32_t words,
                                                    int32_t rare_length, uint32_t w0, uint32_t w1,
-                                                   uint32_t w2) {
+                                                   uint32_t w2, int32_t center_value = 0) {
         stage = stage_rows - 3 * kStride;
         tb = tables;
         pos = 0;
@@ -248,6 +294,7 @@ struct StreamCursorT {
         next_row = 3;
         pending = 0;
         rare = rare_length;
+        center = center_value;
     }
 
     // Decode the next two symbols into entries f0/f1 (length | field << 7) and
@@ -281,17 +328,18 @@ struct StreamCursorT {
     // ... and escaped symbols; returns len0 + len1.
     __device__ __forceinline__ uint32_t resolve(uint32_t bits, uint32_t &t0, uint32_t &t1) const {
         uint32_t sum = (t0 + t1) & 127u;
-        if (__any(sum >= 32u)) {
+        if (__builtin_expect(__any(sum >= 32u), 0)) {
             // ESC + 8-bit literal table index (primitives.py:29-35).
             const uint32_t escaped = static_cast<uint32_t>(rare) + 8u;
             uint32_t l0 = t0 & 31u;
             if (l0 == kEscapeLength) {
                 l0 = escaped;
-                t0 = tb->escape[(bits >> rare) & 255u] | escaped;
+                t0 = tb->escaped((bits >> rare) & 255u, center) | escaped;
                 t1 = tb->entry[(bits >> l0) & 255u];
             }
             if ((t1 & 31u) == kEscapeLength)
-                t1 = tb->escape[(bits >> (l0 + static_cast<uint32_t>(rare))) & 255u] | escaped;
+                t1 = tb->escaped((bits >> (l0 + static_cast<uint32_t>(rare))) & 255u, center)
+                    | escaped;
             sum = (t0 + t1) & 127u;
         }
         return sum;
@@ -322,20 +370,25 @@ using StreamCursor = StreamCursorT<kLanes>;
 // no read leaves the stage whatever the payload holds.
 __host__ __device__ constexpr int32_t window_stage_bytes(int W) { return (W + 2) * kLanes * 4; }
 
-struct WindowCursor {
+template <class Tables = DecodeTables>
+struct WindowCursorT {
+    using TablesT = Tables;
     const uint32_t *stage;   // stage + lane; row r at stage[r * kLanes]
-    const DecodeTables *tb;
+    const Tables *tb;
     uint32_t pos;            // bits consumed
     uint32_t last_row;       // W: the first pad row
     int32_t rare;
+    int32_t center;
 
-    __device__ __forceinline__ void init(const uint32_t *stage_lane, const DecodeTables *tables,
-                                         uint32_t words, int32_t rare_length) {
+    __device__ __forceinline__ void init(const uint32_t *stage_lane, const Tables *tables,
+                                         uint32_t words, int32_t rare_length,
+                                         int32_t center_value = 0) {
         stage = stage_lane;
         tb = tables;
         pos = 0;
         last_row = words;
         rare = rare_length;
+        center = center_value;
     }
 
     __device__ __forceinline__ void first_lookup(uint32_t &bits, uint32_t &t0) {
@@ -352,16 +405,17 @@ struct WindowCursor {
     // Escaped symbols (as StreamCursorT::resolve); returns len0 + len1.
     __device__ __forceinline__ uint32_t resolve(uint32_t bits, uint32_t &t0, uint32_t &t1) const {
         uint32_t sum = (t0 + t1) & 127u;
-        if (__any(sum >= 32u)) {
+        if (__builtin_expect(__any(sum >= 32u), 0)) {
             const uint32_t escaped = static_cast<uint32_t>(rare) + 8u;
             uint32_t l0 = t0 & 31u;
             if (l0 == kEscapeLength) {
                 l0 = escaped;
-                t0 = tb->escape[(bits >> rare) & 255u] | escaped;
+                t0 = tb->escaped((bits >> rare) & 255u, center) | escaped;
                 t1 = tb->entry[(bits >> l0) & 255u];
             }
             if ((t1 & 31u) == kEscapeLength)
-                t1 = tb->escape[(bits >> (l0 + static_cast<uint32_t>(rare))) & 255u] | escaped;
+                t1 = tb->escaped((bits >> (l0 + static_cast<uint32_t>(rare))) & 255u, center)
+                    | escaped;
             sum = (t0 + t1) & 127u;
         }
         return sum;
@@ -380,6 +434,8 @@ struct WindowCursor {
     __device__ __forceinline__ void advance(uint32_t bits) { pos += bits; }
 };
 
+using WindowCursor = WindowCursorT<>;
+
 // BF16 bits of a decoded entry (exponent field at bits 7..14, nothing at bit 15
 // or above) and its side byte: one multiply and one bit-field insert
 // (v_bfi_b32 takes bits 0..6 and 15 from the spread side byte and the rest
@@ -392,24 +448,34 @@ __device__ __forceinline__ uint32_t join_entry(uint32_t entry, uint32_t sm) {
     return out;
 }
 
-// Exponent field of an overflow tail byte int8(e - 127).
-__device__ __forceinline__ uint32_t tail_field(uint32_t byte) {
-    return ((byte + 127u) & 255u) << 7;
+// FP32 bits of a decoded FloatDecodeTables entry and its side byte: v_perm
+// copies the side byte into bytes 2 and 3 (mantissa at bits 16..22, sign at
+// bit 31, zeros below bit 16), and one bit-field insert (mask 0x807FFFFF)
+// takes those bits and the entry's exponent, dropping its length bits.
+__device__ __forceinline__ uint32_t join_float(uint32_t entry, uint32_t sm) {
+    const uint32_t spread = __builtin_amdgcn_perm(sm, sm, 0x00000C0Cu);
+    uint32_t out;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(out) : "s"(0x807FFFFFu), "v"(spread), "v"(entry));
+    return out;
 }
+
+// Exponent field of an overflow tail byte int8(e - 127).
+__device__ __forceinline__ uint32_t tail_field(uint32_t byte) { return DecodeTables::tail(byte); }
 
 // Overlay one lane's pair if it is at/after its overflow start: the entries
 // become the tail bytes' exponent fields with length 0, so the pair consumes
 // no payload bits.  kLdsTails picks the block's LDS copy (build_overlay staged
 // it) or the tails in HBM; the two are separate instantiations so LDS reads
-// stay ds_read instructions.
-template <bool kLdsTails>
+// stay ds_read instructions.  Tables is the cursor's table type, which fixes
+// where an entry holds the exponent.
+template <bool kLdsTails, class Tables>
 __device__ __forceinline__ void overlay_pair(const LaneOverlay &lane, const uint8_t *tail_lds,
                                              int step, uint32_t &f0, uint32_t &f1) {
     if (step >= lane.start) {
         const int32_t i = lane.offset + (step - lane.start);
         const uint8_t *src = kLdsTails ? tail_lds : lane.tail;
-        f0 = tail_field(src[i]);
-        f1 = tail_field(src[i + 1]);
+        f0 = Tables::tail(src[i]);
+        f1 = Tables::tail(src[i + 1]);
     }
 }
 
@@ -475,7 +541,9 @@ __device__ __forceinline__ void decode_pair(Cursor &cursor, const LaneOverlay &l
                                             uint32_t &f1) {
     constexpr bool kRecount = !kFull || kOverlay != kNoOverlay;
     uint32_t sum = cursor.next_fields(f0, f1);
-    if (kOverlay != kNoOverlay) overlay_pair<kOverlay == kLdsOverlay>(lane, tail_lds, step, f0, f1);
+    if (kOverlay != kNoOverlay)
+        overlay_pair<kOverlay == kLdsOverlay, typename Cursor::TablesT>(lane, tail_lds, step, f0,
+                                                                         f1);
     if (!kFull) {
         // Padding positions of the last block consume no payload bits.
         const uint32_t off0 = static_cast<uint32_t>(step) * kLanes

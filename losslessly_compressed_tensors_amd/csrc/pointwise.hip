@@ -258,8 +258,8 @@ __device__ __forceinline__ void dual_rows(const StreamCursor &a_in, const LaneOv
         const uint32_t slot = static_cast<uint32_t>(step) * kLanes + t;
         const uint32_t asm0 = a_side[slot], asm1 = a_side[slot + kLanes];
         const uint32_t bsm0 = b_side[slot], bsm1 = b_side[slot + kLanes];
-        overlay_pair<false>(a_lane, nullptr, step, af0, af1);
-        overlay_pair<false>(b_lane, nullptr, step, bf0, bf1);
+        overlay_pair<false, DecodeTables>(a_lane, nullptr, step, af0, af1);
+        overlay_pair<false, DecodeTables>(b_lane, nullptr, step, bf0, bf1);
         uint32_t alen0 = af0 & 31u, alen1 = af1 & 31u, blen0 = bf0 & 31u, blen1 = bf1 & 31u;
         const uint32_t col = t ^ static_cast<uint32_t>((row_base + step) & 254);
         const uint32_t off0 = static_cast<uint32_t>(step) * kLanes + col;

@@ -49,6 +49,11 @@ struct OpArgs {
     int32_t beta_is_one;
 };
 
+// Cursors of the fused encode kernels, over FloatDecodeTables: decoded
+// entries become FP32 operands with one v_perm and one v_bfi (join_float).
+using UpdateCursor = StreamCursorT<kLanes, FloatDecodeTables>;
+using UpdateWindow = WindowCursorT<FloatDecodeTables>;
+
 // Overflow start and tail byte index of one stream (block, lane) of A, from
 // the block's entry list (ascending lanes, tails concatenated in entry order:
 // LCT/kernels/generic/compaction.py:137-228, decode.py:195-240).  `start` is S
@@ -214,6 +219,11 @@ struct StreamWriter {
 
     __device__ __forceinline__ bool overflowed() const { return pos > limit; }
 
+    // Hold row_bytes in a VGPR from here on: a row advance is then one
+    // v_cndmask and one v_add per pair (with row_bytes in an SGPR beside the
+    // SGPR condition, gfx9's one-scalar-operand limit costs a copy per pair).
+    __device__ __forceinline__ void keep_row_bytes_in_vgpr() { asm volatile("" : "+v"(row_bytes)); }
+
     // The first pair that did not fit is the one after the pairs that fit, so
     // its (even) step is twice their count.
     __device__ __forceinline__ int32_t extra_start() const { return static_cast<int32_t>(2 * fits); }
@@ -282,6 +292,16 @@ __device__ __forceinline__ uint2 repack_encode_entry(uint32_t packed) {
     return make_uint2(packed & 0xFFFFu, packed >> 20);
 }
 
+// Exponent bytes of a pair of BF16 results r (step s0 in bits 0..15, s0 + 1 in
+// bits 16..31): bytes 0 and 2 of r >> 7.  The shift is kept opaque so that
+// each encode-table address is one byte-selecting shift (SDWA) of it, where
+// the compiler would otherwise fold shift and mask into two ops per index.
+__device__ __forceinline__ uint32_t exponent_bytes(uint32_t r) {
+    uint32_t x = r >> 7;
+    asm("" : "+v"(x));
+    return x;
+}
+
 // The side byte of a high-half BF16 result in bits 16..23: the mantissa stays
 // in bits 16..22 and the sign comes down from bit 31 (one v_bfi_b32 after a
 // shift; the compiler otherwise builds it from three instructions).
@@ -337,7 +357,7 @@ __device__ __forceinline__ void emit_pair(StreamWriter &writer, const uint2 *enc
 // blocks); on exit those of chunk c_end.  kForm < 0: the operation is chosen at
 // run time (the last, partial block).
 template <bool kFull, Overlay kOverlay, int S, int kForm>
-__device__ __forceinline__ void update_chunks(StreamCursor &cursor, const LaneOverlay &lane,
+__device__ __forceinline__ void update_chunks(UpdateCursor &cursor, const LaneOverlay &lane,
                                               const uint8_t *tail_lds, uint8_t *slice,
                                               SideChunk &side_next,
                                               uint32_t (&b_next)[kChunkSteps / 2],
@@ -372,15 +392,15 @@ __device__ __forceinline__ void update_chunks(StreamCursor &cursor, const LaneOv
                 // mask ^ s0.
                 const uint32_t off0 = static_cast<uint32_t>(step) * kLanes
                     + (threadIdx.x ^ mask ^ static_cast<uint32_t>(s0));
-                const uint32_t a0 = join_entry(f[j], side_byte(slice, s0));
-                const uint32_t a1 = join_entry(f[j + 1], side_byte(slice, s0 + 1));
+                const float a0 = __uint_as_float(join_float(f[j], side_byte(slice, s0)));
+                const float a1 = __uint_as_float(join_float(f[j + 1], side_byte(slice, s0 + 1)));
                 uint32_t h0, h1;
                 bool v0 = true, v1 = true;
                 if (kFull) {
                     float b0, b1;
                     pair_unpack16(lp, b_cur[s0 / 2], b0, b1);
-                    h0 = round_bf16_high(apply_form<kForm>(p, bf16_to_float(a0), b0));
-                    h1 = round_bf16_high(apply_form<kForm>(p, bf16_to_float(a1), b1));
+                    h0 = round_bf16_high(apply_form<kForm>(p, a0, b0));
+                    h1 = round_bf16_high(apply_form<kForm>(p, a1, b1));
                 } else {
                     v0 = off0 < valid_in_block;
                     v1 = off0 + kLanes < valid_in_block;
@@ -389,8 +409,8 @@ __device__ __forceinline__ void update_chunks(StreamCursor &cursor, const LaneOv
                     const uint32_t b1 = __builtin_amdgcn_raw_buffer_load_b16(
                         io.other, (off0 + kLanes) * 2, 0, 0);
                     // Padding positions hold 0 (side byte 0, no code).
-                    h0 = v0 ? apply_op(p, a0, b0) << 16 : 0u;
-                    h1 = v1 ? apply_op(p, a1, b1) << 16 : 0u;
+                    h0 = v0 ? apply_op_f(p, a0, bf16_to_float(b0)) << 16 : 0u;
+                    h1 = v1 ? apply_op_f(p, a1, bf16_to_float(b1)) << 16 : 0u;
                 }
                 emit_pair(writer, enc, slice, s0, h0, h1, v0, v1, off0, io);
             }
@@ -437,10 +457,10 @@ __device__ __forceinline__ void emit_result(EmitState &st, const uint2 *enc, uin
                                             int s0, uint32_t f0, uint32_t f1,
                                             const OpParams &p) {
     const uint32_t lane = threadIdx.x & (kWave - 1);
-    const uint32_t a0 = join_entry(f0, st.sa0);
-    const uint32_t a1 = join_entry(f1, st.sa1);
-    const uint32_t r = round_pair_bf16(apply_form<kForm>(p, bf16_to_float(a0), st.b0),
-                                       apply_form<kForm>(p, bf16_to_float(a1), st.b1));
+    const float a0 = __uint_as_float(join_float(f0, st.sa0));
+    const float a1 = __uint_as_float(join_float(f1, st.sa1));
+    const uint32_t r = round_pair_bf16(apply_form<kForm>(p, a0, st.b0),
+                                       apply_form<kForm>(p, a1, st.b1));
     // Side bytes: the mantissa and, from r >> 8, the sign of each half.
     const uint32_t sign_down = r >> 8;
     uint32_t side0, side1;
@@ -448,10 +468,9 @@ __device__ __forceinline__ void emit_result(EmitState &st, const uint2 *enc, uin
     asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(side1) : "s"(0x007F0000u), "v"(r), "v"(sign_down));
     slice[s0 * kWave + lane] = static_cast<uint8_t>(side0);
     slice[(s0 + 1) * kWave + lane] = static_cast<uint8_t>(side1 >> 16);
-    // Encode entries are 8 bytes: byte offset exponent * 8.
-    const uint8_t *table = reinterpret_cast<const uint8_t *>(enc);
-    st.e0 = *reinterpret_cast<const uint2 *>(table + ((r >> 4) & 0x7F8u));
-    st.e1 = *reinterpret_cast<const uint2 *>(table + ((r >> 20) & 0x7F8u));
+    const uint32_t x = exponent_bytes(r);
+    st.e0 = enc[x & 255u];
+    st.e1 = enc[(x >> 16) & 255u];
     st.r = r;
 }
 
@@ -501,7 +520,9 @@ __device__ __forceinline__ void pipelined_half(Cursor &cursor, const LaneOverlay
         if (kDecode) {
             uint32_t sum = cursor.resolve(bits, t0, t1);
             if (kOverlay != kNoOverlay) {
-                overlay_pair<kOverlay == kLdsOverlay>(lane, tail_lds, next_step + j, t0, t1);
+                overlay_pair<kOverlay == kLdsOverlay, typename Cursor::TablesT>(lane, tail_lds,
+                                                                                next_step + j,
+                                                                                t0, t1);
                 sum = (t0 + t1) & 127u;
             }
             cursor.advance(sum);
@@ -621,7 +642,7 @@ __device__ __forceinline__ void update_chunks_pipelined(
 }
 
 template <bool kFull, int S, int kForm>
-__device__ __forceinline__ void update_rows(StreamCursor cursor, const LaneOverlay &lane,
+__device__ __forceinline__ void update_rows(UpdateCursor cursor, const LaneOverlay &lane,
                                             const uint8_t *tail_lds, uint8_t *slice,
                                             SideChunk side_next, StreamWriter &writer,
                                             const uint2 *enc, const UpdateIo &io,
@@ -632,8 +653,8 @@ __device__ __forceinline__ void update_rows(StreamCursor cursor, const LaneOverl
     if (kFull) {
         // Full blocks decode with the LDS-window cursor (the stage has two pad
         // rows); the partial block keeps the register window.
-        WindowCursor wc;
-        wc.init(cursor.stage, cursor.tb, cursor.pad_row, cursor.rare);
+        UpdateWindow wc;
+        wc.init(cursor.stage, cursor.tb, cursor.pad_row, cursor.rare, cursor.center);
         Prefetch pf;
         pf.side1 = side_next;
         pf.side2 = fetch_side_chunk(io.side, side_fetch_offset(), kChunkSteps);
@@ -670,7 +691,7 @@ __device__ __forceinline__ void update_rows(StreamCursor cursor, const LaneOverl
 // Full blocks take the operation's form as a template parameter; the last,
 // partial block decides at run time.
 template <int S>
-__device__ __forceinline__ void update_block(int32_t form, bool full, const StreamCursor &cursor,
+__device__ __forceinline__ void update_block(int32_t form, bool full, const UpdateCursor &cursor,
                                              const LaneOverlay &lane, const uint8_t *tail_lds,
                                              uint8_t *slice, const SideChunk &side_next,
                                              StreamWriter &writer, const uint2 *enc,
@@ -711,7 +732,7 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     uint8_t *__restrict__ exponents, int64_t n_blocks, int64_t logical_numel, int S, int W,
     int rare) {
     extern __shared__ uint32_t stage[];   // A's payload: window_stage_bytes(W)
-    __shared__ DecodeTables tb;
+    __shared__ FloatDecodeTables tb;
     __shared__ uint2 enc[256];
     __shared__ int32_t scratch[kWavesPerBlock];
     __shared__ int32_t shared_center;
@@ -739,7 +760,8 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     // The result's center from the sampler's partial sums.
     raw_encode[t] = base_encode[t];
     center_from_partials(partials, n_groups, &shared_center);
-    build_decode_tables(tb, a.shifted_decode, a.center[0]);
+    build_float_decode_tables(tb, a.shifted_decode);
+    const int32_t a_center = a.center[0];
     stage_payload(stage, a.encoded, n_blocks * kLanes, block, W);
     stage[(W + 1) * kLanes + t] = 0u;   // the window cursor's second pad row
     __syncthreads();   // center and raw encode table
@@ -758,14 +780,15 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     wait_memory();
     __syncthreads();   // payload, tails and encode table visible; maps no longer read
 
-    StreamCursor cursor;
-    cursor.init(stage + t, &tb, static_cast<uint32_t>(W), rare);
+    UpdateCursor cursor;
+    cursor.init(stage + t, &tb, static_cast<uint32_t>(W), rare, a_center);
     const uint32_t row_bytes = static_cast<uint32_t>(n_blocks * kLanes * 4);
     StreamWriter writer{make_rsrc(encoded_out + block * kLanes,
                                   static_cast<uint32_t>(W - 1) * row_bytes + kLanes * 4),
                         row_bytes, static_cast<uint32_t>(t) * 4u,
                         static_cast<uint32_t>(W) * row_bytes + static_cast<uint32_t>(t) * 4u,
                         static_cast<uint32_t>(W) * 32u, 0u, 0u, 0u};
+    writer.keep_row_bytes_in_vgpr();
     uint8_t *slice = side_slices[t / kWave];
     const bool full = valid == block_elems;
     const int32_t form = form_of(args.op, args.alpha_is_one, args.beta_is_one);
@@ -940,8 +963,8 @@ __device__ __forceinline__ void store_half_side(uint8_t *half, u32x2 q) {
 // both operands (tails read from HBM).  On entry side_a/side_b hold half
 // c_begin's side bytes of A and B.
 template <bool kFull, Overlay kOverlay, int S>
-__device__ __forceinline__ void dual_halves(StreamCursor &ca, const LaneOverlay &lane_a,
-                                            StreamCursor &cb, const LaneOverlay &lane_b,
+__device__ __forceinline__ void dual_halves(UpdateCursor &ca, const LaneOverlay &lane_a,
+                                            UpdateCursor &cb, const LaneOverlay &lane_b,
                                             uint8_t *slice, u32x2 &side_a, u32x2 &side_b,
                                             __amdgpu_buffer_rsrc_t b_side, StreamWriter &writer,
                                             const uint2 *enc, const UpdateIo &io,
@@ -970,10 +993,10 @@ __device__ __forceinline__ void dual_halves(StreamCursor &ca, const LaneOverlay 
                 + (threadIdx.x ^ mask ^ static_cast<uint32_t>(j));
             const bool v0 = kFull || off0 < valid_in_block;
             const bool v1 = kFull || off0 + kLanes < valid_in_block;
-            const float a0 = bf16_to_float(join_entry(fa[j], side_byte(half_a, j)));
-            const float a1 = bf16_to_float(join_entry(fa[j + 1], side_byte(half_a, j + 1)));
-            const float b0 = bf16_to_float(join_entry(fb[j], side_byte(half_b, j)));
-            const float b1 = bf16_to_float(join_entry(fb[j + 1], side_byte(half_b, j + 1)));
+            const float a0 = __uint_as_float(join_float(fa[j], side_byte(half_a, j)));
+            const float a1 = __uint_as_float(join_float(fa[j + 1], side_byte(half_a, j + 1)));
+            const float b0 = __uint_as_float(join_float(fb[j], side_byte(half_b, j)));
+            const float b1 = __uint_as_float(join_float(fb[j + 1], side_byte(half_b, j + 1)));
             // Padding positions hold 0 (side byte 0, no code).
             const uint32_t h0 = v0 ? round_bf16_high(__builtin_fmaf(a0, alpha, b0)) : 0u;
             const uint32_t h1 = v1 ? round_bf16_high(__builtin_fmaf(a1, alpha, b1)) : 0u;
@@ -1010,10 +1033,10 @@ __device__ __forceinline__ void dual_emit_result(DualEmit &st, const uint2 *enc,
                                                  int j, uint32_t fa0, uint32_t fa1, uint32_t fb0,
                                                  uint32_t fb1, float alpha) {
     const uint32_t lane = threadIdx.x & (kWave - 1);
-    const float a0 = bf16_to_float(join_entry(fa0, st.sa0));
-    const float a1 = bf16_to_float(join_entry(fa1, st.sa1));
-    const float b0 = bf16_to_float(join_entry(fb0, st.sb0));
-    const float b1 = bf16_to_float(join_entry(fb1, st.sb1));
+    const float a0 = __uint_as_float(join_float(fa0, st.sa0));
+    const float a1 = __uint_as_float(join_float(fa1, st.sa1));
+    const float b0 = __uint_as_float(join_float(fb0, st.sb0));
+    const float b1 = __uint_as_float(join_float(fb1, st.sb1));
     const uint32_t r = round_pair_bf16(__builtin_fmaf(a0, alpha, b0), __builtin_fmaf(a1, alpha, b1));
     const uint32_t sign_down = r >> 8;
     uint32_t side0, side1;
@@ -1021,63 +1044,58 @@ __device__ __forceinline__ void dual_emit_result(DualEmit &st, const uint2 *enc,
     asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(side1) : "s"(0x007F0000u), "v"(r), "v"(sign_down));
     half_a[j * kWave + lane] = static_cast<uint8_t>(side0);
     half_a[(j + 1) * kWave + lane] = static_cast<uint8_t>(side1 >> 16);
-    const uint8_t *table = reinterpret_cast<const uint8_t *>(enc);
-    st.e0 = *reinterpret_cast<const uint2 *>(table + ((r >> 4) & 0x7F8u));
-    st.e1 = *reinterpret_cast<const uint2 *>(table + ((r >> 20) & 0x7F8u));
+    const uint32_t x = exponent_bytes(r);
+    st.e0 = enc[x & 255u];
+    st.e1 = enc[(x >> 16) & 255u];
     st.r = r;
 }
 
 // One operand's staged lookups for the pair at `step` (kOverlay: tails from HBM).
 template <Overlay kOverlay>
-__device__ __forceinline__ void finish_pair(StreamCursor &cursor, const LaneOverlay &lane,
+__device__ __forceinline__ void finish_pair(UpdateCursor &cursor, const LaneOverlay &lane,
                                             int step, uint32_t bits, uint32_t &t0,
                                             uint32_t &t1) {
     uint32_t sum = cursor.resolve(bits, t0, t1);
     if (kOverlay != kNoOverlay) {
-        overlay_pair<false>(lane, nullptr, step, t0, t1);
+        overlay_pair<false, FloatDecodeTables>(lane, nullptr, step, t0, t1);
         sum = (t0 + t1) & 127u;
     }
     cursor.advance(sum);
 }
 
 // The half at c: emit from fa/fb while decoding the half at c + 8 into them
-// (kDecode).
+// (kDecode).  Within a pair, each lookup's latency is filled with emit work
+// that does not depend on it: the first lookups with the operation on the
+// pair being emitted, the second lookups with its codes.  The side bytes of
+// the next pair are read a pair ahead.
 template <Overlay kOverlay, bool kFast, bool kDecode>
-__device__ __forceinline__ void dual_pipelined_half(StreamCursor &ca, const LaneOverlay &lane_a,
-                                                    StreamCursor &cb, const LaneOverlay &lane_b,
+__device__ __forceinline__ void dual_pipelined_half(UpdateCursor &ca, const LaneOverlay &lane_a,
+                                                    UpdateCursor &cb, const LaneOverlay &lane_b,
                                                     uint8_t *half_a, const uint8_t *half_b,
                                                     StreamWriter &writer, const uint2 *enc,
                                                     const UpdateIo &io, int c, uint32_t mask,
                                                     float alpha, uint32_t (&fa)[kHalfSteps],
                                                     uint32_t (&fb)[kHalfSteps]) {
     uint32_t ga[kHalfSteps], gb[kHalfSteps];
+    DualEmit st;
+    dual_emit_operands(st, half_a, half_b, 0);
 #pragma unroll
     for (int j = 0; j < kHalfSteps; j += 2) {
         const uint32_t off0 = static_cast<uint32_t>(c + j) * kLanes
             + (threadIdx.x ^ mask ^ static_cast<uint32_t>(j));
-        DualEmit st;
         uint32_t bits_a = 0, ta0 = 0, ta1 = 0, bits_b = 0, tb0 = 0, tb1 = 0;
         if (kDecode) {
             ca.first_lookup(bits_a, ta0);
             cb.first_lookup(bits_b, tb0);
         }
         __builtin_amdgcn_sched_barrier(0);
-        dual_emit_operands(st, half_a, half_b, j);
+        dual_emit_result(st, enc, half_a, j, fa[j], fa[j + 1], fb[j], fb[j + 1], alpha);
+        DualEmit next = st;
+        if (j + 2 < kHalfSteps) dual_emit_operands(next, half_a, half_b, j + 2);
         __builtin_amdgcn_sched_barrier(0);
         if (kDecode) {
             ta1 = ca.second_lookup(bits_a, ta0);
             tb1 = cb.second_lookup(bits_b, tb0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        dual_emit_result(st, enc, half_a, j, fa[j], fa[j + 1], fb[j], fb[j + 1], alpha);
-        __builtin_amdgcn_sched_barrier(0);
-        if (kDecode) {
-            finish_pair<kOverlay>(ca, lane_a, c + kHalfSteps + j, bits_a, ta0, ta1);
-            finish_pair<kOverlay>(cb, lane_b, c + kHalfSteps + j, bits_b, tb0, tb1);
-            ga[j] = ta0;
-            ga[j + 1] = ta1;
-            gb[j] = tb0;
-            gb[j + 1] = tb1;
         }
         __builtin_amdgcn_sched_barrier(0);
         if (kFast) {
@@ -1088,6 +1106,17 @@ __device__ __forceinline__ void dual_pipelined_half(StreamCursor &ca, const Lane
             __builtin_amdgcn_raw_buffer_store_b8(st.r >> 7, io.exponents, exp_off, 0, 0);
             __builtin_amdgcn_raw_buffer_store_b8(st.r >> 23, io.exponents, exp_off + kLanes, 0, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        if (kDecode) {
+            finish_pair<kOverlay>(ca, lane_a, c + kHalfSteps + j, bits_a, ta0, ta1);
+            finish_pair<kOverlay>(cb, lane_b, c + kHalfSteps + j, bits_b, tb0, tb1);
+            ga[j] = ta0;
+            ga[j + 1] = ta1;
+            gb[j] = tb0;
+            gb[j + 1] = tb1;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        st = next;
     }
     if (kDecode) {
 #pragma unroll
@@ -1099,61 +1128,124 @@ __device__ __forceinline__ void dual_pipelined_half(StreamCursor &ca, const Lane
     if (kFast) writer.fits += kHalfSteps / 2;
 }
 
-// Halves [c_begin, c_end) of a full block with one overlay variant of both
-// operands (tails from HBM); as dual_halves<true, ...>.
+// A's and B's side bytes of the next kDualDepth halves: fetched that many
+// halves ahead (one half of work is far shorter than HBM's latency under
+// load), in copies that rotate, so no register copy of an in-flight load
+// (which would wait for it) is made.  Copy 0 holds the half being started.
+constexpr int kDualDepth = 2;
+
+struct DualPrefetch {
+    u32x2 a[kDualDepth], b[kDualDepth];
+
+    // After k halves: copy k becomes copy 0 (waits for those loads; once per
+    // overlay segment at most).
+    __device__ __forceinline__ void rotate(int k) {
+        u32x2 ta[kDualDepth], tb[kDualDepth];
+#pragma unroll
+        for (int i = 0; i < kDualDepth; ++i) {
+            ta[i] = a[(i + k) % kDualDepth];
+            tb[i] = b[(i + k) % kDualDepth];
+        }
+#pragma unroll
+        for (int i = 0; i < kDualDepth; ++i) {
+            a[i] = ta[i];
+            b[i] = tb[i];
+        }
+    }
+};
+
+// The half at c using the side bytes in (side_a, side_b) -- the copy holding
+// half c -- and refilling them with half c + 8 * kDualDepth.
 template <Overlay kOverlay, int S>
-__device__ __forceinline__ void dual_halves_pipelined(
-    StreamCursor &ca, const LaneOverlay &lane_a, StreamCursor &cb, const LaneOverlay &lane_b,
+__device__ __forceinline__ void dual_half_step(
+    UpdateCursor &ca, const LaneOverlay &lane_a, UpdateCursor &cb, const LaneOverlay &lane_b,
     uint8_t *slice, u32x2 &side_a, u32x2 &side_b, __amdgpu_buffer_rsrc_t b_side,
-    StreamWriter &writer, const uint2 *enc, const UpdateIo &io, int64_t row_base, int c_begin,
-    int c_end, float alpha) {
-    if (c_begin >= c_end) return;
+    StreamWriter &writer, const uint2 *enc, const UpdateIo &io, int64_t row_base, int c,
+    int c_end, float alpha, uint32_t (&fa)[kHalfSteps], uint32_t (&fb)[kHalfSteps]) {
     const uint32_t voffset = half_side_offset();
     uint8_t *half_a = slice;
     uint8_t *half_b = slice + kHalfSlice;
-    uint32_t fa[kHalfSteps], fb[kHalfSteps];
-    decode_fields<true, kOverlay>(ca, lane_a, nullptr, c_begin, row_base, 0u, fa);
-    decode_fields<true, kOverlay>(cb, lane_b, nullptr, c_begin, row_base, 0u, fb);
-#pragma unroll 1
-    for (int c = c_begin; c < c_end; c += kHalfSteps) {
-        store_half_side(half_a, side_a);
-        store_half_side(half_b, side_b);
-        const bool more = c + kHalfSteps < S;
-        side_a = fetch_half_side(io.side, more ? voffset : kOutOfRange, c + kHalfSteps);
-        side_b = fetch_half_side(b_side, more ? voffset : kOutOfRange, c + kHalfSteps);
-        const uint32_t mask = static_cast<uint32_t>((row_base + c) & 254);
-        const bool fast = writer.fits_chunk(kHalfSteps);
-        const bool next = c + kHalfSteps < c_end;
+    store_half_side(half_a, side_a);
+    store_half_side(half_b, side_b);
+    const int ahead = c + kDualDepth * kHalfSteps;
+    const bool more = ahead < S;
+    side_a = fetch_half_side(io.side, more ? voffset : kOutOfRange, ahead);
+    side_b = fetch_half_side(b_side, more ? voffset : kOutOfRange, ahead);
+    const uint32_t mask = static_cast<uint32_t>((row_base + c) & 254);
+    const bool fast = writer.fits_chunk(kHalfSteps);
+    const bool next = c + kHalfSteps < c_end;
 #define LCT_HALF(FAST, NEXT)                                                                   \
     dual_pipelined_half<kOverlay, FAST, NEXT>(ca, lane_a, cb, lane_b, half_a, half_b, writer, \
                                               enc, io, c, mask, alpha, fa, fb)
-        if (fast) {
-            if (next) LCT_HALF(true, true);
-            else LCT_HALF(true, false);
-        } else {
-            if (next) LCT_HALF(false, true);
-            else LCT_HALF(false, false);
-        }
-#undef LCT_HALF
-        // A's half now holds the result's side bytes.
-        const u32x2 q = reinterpret_cast<const u32x2 *>(half_a)[threadIdx.x & (kWave - 1)];
-        __builtin_amdgcn_raw_buffer_store_b64(q, io.side_out, voffset, c * kLanes, kStreaming);
+    if (fast) {
+        if (next) LCT_HALF(true, true);
+        else LCT_HALF(true, false);
+    } else {
+        if (next) LCT_HALF(false, true);
+        else LCT_HALF(false, false);
     }
+#undef LCT_HALF
+    // A's half now holds the result's side bytes.
+    const u32x2 q = reinterpret_cast<const u32x2 *>(half_a)[threadIdx.x & (kWave - 1)];
+    __builtin_amdgcn_raw_buffer_store_b64(q, io.side_out, voffset, c * kLanes, kStreaming);
+}
+
+// Halves [c_begin, c_end) of a full block with one overlay variant of both
+// operands (tails from HBM); as dual_halves<true, ...>.  On entry pf's copy i
+// holds half c_begin + 8i; on exit the same holds for c_end.
+template <Overlay kOverlay, int S>
+__device__ __forceinline__ void dual_halves_pipelined(
+    UpdateCursor &ca, const LaneOverlay &lane_a, UpdateCursor &cb, const LaneOverlay &lane_b,
+    uint8_t *slice, DualPrefetch &pf, __amdgpu_buffer_rsrc_t b_side, StreamWriter &writer,
+    const uint2 *enc, const UpdateIo &io, int64_t row_base, int c_begin, int c_end,
+    float alpha) {
+    if (c_begin >= c_end) return;
+    uint32_t fa[kHalfSteps], fb[kHalfSteps];
+    decode_fields<true, kOverlay>(ca, lane_a, nullptr, c_begin, row_base, 0u, fa);
+    decode_fields<true, kOverlay>(cb, lane_b, nullptr, c_begin, row_base, 0u, fb);
+    int c = c_begin;
+#pragma unroll 1
+    for (; c + (kDualDepth - 1) * kHalfSteps < c_end; c += kDualDepth * kHalfSteps) {
+#pragma unroll
+        for (int k = 0; k < kDualDepth; ++k)
+            dual_half_step<kOverlay, S>(ca, lane_a, cb, lane_b, slice, pf.a[k], pf.b[k], b_side,
+                                        writer, enc, io, row_base, c + k * kHalfSteps, c_end,
+                                        alpha, fa, fb);
+    }
+    // Fewer than kDualDepth halves left.
+    const int left = (c_end - c) / kHalfSteps;
+#pragma unroll
+    for (int k = 0; k < kDualDepth - 1; ++k)
+        if (k < left)
+            dual_half_step<kOverlay, S>(ca, lane_a, cb, lane_b, slice, pf.a[k], pf.b[k], b_side,
+                                        writer, enc, io, row_base, c + k * kHalfSteps, c_end,
+                                        alpha, fa, fb);
+    if (left == 1) pf.rotate(1);
+    else if (left == 2) pf.rotate(2);
+    else if (left == 3) pf.rotate(3);
 }
 
 template <bool kFull, int S>
-__device__ __forceinline__ void dual_rows(StreamCursor ca, const LaneOverlay &lane_a,
-                                          StreamCursor cb, const LaneOverlay &lane_b,
+__device__ __forceinline__ void dual_rows(UpdateCursor ca, const LaneOverlay &lane_a,
+                                          UpdateCursor cb, const LaneOverlay &lane_b,
                                           uint8_t *slice, u32x2 side_a, u32x2 side_b,
                                           __amdgpu_buffer_rsrc_t b_side, StreamWriter &writer,
                                           const uint2 *enc, const UpdateIo &io,
                                           int64_t row_base, uint32_t valid_in_block, float alpha) {
     const int split = min(S, min(lane_a.wave_start, lane_b.wave_start) & ~(kHalfSteps - 1));
     if (kFull) {
-        dual_halves_pipelined<kNoOverlay, S>(ca, lane_a, cb, lane_b, slice, side_a, side_b,
-                                             b_side, writer, enc, io, row_base, 0, split, alpha);
-        dual_halves_pipelined<kHbmOverlay, S>(ca, lane_a, cb, lane_b, slice, side_a, side_b,
-                                              b_side, writer, enc, io, row_base, split, S, alpha);
+        DualPrefetch pf;
+        pf.a[0] = side_a;
+        pf.b[0] = side_b;
+#pragma unroll
+        for (int k = 1; k < kDualDepth; ++k) {
+            pf.a[k] = fetch_half_side(io.side, half_side_offset(), k * kHalfSteps);
+            pf.b[k] = fetch_half_side(b_side, half_side_offset(), k * kHalfSteps);
+        }
+        dual_halves_pipelined<kNoOverlay, S>(ca, lane_a, cb, lane_b, slice, pf, b_side, writer,
+                                             enc, io, row_base, 0, split, alpha);
+        dual_halves_pipelined<kHbmOverlay, S>(ca, lane_a, cb, lane_b, slice, pf, b_side, writer,
+                                              enc, io, row_base, split, S, alpha);
         return;
     }
     dual_halves<kFull, kNoOverlay, S>(ca, lane_a, cb, lane_b, slice, side_a, side_b, b_side,
@@ -1174,7 +1266,7 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     uint8_t *__restrict__ exponents, int64_t n_blocks, int64_t logical_numel, int S, int W,
     int rare) {
     extern __shared__ uint32_t stages[];   // A's rows 3..W-1, then B's
-    __shared__ DecodeTables tba, tbb;
+    __shared__ FloatDecodeTables tba, tbb;
     __shared__ uint2 enc[256];
     __shared__ int32_t scratch[kWavesPerBlock];
     __shared__ int32_t shared_center;
@@ -1209,8 +1301,9 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
 
     raw_encode[t] = base_encode[t];
     center_from_partials(partials, n_groups, &shared_center);
-    build_decode_tables(tba, a.shifted_decode, a.center[0]);
-    build_decode_tables(tbb, b.shifted_decode, b.center[0]);
+    build_float_decode_tables(tba, a.shifted_decode);
+    build_float_decode_tables(tbb, b.shifted_decode);
+    const int32_t a_center = a.center[0], b_center = b.center[0];
     stage_payload_rows(stage_a, a.encoded, n_streams, block, kRegisterRows, W);
     stage_payload_rows(stage_b, b.encoded, n_streams, block, kRegisterRows, W);
     __syncthreads();   // center and raw encode table
@@ -1231,15 +1324,18 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     wait_memory();
     __syncthreads();   // payloads and encode table visible; maps no longer read
 
-    StreamCursor ca, cb;
-    ca.init_registers(stage_a + t, &tba, static_cast<uint32_t>(W), rare, wa[0], wa[1], wa[2]);
-    cb.init_registers(stage_b + t, &tbb, static_cast<uint32_t>(W), rare, wb[0], wb[1], wb[2]);
+    UpdateCursor ca, cb;
+    ca.init_registers(stage_a + t, &tba, static_cast<uint32_t>(W), rare, wa[0], wa[1], wa[2],
+                      a_center);
+    cb.init_registers(stage_b + t, &tbb, static_cast<uint32_t>(W), rare, wb[0], wb[1], wb[2],
+                      b_center);
     const uint32_t row_bytes = static_cast<uint32_t>(n_streams * 4);
     StreamWriter writer{make_rsrc(encoded_out + block * kLanes,
                                   static_cast<uint32_t>(W - 1) * row_bytes + kLanes * 4),
                         row_bytes, static_cast<uint32_t>(t) * 4u,
                         static_cast<uint32_t>(W) * row_bytes + static_cast<uint32_t>(t) * 4u,
                         static_cast<uint32_t>(W) * 32u, 0u, 0u, 0u};
+    writer.keep_row_bytes_in_vgpr();
     uint8_t *slice = slices[t / kWave];
     const bool full = valid == block_elems;
 #define LCT_DUAL_ROWS(FULL, SS)                                                                \
