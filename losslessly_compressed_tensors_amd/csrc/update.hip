@@ -26,11 +26,18 @@
 // The encoder side writes each payload word straight to HBM when the word
 // completes (one 4-byte store by the lanes whose word completed in a pair,
 // merged in L2), so the workgroup's LDS holds only A's payload: at W = 25,
-// four blocks fit per CU.
+// four blocks fit per CU.  The result's side bytes leave with the default
+// cache policy: a wave writes 64 bytes of each 128-byte row line, and
+// non-temporal stores of half lines wrote 16% more than the side bytes (C4:
+// 73.6 MB against 62.9 MB per launch; with the default policy 63.3 MB, at
+// equal kernel time).
 #include "pointwise_ops.h"
 
 namespace lct {
 namespace {
+
+// Cache policy of the result's side-byte stores: the default (see above).
+constexpr int kSideStore = 0;
 
 struct OperandA {
     const int32_t *encoded;
@@ -417,7 +424,7 @@ __device__ __forceinline__ void update_chunks(UpdateCursor &cursor, const LaneOv
         }
         // The slice now holds the chunk's result side bytes.
         const uint4 q = reinterpret_cast<const uint4 *>(slice)[threadIdx.x & (kWave - 1)];
-        store_b128<kStreaming>(q, io.side_out, voffset + static_cast<uint32_t>(c) * kLanes);
+        store_b128<kSideStore>(q, io.side_out, voffset + static_cast<uint32_t>(c) * kLanes);
     }
 }
 
@@ -602,7 +609,7 @@ __device__ __forceinline__ void pipelined_step(Cursor &cursor, const LaneOverlay
 #undef LCT_CHUNK
     // The slice now holds the chunk's result side bytes.
     const uint4 q = reinterpret_cast<const uint4 *>(slice)[threadIdx.x & (kWave - 1)];
-    store_b128<kStreaming>(q, io.side_out, voffset + static_cast<uint32_t>(c) * kLanes);
+    store_b128<kSideStore>(q, io.side_out, voffset + static_cast<uint32_t>(c) * kLanes);
 }
 
 // Chunks [c_begin, c_end); pf.side1/b1 hold chunk c_begin's data and
@@ -1004,7 +1011,7 @@ __device__ __forceinline__ void dual_halves(UpdateCursor &ca, const LaneOverlay 
         }
         // A's half now holds the result's side bytes.
         const u32x2 q = reinterpret_cast<const u32x2 *>(half_a)[threadIdx.x & (kWave - 1)];
-        __builtin_amdgcn_raw_buffer_store_b64(q, io.side_out, voffset, c * kLanes, kStreaming);
+        __builtin_amdgcn_raw_buffer_store_b64(q, io.side_out, voffset, c * kLanes, kSideStore);
     }
 }
 
@@ -1187,7 +1194,7 @@ __device__ __forceinline__ void dual_half_step(
 #undef LCT_HALF
     // A's half now holds the result's side bytes.
     const u32x2 q = reinterpret_cast<const u32x2 *>(half_a)[threadIdx.x & (kWave - 1)];
-    __builtin_amdgcn_raw_buffer_store_b64(q, io.side_out, voffset, c * kLanes, kStreaming);
+    __builtin_amdgcn_raw_buffer_store_b64(q, io.side_out, voffset, c * kLanes, kSideStore);
 }
 
 // Halves [c_begin, c_end) of a full block with one overlay variant of both
