@@ -19,13 +19,16 @@
 //    the caches to the next launches: the public compress is 2 us shorter.
 //    (Rewriting one output block over and over, the default policy lets the
 //    256 MB Infinity Cache absorb the writes: 78 us, a figure no real caller
-//    sees.)  The input loads and the payload copy-out are non-temporal too;
+//    sees.)  The input loads are non-temporal too (default-policy loads:
+//    91 us against 88);
 //  * payload: built in a zeroed LDS stage -- each pair ORs its code, placed at
 //    the lane's bit position, into stage rows pos/32 and pos/32 + 1 (two
 //    ds_or_b32, conflict-free: row stride 256 words), so no partial word is
 //    carried in registers; after the loop the block copies rows 0..W-1 to
-//    `encoded` with 16-byte stores.  Rows W and W+1 are pad rows that take the
-//    pairs that do not fit;
+//    `encoded` with 16-byte stores of the default cache policy (each block's
+//    rows are 1 KiB pieces 4 MiB apart; non-temporal stores of them took the
+//    kernel from 82 to 88 us at 4096 blocks).  Rows W and W+1 are pad rows
+//    that take the pairs that do not fit;
 //  * side bytes: once a pair's two input rows are read, their side bytes take
 //    the first 64 bytes of those rows in the input slice.
 //
@@ -337,14 +340,13 @@ __global__ __launch_bounds__(kLanes) void encode_kernel(
     extra_starts[block * kLanes + t] = static_cast<uint8_t>(overflow ? extra : 255);
     __syncthreads();
 
-    // Copy the W payload rows out, 16 bytes per thread per non-temporal store.
+    // Copy the W payload rows out, 16 bytes per thread per store.
     const int chunks = W * (kLanes / 4);
     for (int c = t; c < chunks; c += kLanes) {
         const int row = c / (kLanes / 4);
         const int quad = c % (kLanes / 4);
         const auto value = reinterpret_cast<const u32x4 *>(stage + row * kLanes)[quad];
-        __builtin_nontemporal_store(value, reinterpret_cast<u32x4 *>(
-                                               encoded + row * n_streams + block * kLanes) + quad);
+        reinterpret_cast<u32x4 *>(encoded + row * n_streams + block * kLanes)[quad] = value;
     }
 
     if (write_summary) {
