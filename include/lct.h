@@ -197,6 +197,36 @@ int32_t lct_allocate_compact(const void *source, int32_t *summaries, int32_t *co
                              int64_t logical_numel, lct_geometry g, int32_t precomputed,
                              hipStream_t stream);
 
+/* ---- replaces, for one tensor, the sequence dispatch.py:33-48 (center +
+ * tables), :294-316 (encoder) and :70-85 (prefix + allocate) that
+ * LCT/codec/encode.py:22-186 runs, in one launch: center samplers, encoders
+ * and one bookkeeping workgroup.  Its outputs equal those of
+ * lct_sample_center (sample_values) -> lct_encode_sampled (side, encoded,
+ * center_out, shifted_decode_out, extra_starts) -> lct_prefix_allocate
+ * (counts, blocks, and the overflow-block list summaries[4*nb .. 5*nb]; the
+ * other summary entries are not written).  With buffer_meta != NULL the
+ * bookkeeping workgroup first applies `frees` (as lct_allocate_compact) and
+ * then makes the reservation of lct_prefix_allocate with buffered = 1 into
+ * descriptor; lct_compact_extra (buffered = 1, or into exact-size private
+ * arrays after the host reads counts) then writes the entries and tails.
+ * control: uint64[control_words >= 64 + nb], one array per stream, zeroed once
+ * when created and never again; epoch: a value != 0 that no earlier call with
+ * this control array used (the launch's cross-workgroup words carry it).
+ * sample_size as lct_sample_center; sample_values may be NULL.  A bounded
+ * device-side wait that gives up marks the tensor incomplete instead of
+ * hanging: counts[3] = 1 and, with a buffer, status 7 and the failure word's
+ * LCT_FAIL_INCOMPLETE bit.  source, side and encoded 16-byte aligned. */
+int32_t lct_encode_fused(const void *source, uint8_t *side, int32_t *encoded,
+                         int64_t sample_size, const int32_t *base_encode,
+                         const int32_t *base_decode, int32_t *center_out,
+                         int32_t *shifted_decode_out, uint16_t *sample_values,
+                         uint8_t *extra_starts, int32_t *summaries, int32_t *blocks,
+                         int32_t *counts, uint64_t *control, int64_t control_words,
+                         uint32_t epoch, int32_t *descriptor, int32_t *buffer_meta,
+                         int32_t max_free_regions, const lct_pending_frees *frees,
+                         int64_t size, int64_t logical_numel, lct_geometry g,
+                         int32_t precomputed, hipStream_t stream);
+
 /* ---- replaces dispatch.py:88-95 (count_bad_streams, the atomic path's
  * totals, LCT/kernels/generic/compaction.py:31-51): adds the number of
  * overflowing streams (extra_starts[s] != 255) to count[0] and their tail

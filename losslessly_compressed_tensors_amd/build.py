@@ -21,6 +21,7 @@ BUILD_DIR = PACKAGE_DIR.parent / "_build" / "lct_hip"
 SOURCES = [
     "tables.hip",
     "encode.hip",
+    "compress.hip",
     "compaction.hip",
     "tensor_buffer.hip",
     "decode.hip",

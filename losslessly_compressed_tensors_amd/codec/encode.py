@@ -1,19 +1,21 @@
 """Compression pipeline: center + tables, encoder, scans/allocation, compaction.
 
-Host sequencing of ``LCT/codec/encode.py:22-218`` on the gfx950 library:
+Host sequencing of ``LCT/codec/encode.py:22-218`` on the gfx950 library.  A
+compress (the center sampled from the input) is two launches:
 
-1. ``lct_sample_center`` samples the center's positions over many
-   workgroups (the sampling half of the reference's table kernel);
-2. ``lct_encode_sampled`` derives the center and the center-shifted tables
-   in every workgroup, then splits fields and writes the fixed payload,
-   per-stream overflow starts and per-block overflow summaries (with a given
-   center: ``lct_shift_tables`` then ``lct_encode``);
-3. ``lct_prefix_allocate`` scans the summaries and, for a shared
-   ``TensorBuffer``, reserves the overflow region on the device;
-4. private storage only: one device->host sync reads the overflow totals so
+1. ``lct_encode_fused``: sampling workgroups publish the center's partial
+   sums; every encoding workgroup reduces them to the center, shifts the
+   tables, splits fields, writes its block's fixed payload and per-stream
+   overflow starts and publishes its block's overflow summary; one
+   bookkeeping workgroup scans the summaries into the block metadata and the
+   overflow-block list and, for a shared ``TensorBuffer``, applies the
+   buffer's deferred frees and reserves the overflow region;
+2. private storage only: one device->host sync reads the overflow totals so
    exact-size lane/start/tail arrays can be allocated (as the reference does);
-5. ``lct_compact_extra`` writes the per-block overflow list and tails.
+3. ``lct_compact_extra`` writes the per-block overflow entries and tails.
 
+With a given center (``lct_shift_tables`` then ``lct_encode``), the
+bookkeeping runs as its own launches after the encoder (``finish_encode``).
 The tensors allocated (and hence ``memory_size()``) match the reference's.
 """
 from __future__ import annotations
@@ -78,19 +80,18 @@ def encode_components(
                   block_symbols=block_symbols, lanes=lanes, steps=steps, fixed_words=fixed_words)
     sample_values = None
     if center is None and logical_numel > 0:
-        # The center's samples are taken by many workgroups; the encoder
-        # reduces their partial sums and shifts the tables itself.  A BF16
+        # One launch samples the center (its partial sums over many
+        # workgroups, which every encoding workgroup reduces to the center),
+        # encodes, and scans the blocks' overflow (for a shared buffer also
+        # reserving the overflow region); the compaction follows.  A BF16
         # source's sampled values are kept for later fused updates.
         center = torch.empty(1, dtype=torch.int32, device=device)
         sample_size = min(logical_numel, CENTER_SAMPLE_SIZE)
-        partials = torch.empty(2 * _cdiv(sample_size, 64), dtype=torch.int32, device=device)
         if not precomputed:
             sample_values = torch.empty(sample_size, dtype=torch.int16, device=device)
-        dispatch.sample_center(source_values, logical_numel, sample_size, precomputed, partials,
-                               sample_values)
-        dispatch.encode_sampled(source_values, sign_mantissa, encoded, partials, sample_size,
-                                encode_table, decode_table, center, shifted_decode, extra_starts,
-                                summaries, size, **launch)
+        return _encode_fused(source_values, sign_mantissa, encoded, extra_starts, summaries, size,
+                             distribution, buffer, shape, encode_table, decode_table, center,
+                             shifted_decode, sample_size, sample_values, launch)
     else:
         if center is None:
             center = torch.zeros(1, dtype=torch.int32, device=device)   # empty: tables.py:47
@@ -105,6 +106,77 @@ def encode_components(
                          distribution, buffer, shape, precomputed=precomputed, center=center,
                          shifted_decode=shifted_decode, logical_numel=logical_numel,
                          sample_values=sample_values)
+
+
+def _encode_fused(source_values, sign_mantissa, encoded, extra_starts, summaries, size,
+                  distribution, buffer, shape, encode_table, decode_table, center,
+                  shifted_decode, sample_size, sample_values, launch) -> CompressedTensor:
+    """``lct_encode_fused`` then ``lct_compact_extra``: the buffered form takes
+    the buffer's deferred frees into the launch and needs no host sync; the
+    private form reads the overflow totals once (as the reference does) to
+    allocate exact-size lane/start/tail arrays."""
+    device = encoded.device
+    stream_geometry = geometry(distribution)
+    block_symbols, lanes, steps, _ = stream_geometry
+    blocks = _cdiv(size, block_symbols)
+    precomputed = launch["precomputed"]
+    logical_numel = launch["logical_numel"]
+    counts = torch.empty(4, dtype=torch.int32, device=device)
+    blocks_out = torch.empty(3 * blocks, dtype=torch.int32, device=device)
+    fused = dict(size=size, **launch)
+    compaction = dict(precomputed=precomputed, logical_numel=logical_numel,
+                      block_symbols=block_symbols, lanes=lanes, steps=steps,
+                      extra_starts=extra_starts, summaries=summaries)
+    if buffer is not None:
+        descriptor = torch.empty(4, dtype=torch.int32, device=device)
+        frees = buffer._take_frees()
+        try:
+            dispatch.encode_fused(source_values, sign_mantissa, encoded, sample_size,
+                                  encode_table, decode_table, center, shifted_decode,
+                                  sample_values, extra_starts, summaries, blocks_out, counts,
+                                  buffer=buffer, descriptor=descriptor, frees=frees, **fused)
+        except BaseException:
+            # Nothing was launched: the deferred frees wait for the next call.
+            buffer._restore_frees(frees)
+            raise
+        arena = buffer.data
+        storage = FallbackStorage(tail=arena, count=counts[:1], lanes=arena, starts=arena,
+                                  blocks=blocks_out, descriptor=descriptor,
+                                  allocation=descriptor)
+        dispatch.compact_extra(source_values, storage, blocks, size, buffered=True, **compaction)
+    else:
+        dispatch.encode_fused(source_values, sign_mantissa, encoded, sample_size, encode_table,
+                              decode_table, center, shifted_decode, sample_values, extra_starts,
+                              summaries, blocks_out, counts, **fused)
+        count, tail_bytes, _, incomplete = (int(v) for v in counts.tolist())
+        if incomplete:
+            raise RuntimeError(
+                "compress: a device-side wait of the encoder gave up (a block's summary or "
+                "the center's samples did not arrive); the tensor was not stored")
+        storage = FallbackStorage(
+            tail=torch.empty(tail_bytes, dtype=torch.uint8, device=device),
+            count=counts[:1],
+            lanes=torch.empty(count, dtype=torch.uint8, device=device),
+            starts=torch.empty(count, dtype=torch.uint8, device=device),
+            blocks=blocks_out, allocation=counts[2:3], base=0)
+        if count > 0:
+            dispatch.compact_extra(source_values, storage, blocks, size, buffered=False,
+                                   **compaction)
+    buffered = buffer is not None
+    return CompressedTensor(
+        encoded, size, sign_mantissa,
+        fallback_starts=None if buffered else storage.starts,
+        fallback_lanes=None if buffered else storage.lanes,
+        fallback_blocks=storage.blocks,
+        fallback_buffer=storage.tail,
+        fallback_descriptor=storage.descriptor,
+        buffer=buffer,
+        fallback_count=counts[:1],
+        fallback_used=counts[1:2],
+        distribution=distribution, center=center, decode_table=shifted_decode,
+        shape=shape, layout=StorageLayout.COMPRESSED, stream_geometry=stream_geometry,
+        sample_values=sample_values,
+    )
 
 
 def finish_encode(

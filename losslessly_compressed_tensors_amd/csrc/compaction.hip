@@ -8,320 +8,13 @@
 // at entries [first, first+count), their exponent tails int8(e-127) for steps
 // start..S-1 concatenated from byte_base, and blocks[3*nb] = {count, first,
 // byte_base} so every reader walks the list one block at a time.
-#include "allocator.h"
 #include "overflow_walk.h"
+#include "reserve.h"
 
 namespace lct {
 namespace {
 
-constexpr int kPrefixPer = 16;                       // blocks per thread per pass
-constexpr int kPrefixPass = kPrefixPer * kLanes;     // 4096 blocks per pass
 constexpr int kCompactGrid = 2048;                   // workgroups walking the overflow-block list
-
-// Exclusive prefix sums of three values over the 256 threads of a block, with
-// their totals; one exchange through `scratch` (3 * kWavesPerBlock ints).
-// Contains barriers.
-__device__ __forceinline__ void block_exclusive_scan3(const int32_t (&v)[3], int32_t *scratch,
-                                                      int32_t (&before)[3],
-                                                      int32_t (&total)[3]) {
-    const int wave = threadIdx.x / kWave;
-    int32_t inclusive[3];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        inclusive[k] = wave_inclusive_scan(v[k]);
-        if (wave_lane() == kWave - 1) scratch[k * kWavesPerBlock + wave] = inclusive[k];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        int32_t prior = 0, sum = 0;
-#pragma unroll
-        for (int w = 0; w < kWavesPerBlock; ++w) {
-            const int32_t s = scratch[k * kWavesPerBlock + w];
-            prior += w < wave ? s : 0;
-            sum += s;
-        }
-        before[k] = prior + inclusive[k] - v[k];
-        total[k] = sum;
-    }
-    __syncthreads();
-}
-
-// summaries layout (int32[5*nb + 1]): per-block overflow counts | tail bytes |
-// exclusive count scan | exclusive byte scan | list of blocks with overflow |
-// list length.  The encoder writes the first two; this kernel the rest.
-// Each pass covers 4096 blocks, 16 consecutive ones per thread, loaded and
-// stored as four 16-byte buffer accesses per array (blocks past the end read
-// as 0 and are not written); running totals carry from pass to pass, so any
-// block count gives the same deterministic layout (entries in block order,
-// lanes ascending within a block).  A buffered call requests the arena's lock
-// and reads its free list while the first pass's loads are in flight, and
-// before scanning, so those latencies overlap.
-//
-// The reservation is a policy: `reserve.begin(scratch)` runs once the first
-// pass's loads are issued (a buffered call takes the arena lock and reads the
-// free list there, overlapping those latencies), `reserve.finish(request,
-// scratch)` at the end.  kWriteScans = false leaves the exclusive scans of
-// summaries[2nb, 4nb) unwritten (the block metadata holds the same values).
-// Workgroup-wide; contains barriers.
-template <bool kWriteScans, class Reserve>
-__device__ __forceinline__ void scan_allocate(int32_t *__restrict__ summaries,
-                                              int32_t *__restrict__ counts,
-                                              int32_t *__restrict__ blocks, int32_t n_blocks,
-                                              Reserve &reserve) {
-    __shared__ int32_t scratch[3 * kWavesPerBlock];
-    const int t = threadIdx.x;
-    const int64_t nb = n_blocks;
-    const uint32_t bytes = static_cast<uint32_t>(n_blocks) * 4u;
-    const __amdgpu_buffer_rsrc_t count_in = make_rsrc(summaries, bytes);
-    const __amdgpu_buffer_rsrc_t bytes_in = make_rsrc(summaries + nb, bytes);
-    const __amdgpu_buffer_rsrc_t first_out = make_rsrc(summaries + 2 * nb, bytes);
-    const __amdgpu_buffer_rsrc_t base_out = make_rsrc(summaries + 3 * nb, bytes);
-    const __amdgpu_buffer_rsrc_t meta_count = make_rsrc(blocks, bytes);
-    const __amdgpu_buffer_rsrc_t meta_first = make_rsrc(blocks + nb, bytes);
-    const __amdgpu_buffer_rsrc_t meta_base = make_rsrc(blocks + 2 * nb, bytes);
-    int32_t *list = summaries + 4 * nb;
-    int32_t carry[3] = {0, 0, 0};   // entries, tail bytes, listed blocks
-    // A thread whose 16 blocks all exist moves them with 16-byte accesses; the
-    // one that straddles the end (and those past it) use 4-byte accesses,
-    // which the range check reads as 0 or drops one by one.
-    int32_t c[kPrefixPer], v[kPrefixPer];
-    auto load_pass = [&](int base) {
-        const int32_t first_block = base + t * kPrefixPer;
-        const uint32_t off = static_cast<uint32_t>(first_block) * 4u;
-        if (first_block + kPrefixPer <= n_blocks) {
-#pragma unroll
-            for (int q = 0; q < kPrefixPer / 4; ++q) {
-                const auto cq = __builtin_amdgcn_raw_buffer_load_b128(count_in, off + 16 * q, 0, 0);
-                const auto vq = __builtin_amdgcn_raw_buffer_load_b128(bytes_in, off + 16 * q, 0, 0);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    c[4 * q + k] = static_cast<int32_t>(cq[k]);
-                    v[4 * q + k] = static_cast<int32_t>(vq[k]);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < kPrefixPer; ++k) {
-                c[k] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(count_in, off + 4 * k, 0, 0));
-                v[k] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(bytes_in, off + 4 * k, 0, 0));
-            }
-        }
-    };
-    // The first pass's loads are issued before the arena lock is requested,
-    // so their latency and the lock's overlap.
-    load_pass(0);
-    reserve.begin(scratch);
-    for (int base = 0; base < n_blocks; base += kPrefixPass) {
-        const int32_t first_block = base + t * kPrefixPer;
-        const uint32_t off = static_cast<uint32_t>(first_block) * 4u;
-        const bool whole = first_block + kPrefixPer <= n_blocks;
-        if (base > 0) load_pass(base);
-        int32_t run[3] = {0, 0, 0};
-#pragma unroll
-        for (int k = 0; k < kPrefixPer; ++k) {
-            run[0] += c[k];
-            run[1] += v[k];
-            run[2] += c[k] > 0 ? 1 : 0;
-        }
-        int32_t before[3], total[3];
-        block_exclusive_scan3(run, scratch, before, total);
-        int32_t count_before = carry[0] + before[0];
-        int32_t byte_before = carry[1] + before[1];
-        int32_t list_before = carry[2] + before[2];
-        int32_t firsts[kPrefixPer], bases[kPrefixPer];
-#pragma unroll
-        for (int k = 0; k < kPrefixPer; ++k) {
-            firsts[k] = count_before;
-            bases[k] = byte_before;
-            if (c[k] > 0) list[list_before++] = first_block + k;
-            count_before += c[k];
-            byte_before += v[k];
-        }
-        if (!whole) {
-#pragma unroll
-            for (int k = 0; k < kPrefixPer; ++k) {
-                const uint32_t o = off + 4 * k;
-                if (kWriteScans) {
-                    __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(firsts[k]), first_out, o, 0, 0);
-                    __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(bases[k]), base_out, o, 0, 0);
-                }
-                __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(c[k]), meta_count, o, 0, 0);
-                __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(firsts[k]), meta_first, o, 0, 0);
-                __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(bases[k]), meta_base, o, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int q = 0; whole && q < kPrefixPer / 4; ++q) {
-            using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
-            const u32x4 fq = {static_cast<uint32_t>(firsts[4 * q]),
-                              static_cast<uint32_t>(firsts[4 * q + 1]),
-                              static_cast<uint32_t>(firsts[4 * q + 2]),
-                              static_cast<uint32_t>(firsts[4 * q + 3])};
-            const u32x4 bq = {static_cast<uint32_t>(bases[4 * q]),
-                              static_cast<uint32_t>(bases[4 * q + 1]),
-                              static_cast<uint32_t>(bases[4 * q + 2]),
-                              static_cast<uint32_t>(bases[4 * q + 3])};
-            const u32x4 cq = {static_cast<uint32_t>(c[4 * q]), static_cast<uint32_t>(c[4 * q + 1]),
-                              static_cast<uint32_t>(c[4 * q + 2]),
-                              static_cast<uint32_t>(c[4 * q + 3])};
-            if (kWriteScans) {
-                __builtin_amdgcn_raw_buffer_store_b128(fq, first_out, off + 16 * q, 0, 0);
-                __builtin_amdgcn_raw_buffer_store_b128(bq, base_out, off + 16 * q, 0, 0);
-            }
-            __builtin_amdgcn_raw_buffer_store_b128(cq, meta_count, off + 16 * q, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(fq, meta_first, off + 16 * q, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(bq, meta_base, off + 16 * q, 0, 0);
-        }
-#pragma unroll
-        for (int k = 0; k < 3; ++k) carry[k] += total[k];
-    }
-    if (t == 0) {
-        counts[0] = carry[0];
-        counts[1] = carry[1];
-        counts[2] = 0;
-        counts[3] = 0;
-        summaries[5 * nb] = carry[2];
-    }
-    // Two metadata bytes per overflowing stream: lane, then start step.
-    reserve.finish(carry[1] + 2 * carry[0], scratch);
-}
-
-// lct_prefix_allocate's reservation: the lock, then the free list in
-// registers (allocator_begin / allocator_finish); nothing when not buffered.
-struct RegisterReserve {
-    AllocatorMeta meta;
-    int32_t *descriptor;
-    int32_t *flag;   // one LDS int
-    bool active;
-    AllocatorSnapshot snap;
-
-    __device__ void begin(int32_t *) {
-        if (active) allocator_begin(meta, snap, flag);
-    }
-    __device__ void finish(int32_t request, int32_t *scratch) {
-        if (active) allocator_finish(meta, snap, request, descriptor, scratch, true);
-    }
-};
-
-// lct_allocate_compact's reservation (workgroup 0).  begin: thread 0 reads
-// the lock word while the first pass's loads and the pending descriptors'
-// values are in flight; then, with the lock seen free at version v, thread 0
-// takes it (v -> v + 1) while every thread reads the free list into LDS with
-// agent-scope loads: the copy is current exactly when that compare-and-swap
-// succeeds (otherwise the lock is waited for and the list read again).  The
-// deferred frees then run on the LDS copy, in order.  finish: the first-fit
-// reservation on the LDS copy, the list written back, the descriptor, and one
-// agent-scope release that publishes every write of the workgroup before the
-// lock goes to v + 2.  Two memory round trips before the scan, where the
-// register path takes three (lock, fence, list) plus one per free.
-struct LdsReserve {
-    AllocatorMeta meta;
-    int32_t *descriptor;
-    lct_pending_frees frees;
-    int32_t *list;   // LDS int32[2 * regions]: starts, then sizes
-    LdsFreeList f;
-    int32_t held;
-
-    __device__ void read_list(int32_t *shared) {
-        const int32_t regions = meta.regions;
-        for (int32_t i = threadIdx.x; i < regions; i += kLanes) {
-            list[i] = coherent_load(meta.starts + i);
-            list[regions + i] = coherent_load(meta.sizes + i);
-        }
-        if (threadIdx.x == 0) {
-            shared[2] = coherent_load(meta.count);
-            shared[3] = coherent_load(meta.generation);
-        }
-    }
-
-    __device__ void begin(int32_t *scratch) {
-        __shared__ int32_t shared[4];   // seen version, held version, count, generation
-        __shared__ int32_t pending[LCT_MAX_PENDING_FREES][4];
-        const int t = threadIdx.x;
-        if (t == 0) shared[0] = coherent_load(meta.lock);
-#pragma unroll
-        for (int j = 0; j < LCT_MAX_PENDING_FREES; ++j)
-            if (j < frees.count && t < 4) pending[j][t] = frees.descriptor[j][t];
-        __syncthreads();
-        const int32_t seen = shared[0];
-        if ((seen & 1) == 0) {
-            if (t == 0) {
-                int32_t expected = seen;
-                shared[1] = __hip_atomic_compare_exchange_strong(
-                                meta.lock, &expected, seen + 1, __ATOMIC_ACQUIRE,
-                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                ? seen
-                                : -1;
-            }
-            read_list(shared);
-        } else if (t == 0) {
-            shared[1] = -1;
-        }
-        __syncthreads();
-        held = shared[1];
-        if (held < 0) {
-            if (t == 0) shared[1] = take_lock_thread0(meta.lock, -1, meta.spins);
-            __syncthreads();
-            held = shared[1];
-            if (held >= 0) read_list(shared);
-            __syncthreads();
-        }
-        f = LdsFreeList{list, list + meta.regions, meta.regions, shared[2], shared[3]};
-        if (held < 0) return;
-#pragma unroll
-        for (int j = 0; j < LCT_MAX_PENDING_FREES; ++j) {
-            if (j < frees.count) {
-                const int32_t d[4] = {pending[j][0], pending[j][1], pending[j][2], pending[j][3]};
-                if (lds_free(f, d, scratch) == kStatusOk) {
-                    if (t == 0) {
-                        frees.descriptor[j][2] = kStatusFreed;
-                        // A later copy of the same descriptor now reads as
-                        // freed, so a second free of it is rejected, as the
-                        // immediate free would reject it (status 4).
-#pragma unroll
-                        for (int k = j + 1; k < LCT_MAX_PENDING_FREES; ++k)
-                            if (k < frees.count && frees.descriptor[k] == frees.descriptor[j])
-                                pending[k][2] = kStatusFreed;
-                    }
-                    __syncthreads();
-                }
-            }
-        }
-    }
-
-    int32_t status;   // the reservation's status (uniform after finish)
-
-    __device__ void finish(int32_t request, int32_t *scratch) {
-        const int t = threadIdx.x;
-        if (held < 0) {
-            status = kStatusLock;
-            if (t == 0) {
-                descriptor[0] = -1;
-                descriptor[1] = 0;
-                descriptor[2] = kStatusLock;
-                descriptor[3] = -1;
-            }
-        } else {
-            int32_t out[3];
-            lds_reserve(f, request, scratch, out);
-            lds_write_back(f, meta);
-            status = out[2];
-            if (t == 0) {
-                descriptor[0] = out[0];
-                descriptor[1] = out[1];
-                descriptor[2] = out[2];
-                descriptor[3] = f.generation;
-            }
-        }
-        if (t == 0 && failure_bits(status, request) != 0)
-            record_failure(meta, failure_bits(status, request));
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __syncthreads();
-        if (held >= 0 && t == 0)
-            __hip_atomic_store(meta.lock, held + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-};
 
 __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     int32_t *__restrict__ summaries, int32_t *__restrict__ counts,
@@ -331,7 +24,8 @@ __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     __shared__ int32_t flag;
     RegisterReserve reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins), descriptor,
                             &flag, buffered != 0, {}};
-    scan_allocate<true>(summaries, counts, blocks, n_blocks, reserve);
+    SummaryLoads source(summaries, n_blocks);
+    scan_allocate<true, true>(source, summaries, counts, blocks, n_blocks, reserve);
 }
 
 // One codec block's overflow entries and tails (compaction.py:137-228), in
@@ -434,27 +128,34 @@ __global__ __launch_bounds__(kLanes) void compact_extra_kernel(
     int S, int precomputed, int buffered) {
     __shared__ int32_t scratch[kWavesPerBlock];
     __shared__ int32_t entry_offset[kLanes], entry_start[kLanes], entry_lane[kLanes];
-    int64_t lane_off = 0, start_off = 0, tail_off = base;
-    if (buffered) {
-        if (descriptor[2] != kStatusOk) return;   // failed allocation: write nothing
-        const int64_t arena = descriptor[0];
-        const int64_t total = count_total[0];
-        lane_off = arena;
-        start_off = arena + total;
-        tail_off = arena + 2 * total;
-    }
     // Without summaries (block metadata from compact_bad_streams_kernel) every
     // block is visited; the entries it rewrites are the ones already there.
     const int32_t *list = summaries != nullptr ? summaries + 4 * n_blocks : nullptr;
-    const int64_t listed = summaries != nullptr ? summaries[5 * n_blocks] : n_blocks;
-    for (int64_t i = blockIdx.x; i < listed; i += gridDim.x) {
-        const int64_t block = list != nullptr ? list[i] : i;
+    // The reservation, the list's length and this workgroup's first list entry
+    // are loaded together -- the entry speculatively (blockIdx.x < n_blocks by
+    // the grid's size, and the list has n_blocks entries), used only if it is
+    // listed -- so one memory round trip precedes the first block's extra
+    // starts instead of three.
+    const int32_t status = buffered ? descriptor[2] : kStatusOk;
+    const int64_t arena = buffered ? descriptor[0] : 0;
+    const int64_t total = buffered ? count_total[0] : 0;
+    const int64_t listed = list != nullptr ? summaries[5 * n_blocks] : n_blocks;
+    int64_t i = blockIdx.x;
+    int64_t block = list != nullptr ? list[i] : i;
+    if (status != kStatusOk) return;   // failed allocation: write nothing
+    const int64_t lane_off = buffered ? arena : 0;
+    const int64_t start_off = buffered ? arena + total : 0;
+    const int64_t tail_off = buffered ? arena + 2 * total : base;
+    for (; i < listed; i += gridDim.x) {
+        if (i != blockIdx.x) block = list != nullptr ? list[i] : i;
         if (list == nullptr && blocks[block] == 0) continue;   // uniform
+        // The block's first 256 tail bytes are read with the ranking.
         const BlockEntries e = rank_block(extra_starts, block, S, scratch, entry_offset,
-                                          entry_start, entry_lane);
+                                          entry_start, entry_lane, source, logical_numel,
+                                          precomputed);
         write_block(source, lanes, starts, tail, lane_off, start_off, tail_off,
                     blocks[n_blocks + block], blocks[2 * n_blocks + block], e, block,
-                    logical_numel, S, precomputed, entry_offset, entry_start, entry_lane);
+                    logical_numel, S, precomputed, entry_offset, entry_start, entry_lane, true);
     }
 }
 
@@ -504,7 +205,8 @@ __global__ __launch_bounds__(kLanes) void allocate_compact_kernel(
     if (blockIdx.x == 0) {
         LdsReserve reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins), descriptor,
                            frees, free_list, {}, -1, kStatusOk};
-        scan_allocate<false>(summaries, counts, blocks, n_blocks, reserve);
+        SummaryLoads loads(summaries, n_blocks);
+        scan_allocate<false, false>(loads, summaries, counts, blocks, n_blocks, reserve);
         // finish() released every write of the workgroup at agent scope.
         if (threadIdx.x == 0) {
             const uint64_t before = __hip_atomic_exchange(ready, epoch, __ATOMIC_RELAXED,

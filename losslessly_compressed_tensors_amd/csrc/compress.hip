@@ -1,0 +1,181 @@
+// Fused compress: center sampling, field split + encoder, and the overflow
+// bookkeeping (block scans, overflow-block list, block metadata and, for a
+// shared TensorBuffer, the arena reservation after the buffer's deferred
+// frees) in one launch.  Only the compaction of the overflowing streams
+// (lct_compact_extra) stays a launch of its own: it reads the extra starts
+// that other workgroups wrote, which a kernel boundary makes visible.
+//
+// Replaces, for one tensor, the sequence LCT/kernels/dispatch.py:33-48
+// (center + tables), :294-316 (encoder) and :70-85 (prefix + allocate) that
+// LCT/codec/encode.py:22-186 runs; the results are those of
+// lct_sample_center -> lct_encode_sampled -> lct_prefix_allocate (or, with a
+// buffer, the reservation of lct_allocate_compact), value for value.
+//
+// Workgroups, in dispatch order:
+//  * 0: bookkeeping.  With a buffer it takes the arena lock, reads the free
+//    list into LDS and applies the deferred frees at once, then polls the
+//    encoders' per-block summaries, scans them and reserves the tensor's
+//    overflow region (request = tail bytes + 2 x entries), so only the last
+//    summary's arrival, the scan and the reservation follow the last block;
+//  * 1..G: center samplers (G = ceil(samples / 64), one wave each), which
+//    publish their partial sums and never wait;
+//  * G+1..G+nb: encoders of codec blocks 0..nb-1.  Each polls the G partial
+//    sums (its first input chunk in flight meanwhile), encodes its block as
+//    lct_encode_sampled does and publishes its overflow count and tail bytes.
+// Every wait is for workgroups dispatched before the waiter that themselves
+// wait only for earlier ones (the samplers for nothing), and every poll is
+// bounded; a summary or partial sum that does not arrive within the bound
+// marks the tensor incomplete (counts[3] = 1; with a buffer, status 7 and the
+// buffer's failure word) instead of hanging.
+//
+// Cross-workgroup values travel in a control array of 64-bit words tagged with
+// the call's epoch (lct_device.h), one array per stream, never cleared: a word
+// is current exactly when its tag is this call's epoch.
+#include "encode_core.h"
+#include "reserve.h"
+
+namespace lct {
+namespace {
+
+__global__ __launch_bounds__(kLanes) void compress_kernel(
+    const void *__restrict__ source, uint8_t *__restrict__ side, int32_t *__restrict__ encoded,
+    const int32_t *__restrict__ base_encode, const int32_t *__restrict__ base_decode,
+    int32_t *__restrict__ center_out, int32_t *__restrict__ shifted_decode_out,
+    uint16_t *__restrict__ sample_values, int64_t sample_size, int32_t n_groups,
+    uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
+    int32_t *__restrict__ blocks, int32_t *__restrict__ counts, uint64_t *__restrict__ control,
+    uint32_t epoch, int32_t *__restrict__ descriptor, int32_t *__restrict__ buffer_meta,
+    int32_t max_free_regions, lct_pending_frees frees, int32_t n_blocks, int64_t logical_numel,
+    int S, int W, int precomputed, int32_t lock_spins, int32_t polls) {
+    extern __shared__ uint32_t stage[];   // (W + 2) rows x 256 lanes, or the free list
+    __shared__ uint2 table[256];
+    __shared__ __attribute__((aligned(16))) uint8_t slices[kWavesPerBlock * kSliceBytes];
+    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ int32_t shared[2];
+    const int64_t group = blockIdx.x;
+
+    if (group == 0) {
+        PolledSummaries polled{control, epoch, n_blocks, polls, false};
+        if (buffer_meta != nullptr) {
+            LdsReserve reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins),
+                               descriptor, frees, reinterpret_cast<int32_t *>(stage), {}, -1,
+                               kStatusOk};
+            scan_allocate<false, false>(polled, summaries, counts, blocks, n_blocks, reserve);
+        } else {
+            NoReserve reserve;
+            scan_allocate<false, false>(polled, summaries, counts, blocks, n_blocks, reserve);
+        }
+        return;
+    }
+
+    if (group <= n_groups) {
+        // Samples (group - 1) * 64 + lane (tables.py:15-49): the kept
+        // exponents' sum and count; a BF16 source's sampled bits also go to
+        // sample_values.
+        if (threadIdx.x >= kWave) return;
+        const int t = threadIdx.x;
+        const int64_t i = (group - 1) * kSampleGroup + t;
+        const bool active = i < sample_size;
+        const int shift = __builtin_ctzll(static_cast<uint64_t>(sample_size));
+        int32_t exp = -127;
+        if (active) {
+            const int64_t pos = sample_position(i, logical_numel, sample_size, shift);
+            if (precomputed) {
+                exp = static_cast<int32_t>(static_cast<const uint8_t *>(source)[pos]) - 127;
+            } else {
+                const uint32_t bits = static_cast<const uint16_t *>(source)[pos];
+                exp = static_cast<int32_t>((bits >> 7) & 0xFFu) - 127;
+                if (sample_values != nullptr) sample_values[i] = static_cast<uint16_t>(bits);
+            }
+        }
+        const bool keep = active && exp >= -120;
+        const int32_t sum = wave_sum(keep ? exp : 0);      // |sum| <= 64 * 128
+        const int32_t kept = wave_sum(keep ? 1 : 0);
+        if (t == 0) {
+            const uint32_t value = (static_cast<uint32_t>(static_cast<uint16_t>(sum)) << 16)
+                                   | static_cast<uint32_t>(kept);
+            control_store(control + (group - 1), tagged_word(epoch, value));
+        }
+        return;
+    }
+
+    const int64_t block = group - 1 - n_groups;
+    const TableSource tables{nullptr, nullptr, n_groups, base_encode, base_decode, center_out,
+                             shifted_decode_out, control, epoch, polls};
+    const EncodeLds lds{stage, table, slices, scratch, shared};
+    const BlockSummary s = encode_codec_block(source, side, encoded, tables, extra_starts, block,
+                                              n_blocks, logical_numel, S, W, precomputed, true,
+                                              lds);
+    if (threadIdx.x == 0) {
+        // count <= 256 and bytes <= 256 * 256 fit 9 and 17 bits.
+        const uint32_t value = s.failed ? (kFailedBlock << 17)
+                                        : (static_cast<uint32_t>(s.count) << 17)
+                                              | static_cast<uint32_t>(s.bytes);
+        control_store(control + kControlPartials + block, tagged_word(epoch, value));
+    }
+}
+
+}  // namespace
+}  // namespace lct
+
+using namespace lct;
+
+extern "C" int32_t lct_encode_fused(
+    const void *source, uint8_t *side, int32_t *encoded, int64_t sample_size,
+    const int32_t *base_encode, const int32_t *base_decode, int32_t *center_out,
+    int32_t *shifted_decode_out, uint16_t *sample_values, uint8_t *extra_starts,
+    int32_t *summaries, int32_t *blocks, int32_t *counts, uint64_t *control,
+    int64_t control_words, uint32_t epoch, int32_t *descriptor, int32_t *buffer_meta,
+    int32_t max_free_regions, const lct_pending_frees *frees, int64_t size,
+    int64_t logical_numel, lct_geometry g, int32_t precomputed, hipStream_t stream) {
+    if (!source || !side || !encoded || !base_encode || !base_decode || !center_out
+        || !shifted_decode_out || !extra_starts || !summaries || !blocks || !counts || !control)
+        return LCT_E_NULL;
+    const bool buffered = buffer_meta != nullptr;
+    if (buffered && !descriptor) return LCT_E_NULL;
+    if (!geometry_ok(g)) return LCT_E_GEOMETRY;
+    if (logical_numel <= 0 || size <= 0 || size % g.block_symbols != 0
+        || logical_numel > size || logical_numel <= size - g.block_symbols)
+        return LCT_E_SIZE;
+    const int64_t n_blocks = size / g.block_symbols;
+    if (n_blocks > kMaxBlocks) return LCT_E_SIZE;
+    if (sample_size <= 0 || sample_size > kMaxSamples || sample_size > logical_numel)
+        return LCT_E_SIZE;
+    if (sample_size != logical_numel && (sample_size & (sample_size - 1)) != 0)
+        return LCT_E_ARG;
+    if (control_words < kControlPartials + n_blocks) return LCT_E_SIZE;
+    // Epoch 0 would match a control array's initial zeros.
+    if (epoch == 0) return LCT_E_ARG;
+    if (((reinterpret_cast<uintptr_t>(encoded) | reinterpret_cast<uintptr_t>(source)
+          | reinterpret_cast<uintptr_t>(side)) & 15) != 0
+        || (reinterpret_cast<uintptr_t>(control) & 7) != 0)
+        return LCT_E_ARG;
+    lct_pending_frees pending{};
+    if (buffered) {
+        if (max_free_regions <= 0 || max_free_regions > 4096
+            || (max_free_regions & (max_free_regions - 1)) != 0)
+            return LCT_E_ARG;
+        if (frees != nullptr) {
+            if (frees->count < 0 || frees->count > LCT_MAX_PENDING_FREES) return LCT_E_ARG;
+            for (int i = 0; i < frees->count; ++i)
+                if (frees->descriptor[i] == nullptr) return LCT_E_NULL;
+            pending = *frees;
+        }
+    }
+    const int32_t n_groups = sample_groups(sample_size);
+    // The encoders' stage, or workgroup 0's LDS copy of the free list.
+    size_t lds = static_cast<size_t>(g.fixed_words + 2) * kLanes * 4;
+    if (buffered && static_cast<size_t>(max_free_regions) * 8 > lds)
+        lds = static_cast<size_t>(max_free_regions) * 8;
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&compress_kernel), lds))
+        return static_cast<int32_t>(e);
+    const uint32_t grid = 1u + static_cast<uint32_t>(n_groups) + static_cast<uint32_t>(n_blocks);
+    hipLaunchKernelGGL(compress_kernel, dim3(grid), dim3(kLanes), lds, stream, source, side,
+                       encoded, base_encode, base_decode, center_out, shifted_decode_out,
+                       precomputed ? nullptr : sample_values, sample_size, n_groups,
+                       extra_starts, summaries, blocks, counts, control, epoch,
+                       buffered ? descriptor : nullptr, buffer_meta, max_free_regions, pending,
+                       static_cast<int32_t>(n_blocks), logical_numel, g.steps, g.fixed_words,
+                       precomputed, lock_spins(), ready_polls());
+    return static_cast<int32_t>(hipGetLastError());
+}

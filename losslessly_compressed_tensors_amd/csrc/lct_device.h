@@ -194,6 +194,67 @@ __device__ __forceinline__ void center_from_partials(const int32_t *__restrict__
     }
 }
 
+// The fused compress's control array (one per stream, reused by every call on
+// it): 64-bit words that carry the call's 32-bit epoch in their high half, so a
+// word an earlier call wrote never reads as current and no call has to clear
+// the array.  Words [0, 64) are the center samplers' partial sums (low half:
+// the kept exponents' sum as int16 in bits 16..31, their count in bits 0..15);
+// words [64, 64 + nb) the encoders' per-block overflow summaries (low half:
+// count << 17 | tail bytes; a count field of kFailedBlock marks a block that
+// could not read its center).  Every word is written with one agent-scope
+// atomic store and read with agent-scope atomic loads, so it is read whole and
+// coherently across the XCDs.
+constexpr int kControlPartials = 64;
+constexpr uint32_t kFailedBlock = 0x1FFu;
+
+__device__ __forceinline__ uint64_t tagged_word(uint32_t epoch, uint32_t value) {
+    return (static_cast<uint64_t>(epoch) << 32) | value;
+}
+
+__device__ __forceinline__ bool tagged_with(uint64_t word, uint32_t epoch) {
+    return static_cast<uint32_t>(word >> 32) == epoch;
+}
+
+__device__ __forceinline__ uint64_t control_load(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void control_store(uint64_t *p, uint64_t value) {
+    __hip_atomic_store(p, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The center from the partial sums the sampling workgroups of the same launch
+// publish in control[0, n_groups), computed by wave 0 of the block: lane g
+// polls word g until it carries `epoch` (at most `polls` times).  Writes the
+// center to shared[0] and whether some word did not arrive to shared[1]
+// (center 0 then), visible to the block after its next barrier.
+__device__ __forceinline__ void center_from_control(const uint64_t *__restrict__ control,
+                                                    int32_t n_groups, uint32_t epoch,
+                                                    int32_t polls, int32_t *shared) {
+    if (threadIdx.x < kWave) {
+        const int t = threadIdx.x;
+        int32_t sum = 0, kept = 0;
+        bool arrived = true;
+        if (t < n_groups) {
+            uint64_t word = control_load(control + t);
+            for (int i = 0; !tagged_with(word, epoch) && i < polls; ++i) {
+                __builtin_amdgcn_s_sleep(2);
+                word = control_load(control + t);
+            }
+            arrived = tagged_with(word, epoch);
+            sum = static_cast<int16_t>(static_cast<uint16_t>(word >> 16));
+            kept = static_cast<int32_t>(word & 0xFFFFu);
+        }
+        const bool missing = __ballot(!arrived) != 0;
+        sum = wave_sum(sum);
+        kept = wave_sum(kept);
+        if (t == 0) {
+            shared[0] = missing ? 0 : center_of(sum, kept);
+            shared[1] = missing ? 1 : 0;
+        }
+    }
+}
+
 // Number of sampling groups for sample_size samples.
 __host__ __device__ constexpr int32_t sample_groups(int64_t sample_size) {
     return static_cast<int32_t>((sample_size + kSampleGroup - 1) / kSampleGroup);

@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import itertools
 import os
+import threading
 from dataclasses import dataclass
 
 import torch
@@ -203,6 +204,73 @@ def allocate_compact(source, summaries, counts, descriptor, buffer, blocks_out, 
              _ptr(descriptor), _ptr(buffer.storage), int(buffer.max_free_regions),
              _ptr(buffer.data), _ptr(blocks_out), _ptr(extra_starts), hip.ctypes.byref(pending),
              _ready_pointer(summaries, n_blocks), next(_EPOCHS), int(size), int(logical_numel),
+             geometry, int(bool(precomputed)), _stream(source))
+
+
+# lct_encode_fused's control arrays: one per (device, stream), zeroed when
+# created and never cleared again (each call's words carry its epoch), grown
+# when a tensor has more codec blocks than the array holds words for.
+CONTROL_PARTIALS = 64
+_control_arrays: dict = {}
+_control_lock = threading.Lock()
+
+# Epochs of lct_encode_fused: unique within the process (a 32-bit counter from
+# a random start, 0 skipped), so no word an earlier call left in a control
+# array matches a later call's epoch before 2^32 calls.
+_FUSED_EPOCHS = itertools.count(int.from_bytes(os.urandom(4), "little"))
+
+
+def _next_fused_epoch() -> int:
+    while True:
+        epoch = next(_FUSED_EPOCHS) & 0xFFFFFFFF
+        if epoch != 0:
+            return epoch
+
+
+def control_array(device: torch.device, n_blocks: int) -> torch.Tensor:
+    """The current stream's control array on ``device`` with room for
+    ``n_blocks`` codec blocks (int64 words, reinterpreted as uint64 by the
+    kernel).  A new or larger array is zeroed on the current stream, so the
+    launch that follows on that stream sees it zeroed."""
+    stream = torch._C._cuda_getCurrentRawStream(device.index)
+    key = (device.index, stream)
+    need = CONTROL_PARTIALS + n_blocks
+    with _control_lock:
+        array = _control_arrays.get(key)
+        if array is None or array.numel() < need:
+            size = max(need, CONTROL_PARTIALS + 4096)
+            if array is not None:
+                size = max(size, 2 * array.numel())
+            array = torch.zeros(size, dtype=torch.int64, device=device)
+            _control_arrays[key] = array
+        return array
+
+
+def encode_fused(source, side, encoded, sample_size, encode_table, decode_table, center,
+                 shifted_decode, sample_values, extra_starts, summaries, blocks_out, counts,
+                 size, *, precomputed, logical_numel, block_symbols, lanes, steps, fixed_words,
+                 buffer=None, descriptor=None, frees=()) -> None:
+    """Center sampling, encoder and overflow bookkeeping in one launch
+    (``dispatch.py:33-48``, ``:294-316`` and ``:70-85`` as
+    ``LCT/codec/encode.py:22-186`` sequences them): for a shared ``buffer``
+    also the deferred ``frees`` and the arena reservation into
+    ``descriptor``.  ``compact_extra`` then writes the entries and tails."""
+    _require_device(source, side, encoded, summaries, counts)
+    n_blocks = size // block_symbols
+    control = control_array(source.device, n_blocks)
+    geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
+    pending = hip.PendingFrees()
+    pending.count = len(frees)
+    for i, freed in enumerate(frees):
+        pending.descriptor[i] = freed.data_ptr()
+    buffered = buffer is not None
+    hip.call("lct_encode_fused", _ptr(source), _ptr(side), _ptr(encoded), int(sample_size),
+             _ptr(encode_table), _ptr(decode_table), _ptr(center), _ptr(shifted_decode),
+             _ptr(sample_values), _ptr(extra_starts), _ptr(summaries), _ptr(blocks_out),
+             _ptr(counts), _ptr(control), int(control.numel()), _next_fused_epoch(),
+             _ptr(descriptor) if buffered else None, _ptr(buffer.storage) if buffered else None,
+             int(buffer.max_free_regions) if buffered else 0,
+             hip.ctypes.byref(pending) if buffered else None, int(size), int(logical_numel),
              geometry, int(bool(precomputed)), _stream(source))
 
 

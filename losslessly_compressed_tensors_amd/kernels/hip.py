@@ -99,6 +99,10 @@ _SIGNATURES = {
     "lct_allocate_compact": [_ptr, _ptr, _ptr, _ptr, _ptr, _c_int32, _ptr, _ptr, _ptr,
                              ctypes.POINTER(PendingFrees), _ptr, ctypes.c_uint64, _c_int64,
                              _c_int64, Geometry, _c_int32, _ptr],
+    "lct_encode_fused": [_ptr, _ptr, _ptr, _c_int64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
+                         _ptr, _ptr, _ptr, _c_int64, ctypes.c_uint32, _ptr, _ptr, _c_int32,
+                         ctypes.POINTER(PendingFrees), _c_int64, _c_int64, Geometry, _c_int32,
+                         _ptr],
     "lct_count_bad_streams": [_ptr, _ptr, _ptr, _c_int64, _c_int32, _ptr],
     "lct_compact_bad_streams": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64,
                                 _c_int32, _c_int64, _c_int32, _ptr],

@@ -44,7 +44,7 @@ FAIL_NO_FIT, FAIL_LOCK, FAIL_INCOMPLETE = 1, 2, 4
 _FAILURE_TEXT = {
     FAIL_NO_FIT: "no free region was large enough",
     FAIL_LOCK: "the arena lock could not be taken",
-    FAIL_INCOMPLETE: "the compaction into the reservation did not complete",
+    FAIL_INCOMPLETE: "the overflow bookkeeping or compaction did not complete",
 }
 _STATUS_FAILURE = {STATUS_NO_FIT: FAIL_NO_FIT, STATUS_LOCK: FAIL_LOCK,
                    STATUS_INCOMPLETE: FAIL_INCOMPLETE}
@@ -63,8 +63,9 @@ def _describe(bits: int) -> str:
 def check_reservation(status: int, count: int) -> None:
     """Raise ``BufferReservationError`` for a codec reservation with ``count``
     overflow entries whose descriptor status says the entries were not
-    stored."""
-    if count > 0 and status in _STATUS_FAILURE:
+    stored, and for every incomplete one (status 7: its bookkeeping or
+    compaction did not finish, so even ``count`` may be short)."""
+    if status == STATUS_INCOMPLETE or (count > 0 and status in _STATUS_FAILURE):
         raise BufferReservationError(
             f"compressed tensor's overflow reservation failed (status {status}: "
             f"{_describe(_STATUS_FAILURE[status])}); its {count} overflow streams were not "

@@ -65,7 +65,7 @@ def _nulls(name):
     for argtype in hip._SIGNATURES[name]:
         if argtype is hip.Geometry:
             args.append(hip.Geometry(32768, 256, 128, 12))
-        elif argtype in (ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64):
+        elif argtype in (ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64):
             args.append(argtype(1))
         else:
             args.append(None)
@@ -142,3 +142,32 @@ def test_no_alloc_compress_rejects_tensors_beyond_its_array(lib):
                                                  fake, fake, fake, None, fake, fake, fake, fake,
                                                  256, fake, None, None)
     assert bad_size == LCT_E_SIZE   # a whole empty block of padding
+
+
+def test_encode_fused_rejects_bad_arguments_before_launch(lib):
+    """lct_encode_fused checks its epoch, control array, sample count, buffer
+    and frees before anything is launched (the fake pointers are never
+    dereferenced)."""
+    fake = ctypes.c_void_p(1 << 20)
+    geometry = hip.Geometry(32768, 256, 128, 12)
+    size = 4 * 32768
+
+    def call(sample_size=4096, control=fake, words=64 + 4, epoch=7, meta=None,
+             regions=256, frees=None, logical=size):
+        return lib.lct_encode_fused(fake, fake, fake, sample_size, fake, fake, fake, fake, None,
+                                    fake, fake, fake, fake, control, words, epoch, fake, meta,
+                                    regions, frees, size, logical, geometry, 0, None)
+
+    assert call(epoch=0) == LCT_E_ARG                       # 0 matches a fresh array
+    assert call(words=64 + 3) == LCT_E_SIZE                 # no word for the last block
+    assert call(control=ctypes.c_void_p((1 << 20) + 4)) == LCT_E_ARG   # not 8-byte aligned
+    assert call(sample_size=3000) == LCT_E_ARG              # neither n nor a power of two
+    assert call(sample_size=8192) == LCT_E_SIZE             # more than 4096 samples
+    assert call(logical=size - 32768) == LCT_E_SIZE         # a whole block of padding
+    assert call(meta=fake, regions=100) == LCT_E_ARG        # not a power of two
+    too_many = hip.PendingFrees()
+    too_many.count = hip.MAX_PENDING_FREES + 1
+    assert call(meta=fake, frees=ctypes.byref(too_many)) == LCT_E_ARG
+    missing = hip.PendingFrees()
+    missing.count = 1
+    assert call(meta=fake, frees=ctypes.byref(missing)) == LCT_E_NULL

@@ -10,8 +10,10 @@ leaving through its own bounded wait:
 * no free region fits (a buffer too small for the tails): status 1;
 * the arena lock is held (an odd version written into the lock word from the
   host, the lock wait bounded by ``lct_set_wait_limits``): status 6;
-* a compacting workgroup stops waiting for the reservation (its poll bound
-  lowered to one poll): status 7, the region still held and freeable.
+* a compacting workgroup of the separate bookkeeping launch stops waiting
+  for the reservation (its poll bound lowered to one poll): status 7, the
+  region still held and freeable (the one-launch compress's own give-up path
+  is tested with it, in test_gpu_fused_compress.py).
 
 In each case ``CompressedTensor.memory_size()``, ``verify_buffer`` and
 ``TensorBuffer.check`` raise ``BufferReservationError``, the free list is left
@@ -23,6 +25,7 @@ import pytest
 import torch
 
 from gpu_util import require_gpu
+from losslessly_compressed_tensors_amd.codec.encode import encode_components
 from losslessly_compressed_tensors_amd.codec.geometry import geometry
 from losslessly_compressed_tensors_amd.comp_format import DistType, Distribution, NoiseLevel
 from losslessly_compressed_tensors_amd.compression.huffman_tables import get_distribution_tables
@@ -179,16 +182,30 @@ def test_prefix_allocate_records_a_lock_failure(wait_limits):
     assert buffer.failures() == FAIL_LOCK
 
 
+def _compress_given_center(x, dist, buffer, center):
+    """A buffered compress through the separate launches that a given center
+    takes (shifted tables, encoder, then the one-launch bookkeeping
+    lct_allocate_compact), as the fused updates' re-encodes use them."""
+    src = x.reshape(-1).view(torch.int16)
+    n = src.numel()
+    nb = -(-n // geometry(dist)[0])
+    size = nb * geometry(dist)[0]
+    side = torch.empty(size, dtype=torch.uint8, device="cuda")
+    return encode_components(src, side, size, dist, buffer, tuple(x.shape), precomputed=False,
+                             center=center, logical_numel=n)
+
+
 def test_compaction_that_stops_waiting_marks_the_reservation_incomplete(wait_limits):
     require_gpu()
     print("case failures incomplete compaction", flush=True)
     buffer = TensorBuffer(8 << 20, device="cuda")
     before = _free_regions_snapshot(buffer)
     x = _overflowing(6, n=40 * 65536)
+    center = compress(x, SPARSE).center
     wait_limits(0, 1)   # compacting workgroups poll the ready word once
     statuses = []
     for attempt in range(4):
-        ct = compress(x, SPARSE, buffer=buffer)
+        ct = _compress_given_center(x, SPARSE, buffer, center)
         status = _descriptor(ct)[2]
         statuses.append(status)
         print(f"attempt {attempt}: status {status}", flush=True)
