@@ -473,4 +473,16 @@ __device__ __forceinline__ void lds_write_back(const LdsFreeList &f, const Alloc
     if (threadIdx.x == 0) *m.count = f.count;
 }
 
+// The same with agent-scope atomic stores, which are coherent across the XCDs
+// once complete: the next lock holder reads them with coherent loads.
+__device__ __forceinline__ void lds_write_back_coherent(const LdsFreeList &f,
+                                                        const AllocatorMeta &m) {
+    for (int32_t i = threadIdx.x; i < f.count; i += kLanes) {
+        __hip_atomic_store(m.starts + i, f.start[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(m.sizes + i, f.size[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (threadIdx.x == 0)
+        __hip_atomic_store(m.count, f.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace lct

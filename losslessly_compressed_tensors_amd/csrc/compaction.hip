@@ -203,7 +203,7 @@ __global__ __launch_bounds__(kLanes) void allocate_compact_kernel(
     extern __shared__ int32_t free_list[];   // 2 * max_free_regions ints (workgroup 0)
     const uint64_t gave_up = ~epoch;
     if (blockIdx.x == 0) {
-        LdsReserve reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins), descriptor,
+        LdsReserve<true> reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins), descriptor,
                            frees, free_list, {}, -1, kStatusOk};
         SummaryLoads loads(summaries, n_blocks);
         scan_allocate<false, false>(loads, summaries, counts, blocks, n_blocks, reserve);

@@ -57,7 +57,7 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
     if (group == 0) {
         PolledSummaries polled{control, epoch, n_blocks, polls, false};
         if (buffer_meta != nullptr) {
-            LdsReserve reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins),
+            LdsReserve<false> reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins),
                                descriptor, frees, reinterpret_cast<int32_t *>(stage), {}, -1,
                                kStatusOk};
             scan_allocate<false, false>(polled, summaries, counts, blocks, n_blocks, reserve);

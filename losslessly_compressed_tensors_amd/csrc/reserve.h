@@ -312,10 +312,16 @@ struct RegisterReserve {
 // agent-scope loads: the copy is current exactly when that compare-and-swap
 // succeeds (otherwise the lock is waited for and the list read again).  The
 // deferred frees then run on the LDS copy, in order.  finish: the first-fit
-// reservation on the LDS copy, the list written back, the descriptor, and one
-// agent-scope release that publishes every write of the workgroup before the
-// lock goes to v + 2.  Two memory round trips before the scan, where the
+// reservation on the LDS copy, the list written back, the descriptor, and the
+// lock to v + 2 after a release.  kPublishAll: an agent-scope release fence
+// that publishes every write of the workgroup (lct_allocate_compact's waiters
+// then read the metadata in the same launch); without it only the free list
+// must be visible before the lock (everything else is read by later launches),
+// so the list is written back with agent-scope atomic stores and the release
+// is a wait for those stores -- the fence's write-back of this XCD's whole L2,
+// which holds the encoders' payload, took 2.5 us at 4096 blocks.  Two memory round trips before the scan, where the
 // register path takes three (lock, fence, list) plus one per free.
+template <bool kPublishAll>
 struct LdsReserve {
     AllocatorMeta meta;
     int32_t *descriptor;
@@ -376,7 +382,8 @@ struct LdsReserve {
                 const int32_t d[4] = {pending[j][0], pending[j][1], pending[j][2], pending[j][3]};
                 if (lds_free(f, d, scratch) == kStatusOk) {
                     if (t == 0) {
-                        frees.descriptor[j][2] = kStatusFreed;
+                        __hip_atomic_store(frees.descriptor[j] + 2, kStatusFreed, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
                         // A later copy of the same descriptor now reads as
                         // freed, so a second free of it is rejected, as the
                         // immediate free would reject it (status 4).
@@ -409,7 +416,10 @@ struct LdsReserve {
         } else {
             int32_t out[3];
             lds_reserve(f, request, scratch, out);
-            lds_write_back(f, meta);
+            if (kPublishAll)
+                lds_write_back(f, meta);
+            else
+                lds_write_back_coherent(f, meta);
             outcome = out[2];
             if (t == 0) {
                 descriptor[0] = out[0];
@@ -423,7 +433,15 @@ struct LdsReserve {
             const int32_t bits = failure_bits(outcome, request) | (incomplete ? kFailIncomplete : 0);
             if (bits != 0) record_failure(meta, bits);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        if (kPublishAll) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        } else {
+            // The free list's agent-scope stores have completed (vmcnt 0) before
+            // any thread passes the barrier; the compiler keeps them above it.
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        }
         __syncthreads();
         if (held >= 0 && t == 0)
             __hip_atomic_store(meta.lock, held + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
