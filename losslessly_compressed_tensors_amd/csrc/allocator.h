@@ -352,28 +352,30 @@ struct LdsFreeList {
     int32_t generation;   // uniform in every thread
 };
 
-// Entries [from, to) move by delta (+1 or -1).  Contains barriers.
+// Entries [from, to) move by delta (+1 or -1), 256 at a time: a +1 shift
+// walks the chunks from the last, a -1 shift from the first, so no entry is
+// overwritten before it is read, and a thread holds one entry at a time (the
+// LDS copy serves kernels whose registers the encoder's path bounds).
+// Contains barriers (none when the range is empty; from and to are uniform).
 __device__ __forceinline__ void lds_shift(LdsFreeList &f, int32_t from, int32_t to,
                                           int32_t delta) {
-    int32_t s[kRegionsPerThread], z[kRegionsPerThread];
-#pragma unroll
-    for (int k = 0; k < kRegionsPerThread; ++k) {
-        const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kLanes;
-        if (i >= from && i < to) {
-            s[k] = f.start[i];
-            z[k] = f.size[i];
+    const int32_t chunks = to > from ? (to - from + kLanes - 1) / kLanes : 0;
+    for (int32_t k = 0; k < chunks; ++k) {
+        const int32_t chunk = delta > 0 ? chunks - 1 - k : k;
+        const int32_t i = from + chunk * kLanes + static_cast<int32_t>(threadIdx.x);
+        const bool mine = i < to;
+        int32_t start = 0, size = 0;
+        if (mine) {
+            start = f.start[i];
+            size = f.size[i];
         }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < kRegionsPerThread; ++k) {
-        const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kLanes;
-        if (i >= from && i < to) {
-            f.start[i + delta] = s[k];
-            f.size[i + delta] = z[k];
+        __syncthreads();
+        if (mine) {
+            f.start[i + delta] = start;
+            f.size[i + delta] = size;
         }
+        __syncthreads();
     }
-    __syncthreads();
 }
 
 // tensor_buffer.py:94-179 on the LDS list for descriptor values d

@@ -25,7 +25,7 @@ __global__ __launch_bounds__(kLanes) void prefix_allocate_kernel(
     RegisterReserve reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins), descriptor,
                             &flag, buffered != 0, {}};
     SummaryLoads source(summaries, n_blocks);
-    scan_allocate<true, true>(source, summaries, counts, blocks, n_blocks, reserve);
+    scan_allocate<true>(source, summaries, counts, blocks, n_blocks, reserve);
 }
 
 // One codec block's overflow entries and tails (compaction.py:137-228), in
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(kLanes) void allocate_compact_kernel(
         LdsReserve<true> reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins), descriptor,
                            frees, free_list, {}, -1, kStatusOk};
         SummaryLoads loads(summaries, n_blocks);
-        scan_allocate<false, false>(loads, summaries, counts, blocks, n_blocks, reserve);
+        scan_allocate<false>(loads, summaries, counts, blocks, n_blocks, reserve);
         // finish() released every write of the workgroup at agent scope.
         if (threadIdx.x == 0) {
             const uint64_t before = __hip_atomic_exchange(ready, epoch, __ATOMIC_RELAXED,

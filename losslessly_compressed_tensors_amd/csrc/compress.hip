@@ -37,6 +37,7 @@
 namespace lct {
 namespace {
 
+template <int kSidePolicy>
 __global__ __launch_bounds__(kLanes) void compress_kernel(
     const void *__restrict__ source, uint8_t *__restrict__ side, int32_t *__restrict__ encoded,
     const int32_t *__restrict__ base_encode, const int32_t *__restrict__ base_decode,
@@ -60,10 +61,10 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
             LdsReserve<false> reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins),
                                descriptor, frees, reinterpret_cast<int32_t *>(stage), {}, -1,
                                kStatusOk};
-            scan_allocate<false, false>(polled, summaries, counts, blocks, n_blocks, reserve);
+            scan_allocate<false>(polled, summaries, counts, blocks, n_blocks, reserve);
         } else {
             NoReserve reserve;
-            scan_allocate<false, false>(polled, summaries, counts, blocks, n_blocks, reserve);
+            scan_allocate<false>(polled, summaries, counts, blocks, n_blocks, reserve);
         }
         return;
     }
@@ -103,9 +104,10 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
     const TableSource tables{nullptr, nullptr, n_groups, base_encode, base_decode, center_out,
                              shifted_decode_out, control, epoch, polls};
     const EncodeLds lds{stage, table, slices, scratch, shared};
-    const BlockSummary s = encode_codec_block(source, side, encoded, tables, extra_starts, block,
-                                              n_blocks, logical_numel, S, W, precomputed, true,
-                                              lds);
+    const BlockSummary s = encode_codec_block<kSidePolicy>(source, side, encoded, tables,
+                                                           extra_starts, block, n_blocks,
+                                                           logical_numel, S, W, precomputed,
+                                                           true, lds);
     if (threadIdx.x == 0) {
         // count <= 256 and bytes <= 256 * 256 fit 9 and 17 bits.
         const uint32_t value = s.failed ? (kFailedBlock << 17)
@@ -167,10 +169,13 @@ extern "C" int32_t lct_encode_fused(
     size_t lds = static_cast<size_t>(g.fixed_words + 2) * kLanes * 4;
     if (buffered && static_cast<size_t>(max_free_regions) * 8 > lds)
         lds = static_cast<size_t>(max_free_regions) * 8;
-    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&compress_kernel), lds))
+    // Side bytes: non-temporal stores for 128-step blocks, the default policy
+    // for 256-step blocks (the encoder's side-byte comment has the figures).
+    const auto kernel = g.steps == 128 ? compress_kernel<kStreaming> : compress_kernel<0>;
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(kernel), lds))
         return static_cast<int32_t>(e);
     const uint32_t grid = 1u + static_cast<uint32_t>(n_groups) + static_cast<uint32_t>(n_blocks);
-    hipLaunchKernelGGL(compress_kernel, dim3(grid), dim3(kLanes), lds, stream, source, side,
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kLanes), lds, stream, source, side,
                        encoded, base_encode, base_decode, center_out, shifted_decode_out,
                        precomputed ? nullptr : sample_values, sample_size, n_groups,
                        extra_starts, summaries, blocks, counts, control, epoch,

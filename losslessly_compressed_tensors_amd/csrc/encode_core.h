@@ -14,15 +14,14 @@
 //    BF16, or 64 exponent bytes) per row, so a chunk is 2 KiB (1 KiB) per
 //    wave; it is fetched with 16-byte non-temporal buffer loads two chunks
 //    ahead of use and staged in a wave-private LDS slice;
-//  * side bytes: written as one 16-byte non-temporal store per lane per chunk
-//    (16 rows x the wave's 64 bytes, half a cache line per row).  With each
-//    call's outputs in fresh memory (as in use) the non-temporal stores time
-//    as the default policy in the kernel (89.4 us at 4096 blocks) and leave
-//    the caches to the next launches: the public compress is 2 us shorter.
-//    (Rewriting one output block over and over, the default policy lets the
-//    256 MB Infinity Cache absorb the writes: 78 us, a figure no real caller
-//    sees.)  The input loads are non-temporal too (default-policy loads:
-//    91 us against 88);
+//  * side bytes: written as one 16-byte store per lane per chunk (16 rows x
+//    the wave's 64 bytes, half a cache line per row) with the cache policy
+//    the launch picks (kSidePolicy), measured with each call's outputs in
+//    fresh memory: the public compress at 4096 blocks of 128 steps takes 96 us
+//    with non-temporal stores and 103 us with the default policy, at 1024
+//    blocks of 256 steps (every block resident at once) 68 us against 64 us.
+//    The input loads are non-temporal (default-policy loads: 91 us against
+//    88 in the encoder alone at 4096 blocks);
 //  * payload: built in a zeroed LDS stage -- each pair ORs its code, placed at
 //    the lane's bit position, into stage rows pos/32 and pos/32 + 1 (two
 //    ds_or_b32, conflict-free: row stride 256 words), so no partial word is
@@ -138,7 +137,7 @@ __device__ __forceinline__ uint32_t side_bits_low(uint32_t v) {
 // complete in order), their side bytes take the first 64 bytes of those rows.
 constexpr uint32_t kInRowBytes = 2 * kWave;
 
-template <bool kFull, bool kPrecomputed, int S>
+template <bool kFull, bool kPrecomputed, int S, int kSidePolicy>
 __device__ __forceinline__ void encode_block(
     __amdgpu_buffer_rsrc_t src, __amdgpu_buffer_rsrc_t side, const uint2 *__restrict__ table,
     uint32_t *__restrict__ stage, uint8_t *in_slice, int64_t row_base,
@@ -216,7 +215,7 @@ __device__ __forceinline__ void encode_block(
         if (!kPrecomputed) {
             const u32x4 sides = *reinterpret_cast<const u32x4 *>(in_slice + side_read);
             __builtin_amdgcn_raw_buffer_store_b128(sides, side, side_store_offset + c * kLanes, 0,
-                                                   kStreaming);
+                                                   kSidePolicy);
         }
     };
 #pragma unroll 1
@@ -279,7 +278,7 @@ __device__ __forceinline__ bool setup_table(const TableSource &tables, uint2 *ta
     return failed;
 }
 
-template <bool kFull, bool kPrecomputed>
+template <bool kFull, bool kPrecomputed, int kSidePolicy>
 __device__ __forceinline__ bool encode_dispatch(int S, const void *source, int64_t logical_base,
                                                 __amdgpu_buffer_rsrc_t side,
                                                 const TableSource &tables, uint2 *table,
@@ -299,10 +298,10 @@ __device__ __forceinline__ bool encode_dispatch(int S, const void *source, int64
     const bool failed = setup_table(tables, table, raw, shared, block);
     __syncthreads();   // encode table and zeroed stage are visible
     if (S == 128)
-        encode_block<kFull, kPrecomputed, 128>(src, side, table, stage, in_slice, row_base,
+        encode_block<kFull, kPrecomputed, 128, kSidePolicy>(src, side, table, stage, in_slice, row_base,
                                                valid, W, first, overflow, extra);
     else
-        encode_block<kFull, kPrecomputed, 256>(src, side, table, stage, in_slice, row_base,
+        encode_block<kFull, kPrecomputed, 256, kSidePolicy>(src, side, table, stage, in_slice, row_base,
                                                valid, W, first, overflow, extra);
     return failed;
 }
@@ -329,6 +328,7 @@ struct BlockSummary {
 // One codec block (the body of every encoder launch): field split, payload,
 // per-stream extra starts, and -- when `summarize` -- the block's overflow
 // count and tail bytes.  Contains barriers.
+template <int kSidePolicy = kStreaming>
 __device__ __forceinline__ BlockSummary encode_codec_block(
     const void *__restrict__ source, uint8_t *__restrict__ side, int32_t *__restrict__ encoded,
     const TableSource &tables, uint8_t *__restrict__ extra_starts, int64_t block,
@@ -352,19 +352,19 @@ __device__ __forceinline__ BlockSummary encode_codec_block(
     int extra;
     bool failed;
     if (precomputed) {
-        if (full) failed = encode_dispatch<true, true>(S, source, logical_base, side_rsrc, tables,
+        if (full) failed = encode_dispatch<true, true, kSidePolicy>(S, source, logical_base, side_rsrc, tables,
                                                        lds.table, raw, lds.shared, block, stage,
                                                        in_slice, row_base, valid, W, overflow,
                                                        extra);
-        else failed = encode_dispatch<false, true>(S, source, logical_base, side_rsrc, tables,
+        else failed = encode_dispatch<false, true, kSidePolicy>(S, source, logical_base, side_rsrc, tables,
                                                    lds.table, raw, lds.shared, block, stage,
                                                    in_slice, row_base, valid, W, overflow, extra);
     } else {
-        if (full) failed = encode_dispatch<true, false>(S, source, logical_base, side_rsrc, tables,
+        if (full) failed = encode_dispatch<true, false, kSidePolicy>(S, source, logical_base, side_rsrc, tables,
                                                         lds.table, raw, lds.shared, block, stage,
                                                         in_slice, row_base, valid, W, overflow,
                                                         extra);
-        else failed = encode_dispatch<false, false>(S, source, logical_base, side_rsrc, tables,
+        else failed = encode_dispatch<false, false, kSidePolicy>(S, source, logical_base, side_rsrc, tables,
                                                     lds.table, raw, lds.shared, block, stage,
                                                     in_slice, row_base, valid, W, overflow,
                                                     extra);

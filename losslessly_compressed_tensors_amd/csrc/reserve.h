@@ -63,12 +63,9 @@ __device__ __forceinline__ void block_exclusive_scan3(const int32_t (&v)[3], int
 // a source of loads, once the first pass's loads are in flight, so those
 // latencies overlap), `reserve.finish(request, scratch, incomplete)` at the
 // end.  kWriteScans = false leaves the exclusive scans of summaries[2nb, 4nb)
-// unwritten (the block metadata holds the same values).  kLateStores stores
-// the last pass and the totals after the reservation, for callers whose
-// readers are later launches: the reservation's release then waits for fewer
-// stores.  Without it everything is stored before finish() releases.
+// unwritten (the block metadata holds the same values).
 // Workgroup-wide; contains barriers.
-template <bool kWriteScans, bool kLateStores, class Source, class Reserve>
+template <bool kWriteScans, class Source, class Reserve>
 __device__ __forceinline__ void scan_allocate(Source &source, int32_t *__restrict__ summaries,
                                               int32_t *__restrict__ counts,
                                               int32_t *__restrict__ blocks, int32_t n_blocks,
@@ -86,17 +83,38 @@ __device__ __forceinline__ void scan_allocate(Source &source, int32_t *__restric
     const __amdgpu_buffer_rsrc_t meta_base = make_rsrc(blocks + 2 * nb, bytes);
     int32_t *list = summaries + 4 * nb;
     int32_t carry[3] = {0, 0, 0};   // entries, tail bytes, listed blocks
-    int32_t c[kPer], v[kPer], firsts[kPer], bases[kPer];
-    int32_t list_before = 0, first_block = 0;
-    // One pass's list entries and block metadata (its blocks from first_block,
-    // firsts/bases their exclusive scans).
-    auto store_pass = [&]() {
+    int32_t c[kPer], v[kPer];
+    // A source whose values are in memory (kEarly) has the first pass's loads
+    // issued before the arena lock is requested, so their latency and the
+    // lock's overlap; a polled source takes the lock first.
+    if (Source::kEarly) source.load(0, c, v);
+    reserve.begin(scratch);
+    for (int base = 0; base < n_blocks; base += kPass) {
+        const int32_t first_block = base + t * kPer;
         const uint32_t off = static_cast<uint32_t>(first_block) * 4u;
         const bool whole = first_block + kPer <= n_blocks;
-        int32_t entry = list_before;
+        if (base > 0 || !Source::kEarly) source.load(base, c, v);
+        int32_t run[3] = {0, 0, 0};
 #pragma unroll
-        for (int k = 0; k < kPer; ++k)
-            if (c[k] > 0) list[entry++] = first_block + k;
+        for (int k = 0; k < kPer; ++k) {
+            run[0] += c[k];
+            run[1] += v[k];
+            run[2] += c[k] > 0 ? 1 : 0;
+        }
+        int32_t before[3], total[3];
+        block_exclusive_scan3(run, scratch, before, total);
+        int32_t count_before = carry[0] + before[0];
+        int32_t byte_before = carry[1] + before[1];
+        int32_t list_before = carry[2] + before[2];
+        int32_t firsts[kPer], bases[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            firsts[k] = count_before;
+            bases[k] = byte_before;
+            if (c[k] > 0) list[list_before++] = first_block + k;
+            count_before += c[k];
+            byte_before += v[k];
+        }
         if (!whole) {
 #pragma unroll
             for (int k = 0; k < kPer; ++k) {
@@ -132,58 +150,21 @@ __device__ __forceinline__ void scan_allocate(Source &source, int32_t *__restric
             __builtin_amdgcn_raw_buffer_store_b128(fq, meta_first, off + 16 * q, 0, 0);
             __builtin_amdgcn_raw_buffer_store_b128(bq, meta_base, off + 16 * q, 0, 0);
         }
-    };
-    // A source whose values are in memory (kEarly) has the first pass's loads
-    // issued before the arena lock is requested, so their latency and the
-    // lock's overlap; a polled source takes the lock first.
-    if (Source::kEarly) source.load(0, c, v);
-    reserve.begin(scratch);
-    for (int base = 0; base < n_blocks; base += kPass) {
-        first_block = base + t * kPer;
-        if (base > 0 || !Source::kEarly) source.load(base, c, v);
-        int32_t run[3] = {0, 0, 0};
-#pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-            run[0] += c[k];
-            run[1] += v[k];
-            run[2] += c[k] > 0 ? 1 : 0;
-        }
-        int32_t before[3], total[3];
-        block_exclusive_scan3(run, scratch, before, total);
-        int32_t count_before = carry[0] + before[0];
-        int32_t byte_before = carry[1] + before[1];
-        list_before = carry[2] + before[2];
-#pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-            firsts[k] = count_before;
-            bases[k] = byte_before;
-            count_before += c[k];
-            byte_before += v[k];
-        }
 #pragma unroll
         for (int k = 0; k < 3; ++k) carry[k] += total[k];
-        // With kLateStores the last pass is stored after the reservation.
-        if (!kLateStores || base + kPass < n_blocks) store_pass();
     }
     // A polled source whose summaries did not all arrive leaves the tensor
     // incomplete: counts[3] and the reservation's status say so.
     const bool incomplete = source.incomplete();
-    auto store_totals = [&]() {
-        if (t == 0) {
-            counts[0] = carry[0];
-            counts[1] = carry[1];
-            counts[2] = 0;
-            counts[3] = incomplete ? 1 : 0;
-            summaries[5 * nb] = carry[2];
-        }
-    };
-    if (!kLateStores) store_totals();
+    if (t == 0) {
+        counts[0] = carry[0];
+        counts[1] = carry[1];
+        counts[2] = 0;
+        counts[3] = incomplete ? 1 : 0;
+        summaries[5 * nb] = carry[2];
+    }
     // Two metadata bytes per overflowing stream: lane, then start step.
     reserve.finish(carry[1] + 2 * carry[0], scratch, incomplete);
-    if (kLateStores) {
-        store_pass();
-        store_totals();
-    }
 }
 
 // Per-block overflow counts and tail bytes from summaries[0, nb) and
