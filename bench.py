@@ -10,10 +10,11 @@ Cache can neither serve repeated reads nor absorb repeated writes.
 Prints one JSON line: ``value`` is decompression throughput in GB/s of
 uncompressed BF16 (2n bytes / time), with compression throughput, the
 compression ratio, the decoder kernel's roofline fraction (``roofline``), the
-encoder kernel's (``encode_roofline``), config C2 (an 8192x8192 weight-like
-tensor, MEDIUM layout: ``config2``), config C3 (a sparse activation-like
-tensor with forced overflow in a shared 64 MiB buffer: ``config3``), the fused momentum update of config
-C4 with its single-pass kernel's roofline (``update``), the weight step of
+one-launch compress kernel's (``encode_roofline``: center sampling, encoder
+and overflow bookkeeping), config C2 (an 8192x8192 weight-like tensor, MEDIUM
+layout: ``config2``), config C3 (a sparse activation-like tensor with forced
+overflow in a shared 64 MiB buffer: ``config3``), the fused momentum update of
+config C4 with its single-pass kernel's roofline (``update``), the weight step of
 compressed SGD-momentum with its single-pass kernel's roofline
 (``weight_update``), config 5 (a GPT-2-small training step with weights,
 activations and Muon momentum compressed, against the same step uncompressed:
@@ -643,31 +644,30 @@ def main() -> int:
                                   max(5, args.steps // 5), 2, torch)
     enc_alg = encode_bytes(cts[0])
 
-    # Encoder kernel alone (field split + tables from the sampler's partials +
-    # payload), launched back to back into preallocated outputs.
+    # The fused compress kernel alone (center sampling, encoder and overflow
+    # bookkeeping in one launch, private form: no arena), launched back to back
+    # into preallocated outputs; each launch's words carry a fresh epoch.
     encode_table, decode_table, _ = get_distribution_tables(dist, device)
     nb = n // B
-    partials = []
-    for x in xs:
-        p = torch.empty(2 * 64, dtype=torch.int32, device=device)
-        dispatch.sample_center(x.view(-1).view(torch.int16), n, 4096, False, p)
-        partials.append(p)
     enc_sets = [dict(side=torch.empty(n, dtype=torch.uint8, device=device),
                      encoded=torch.empty(nb * L * W + 4, dtype=torch.int32, device=device),
                      center=torch.empty(1, dtype=torch.int32, device=device),
                      shifted=torch.empty(1024, dtype=torch.int32, device=device),
+                     samples=torch.empty(4096, dtype=torch.int16, device=device),
                      extra=torch.empty(nb * L, dtype=torch.uint8, device=device),
-                     summaries=torch.empty(5 * nb + 1, dtype=torch.int32, device=device))
+                     summaries=torch.empty(dispatch.summaries_length(nb), dtype=torch.int32,
+                                           device=device),
+                     counts=torch.empty(4, dtype=torch.int32, device=device),
+                     blocks=torch.empty(3 * nb, dtype=torch.int32, device=device))
                 for _ in range(ROTATION)]
 
     def launch_encode(i):
-        enc_outs = enc_sets[i % ROTATION]
-        dispatch.encode_sampled(xs[i % 2].view(-1).view(torch.int16), enc_outs["side"],
-                                enc_outs["encoded"], partials[i % 2], 4096, encode_table,
-                                decode_table, enc_outs["center"], enc_outs["shifted"],
-                                enc_outs["extra"], enc_outs["summaries"], n, precomputed=False,
-                                logical_numel=n, block_symbols=B, lanes=L, steps=S,
-                                fixed_words=W)
+        o = enc_sets[i % ROTATION]
+        dispatch.encode_fused(xs[i % 2].view(-1).view(torch.int16), o["side"], o["encoded"],
+                              4096, encode_table, decode_table, o["center"], o["shifted"],
+                              o["samples"], o["extra"], o["summaries"], o["blocks"], o["counts"],
+                              n, precomputed=False, logical_numel=n, block_symbols=B, lanes=L,
+                              steps=S, fixed_words=W)
 
     for i in range(args.warmup):
         launch_encode(i)
@@ -733,12 +733,12 @@ def main() -> int:
                                        / HBM_PEAK_GBPS, 4),
         },
         "encode_roofline": {
-            "kernel": "encode_kernel",
+            "kernel": "compress_kernel",
             "kernel_us": round(encode_kernel_ms * 1e3, 2),
             "algorithmic_bytes": enc_alg,
             "achieved": round(enc_alg / (encode_kernel_ms * 1e-3) / 1e9, 1),
             "frac": round(enc_alg / (encode_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-            "traffic": measured_traffic("encode_kernel", nb),
+            "traffic": measured_traffic("compress_kernel<2>", nb + 65),
         },
     }
     result["config2"] = config2
