@@ -108,13 +108,30 @@ __device__ __forceinline__ void write_block(
         starts[start_off + first + e.rank] = static_cast<uint8_t>(e.start);
     }
     uint8_t *out = tail + tail_off + byte_base;
-    // Byte t may have been read by rank_block already (prefetched).
-    for (int32_t i = t; i < e.bytes; i += kLanes) {
-        const int32_t x = prefetched && i == t
-                              ? e.first_tail
-                              : tail_byte(source, i, e.count, block, logical_numel, S,
-                                          precomputed, entry_offset, entry_start, entry_lane);
-        out[i] = static_cast<uint8_t>(x);
+    // Byte t may have been read by rank_block already (prefetched).  The rest
+    // go kTailBatch per thread at a time, every load issued before the batch's
+    // stores, so a block with many tail bytes waits for one load latency per
+    // batch instead of one per byte.
+    int32_t i = t;
+    if (prefetched) {
+        if (i < e.bytes) out[i] = static_cast<uint8_t>(e.first_tail);
+        i += kLanes;
+    }
+    constexpr int kTailBatch = 4;
+    for (; i < e.bytes; i += kTailBatch * kLanes) {
+        int32_t x[kTailBatch];
+#pragma unroll
+        for (int k = 0; k < kTailBatch; ++k) {
+            const int32_t j = i + k * kLanes;
+            x[k] = j < e.bytes ? tail_byte(source, j, e.count, block, logical_numel, S,
+                                           precomputed, entry_offset, entry_start, entry_lane)
+                               : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < kTailBatch; ++k) {
+            const int32_t j = i + k * kLanes;
+            if (j < e.bytes) out[j] = static_cast<uint8_t>(x[k]);
+        }
     }
     __syncthreads();   // the entry arrays are reused by the next block
 }

@@ -11,22 +11,29 @@
 // lct_sample_center -> lct_encode_sampled -> lct_prefix_allocate (or, with a
 // buffer, the reservation of lct_allocate_compact), value for value.
 //
-// Workgroups, in dispatch order:
-//  * 0: bookkeeping.  With a buffer it takes the arena lock, reads the free
-//    list into LDS and applies the deferred frees at once, then polls the
-//    encoders' per-block summaries, scans them and reserves the tensor's
-//    overflow region (request = tail bytes + 2 x entries), so only the last
-//    summary's arrival, the scan and the reservation follow the last block;
-//  * 1..G: center samplers (G = ceil(samples / 64), one wave each), which
-//    publish their partial sums and never wait;
-//  * G+1..G+nb: encoders of codec blocks 0..nb-1.  Each polls the G partial
-//    sums (its first input chunk in flight meanwhile), encodes its block as
-//    lct_encode_sampled does and publishes its overflow count and tail bytes.
-// Every wait is for workgroups dispatched before the waiter that themselves
-// wait only for earlier ones (the samplers for nothing), and every poll is
-// bounded; a summary or partial sum that does not arrive within the bound
-// marks the tensor incomplete (counts[3] = 1; with a buffer, status 7 and the
-// buffer's failure word) instead of hanging.
+// One workgroup per codec block (and, for tensors of fewer blocks than
+// center-sample groups, one per group), in dispatch order; no workgroup is
+// only a helper, so a grid that fills the device runs in whole rounds:
+//  * workgroup g < G (G = ceil(samples / 64) <= 64): wave 0 first samples
+//    center group g (64 positions) and publishes its partial sum; it waits
+//    for nothing before that;
+//  * every workgroup b < nb then polls the G partial sums (its first input
+//    chunk in flight meanwhile), encodes block b as lct_encode_sampled does
+//    and publishes its overflow count and tail bytes;
+//  * workgroup 0, after its own block, does the bookkeeping: with a buffer it
+//    takes the arena lock, reads the free list into LDS and applies the
+//    deferred frees, then polls every block's summary, scans them into the
+//    metadata and the overflow-block list and reserves the tensor's overflow
+//    region (request = tail bytes + 2 x entries).  Only the last summary's
+//    arrival, the scan's last pass and the reservation follow the last block.
+// Every wait is for words that workgroups dispatched no later than the waiter
+// publish before they wait for anything, and every poll is bounded; a summary
+// or partial sum that does not arrive within the bound marks the tensor
+// incomplete (counts[3] = 1; with a buffer, status 7 and the buffer's failure
+// word) instead of hanging.  (Helper workgroups of their own -- a bookkeeping
+// workgroup and 64 samplers in front of the encoders -- pushed the last of
+// 1024 blocks of 256 steps, four per CU, into a second round: 55 us against
+// the 43 us in which the other blocks had finished.)
 //
 // Cross-workgroup values travel in a control array of 64-bit words tagged with
 // the call's epoch (lct_device.h), one array per stream, never cleared: a word
@@ -55,27 +62,11 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
     __shared__ int32_t shared[2];
     const int64_t group = blockIdx.x;
 
-    if (group == 0) {
-        PolledSummaries polled{control, epoch, n_blocks, polls, false};
-        if (buffer_meta != nullptr) {
-            LdsReserve<false> reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins),
-                               descriptor, frees, reinterpret_cast<int32_t *>(stage), {}, -1,
-                               kStatusOk};
-            scan_allocate<false>(polled, summaries, counts, blocks, n_blocks, reserve);
-        } else {
-            NoReserve reserve;
-            scan_allocate<false>(polled, summaries, counts, blocks, n_blocks, reserve);
-        }
-        return;
-    }
-
-    if (group <= n_groups) {
-        // Samples (group - 1) * 64 + lane (tables.py:15-49): the kept
-        // exponents' sum and count; a BF16 source's sampled bits also go to
-        // sample_values.
-        if (threadIdx.x >= kWave) return;
+    if (group < n_groups && threadIdx.x < kWave) {
+        // Samples group * 64 + lane (tables.py:15-49): the kept exponents' sum
+        // and count; a BF16 source's sampled bits also go to sample_values.
         const int t = threadIdx.x;
-        const int64_t i = (group - 1) * kSampleGroup + t;
+        const int64_t i = group * kSampleGroup + t;
         const bool active = i < sample_size;
         const int shift = __builtin_ctzll(static_cast<uint64_t>(sample_size));
         int32_t exp = -127;
@@ -95,12 +86,12 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
         if (t == 0) {
             const uint32_t value = (static_cast<uint32_t>(static_cast<uint16_t>(sum)) << 16)
                                    | static_cast<uint32_t>(kept);
-            control_store(control + (group - 1), tagged_word(epoch, value));
+            control_store(control + group, tagged_word(epoch, value));
         }
-        return;
     }
+    if (group >= n_blocks) return;   // a sample group past the last block
 
-    const int64_t block = group - 1 - n_groups;
+    const int64_t block = group;
     const TableSource tables{nullptr, nullptr, n_groups, base_encode, base_decode, center_out,
                              shifted_decode_out, control, epoch, polls};
     const EncodeLds lds{stage, table, slices, scratch, shared};
@@ -114,6 +105,20 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
                                         : (static_cast<uint32_t>(s.count) << 17)
                                               | static_cast<uint32_t>(s.bytes);
         control_store(control + kControlPartials + block, tagged_word(epoch, value));
+    }
+    if (block != 0) return;
+
+    // The bookkeeping.  The stage's last readers passed the summary's
+    // barriers, so it can hold the free list.
+    PolledSummaries polled{control, epoch, n_blocks, polls, false};
+    if (buffer_meta != nullptr) {
+        LdsReserve<false> reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins),
+                                  descriptor, frees, reinterpret_cast<int32_t *>(stage), {}, -1,
+                                  kStatusOk};
+        scan_allocate<false>(polled, summaries, counts, blocks, n_blocks, reserve);
+    } else {
+        NoReserve reserve;
+        scan_allocate<false>(polled, summaries, counts, blocks, n_blocks, reserve);
     }
 }
 
@@ -174,7 +179,7 @@ extern "C" int32_t lct_encode_fused(
     const auto kernel = g.steps == 128 ? compress_kernel<kStreaming> : compress_kernel<0>;
     if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(kernel), lds))
         return static_cast<int32_t>(e);
-    const uint32_t grid = 1u + static_cast<uint32_t>(n_groups) + static_cast<uint32_t>(n_blocks);
+    const uint32_t grid = static_cast<uint32_t>(n_blocks > n_groups ? n_blocks : n_groups);
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kLanes), lds, stream, source, side,
                        encoded, base_encode, base_decode, center_out, shifted_decode_out,
                        precomputed ? nullptr : sample_values, sample_size, n_groups,
