@@ -199,8 +199,9 @@ int32_t lct_allocate_compact(const void *source, int32_t *summaries, int32_t *co
 
 /* ---- replaces, for one tensor, the sequence dispatch.py:33-48 (center +
  * tables), :294-316 (encoder) and :70-85 (prefix + allocate) that
- * LCT/codec/encode.py:22-186 runs, in one launch: center samplers, encoders
- * and one bookkeeping workgroup.  Its outputs equal those of
+ * LCT/codec/encode.py:22-186 runs, in one launch of one workgroup per codec
+ * block (the first 64 also sample the center before they encode; workgroup 0
+ * does the bookkeeping after its block).  Its outputs equal those of
  * lct_sample_center (sample_values) -> lct_encode_sampled (side, encoded,
  * center_out, shifted_decode_out, extra_starts) -> lct_prefix_allocate
  * (counts, blocks, and the overflow-block list summaries[4*nb .. 5*nb]; the
@@ -208,7 +209,8 @@ int32_t lct_allocate_compact(const void *source, int32_t *summaries, int32_t *co
  * bookkeeping workgroup first applies `frees` (as lct_allocate_compact) and
  * then makes the reservation of lct_prefix_allocate with buffered = 1 into
  * descriptor; lct_compact_extra (buffered = 1, or into exact-size private
- * arrays after the host reads counts) then writes the entries and tails.
+ * arrays after the host reads counts; summaries NULL or as written here) then
+ * writes the entries and tails.
  * control: uint64[control_words >= 64 + nb], one array per stream, zeroed once
  * when created and never again; epoch: a value != 0 that no earlier call with
  * this control array used (the launch's cross-workgroup words carry it).
@@ -255,7 +257,8 @@ int32_t lct_compact_bad_streams(const uint8_t *extra_starts, uint8_t *lanes,
 /* ---- replaces dispatch.py:113-130 (compact_extra): for the blocks listed by
  * lct_prefix_allocate (summaries path), or for every block with overflow
  * when summaries is NULL (block metadata from lct_compact_bad_streams,
- * BUILD_META=False), write the overflowing streams' lane and start bytes
+ * BUILD_META=False, or from lct_encode_fused; one workgroup per block, which
+ * needs no list), write the overflowing streams' lane and start bytes
  * (ascending lane) at entries blocks[nb+k].. and their exponent tails
  * int8(e-127) for steps start..S-1 from byte blocks[2nb+k].  Private:
  * lanes/starts/tail are exact-size arrays, tails at tail + base.  Buffered:

@@ -126,7 +126,7 @@ def _encode_fused(source_values, sign_mantissa, encoded, extra_starts, summaries
     fused = dict(size=size, **launch)
     compaction = dict(precomputed=precomputed, logical_numel=logical_numel,
                       block_symbols=block_symbols, lanes=lanes, steps=steps,
-                      extra_starts=extra_starts, summaries=summaries)
+                      extra_starts=extra_starts, summaries=None)
     if buffer is not None:
         descriptor = torch.empty(4, dtype=torch.int32, device=device)
         frees = buffer._take_frees()

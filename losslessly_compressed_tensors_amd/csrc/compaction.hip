@@ -70,16 +70,14 @@ __device__ __forceinline__ int32_t tail_byte(const void *__restrict__ source, in
 
 // With `source` given, the block's first 256 tail bytes are also read here
 // (they depend on the ranking only), one per thread.
-__device__ __forceinline__ BlockEntries rank_block(const uint8_t *__restrict__ extra_starts,
-                                                   int64_t block, int S, int32_t *scratch,
-                                                   int32_t *entry_offset, int32_t *entry_start,
-                                                   int32_t *entry_lane,
-                                                   const void *__restrict__ source = nullptr,
-                                                   int64_t logical_numel = 0,
-                                                   int precomputed = 0) {
+__device__ __forceinline__ BlockEntries rank_block_start(int32_t start, int64_t block, int S,
+                                                         int32_t *scratch, int32_t *entry_offset,
+                                                         int32_t *entry_start, int32_t *entry_lane,
+                                                         const void *__restrict__ source,
+                                                         int64_t logical_numel, int precomputed) {
     const int t = threadIdx.x;
     BlockEntries e;
-    e.start = extra_starts[block * kLanes + t];
+    e.start = start;
     const bool bad = e.start != 255;
     const int32_t local = block_exclusive_scan(bad ? S - e.start : 0, scratch, &e.bytes);
     e.rank = block_exclusive_scan(bad ? 1 : 0, scratch, &e.count);
@@ -94,6 +92,19 @@ __device__ __forceinline__ BlockEntries rank_block(const uint8_t *__restrict__ e
                                    entry_offset, entry_start, entry_lane)
                        : 0;
     return e;
+}
+
+// The same, loading this lane's extra start.
+__device__ __forceinline__ BlockEntries rank_block(const uint8_t *__restrict__ extra_starts,
+                                                   int64_t block, int S, int32_t *scratch,
+                                                   int32_t *entry_offset, int32_t *entry_start,
+                                                   int32_t *entry_lane,
+                                                   const void *__restrict__ source = nullptr,
+                                                   int64_t logical_numel = 0,
+                                                   int precomputed = 0) {
+    return rank_block_start(extra_starts[block * kLanes + threadIdx.x], block, S, scratch,
+                            entry_offset, entry_start, entry_lane, source, logical_numel,
+                            precomputed);
 }
 
 __device__ __forceinline__ void write_block(
@@ -145,9 +156,7 @@ __global__ __launch_bounds__(kLanes) void compact_extra_kernel(
     int S, int precomputed, int buffered) {
     __shared__ int32_t scratch[kWavesPerBlock];
     __shared__ int32_t entry_offset[kLanes], entry_start[kLanes], entry_lane[kLanes];
-    // Without summaries (block metadata from compact_bad_streams_kernel) every
-    // block is visited; the entries it rewrites are the ones already there.
-    const int32_t *list = summaries != nullptr ? summaries + 4 * n_blocks : nullptr;
+    const int32_t *list = summaries + 4 * n_blocks;
     // The reservation, the list's length and this workgroup's first list entry
     // are loaded together -- the entry speculatively (blockIdx.x < n_blocks by
     // the grid's size, and the list has n_blocks entries), used only if it is
@@ -156,16 +165,15 @@ __global__ __launch_bounds__(kLanes) void compact_extra_kernel(
     const int32_t status = buffered ? descriptor[2] : kStatusOk;
     const int64_t arena = buffered ? descriptor[0] : 0;
     const int64_t total = buffered ? count_total[0] : 0;
-    const int64_t listed = list != nullptr ? summaries[5 * n_blocks] : n_blocks;
+    const int64_t listed = summaries[5 * n_blocks];
     int64_t i = blockIdx.x;
-    int64_t block = list != nullptr ? list[i] : i;
+    int64_t block = list[i];
     if (status != kStatusOk) return;   // failed allocation: write nothing
     const int64_t lane_off = buffered ? arena : 0;
     const int64_t start_off = buffered ? arena + total : 0;
     const int64_t tail_off = buffered ? arena + 2 * total : base;
     for (; i < listed; i += gridDim.x) {
-        if (i != blockIdx.x) block = list != nullptr ? list[i] : i;
-        if (list == nullptr && blocks[block] == 0) continue;   // uniform
+        if (i != blockIdx.x) block = list[i];
         // The block's first 256 tail bytes are read with the ranking.
         const BlockEntries e = rank_block(extra_starts, block, S, scratch, entry_offset,
                                           entry_start, entry_lane, source, logical_numel,
@@ -174,6 +182,39 @@ __global__ __launch_bounds__(kLanes) void compact_extra_kernel(
                     blocks[n_blocks + block], blocks[2 * n_blocks + block], e, block,
                     logical_numel, S, precomputed, entry_offset, entry_start, entry_lane, true);
     }
+}
+
+// compact_extra's form without summaries (every block's metadata written
+// before the launch: lct_compact_bad_streams, or the one-launch compress's
+// bookkeeping): one workgroup per codec block loads the block's metadata, the
+// reservation and its lanes' extra starts at once -- one memory round trip
+// before the ranking -- and leaves if the block has no overflow.  The entries
+// a block rewrites are the ones already there.
+__global__ __launch_bounds__(kLanes) void compact_blocks_kernel(
+    const void *__restrict__ source, uint8_t *__restrict__ lanes,
+    uint8_t *__restrict__ starts, uint8_t *__restrict__ tail,
+    const int32_t *__restrict__ descriptor, const int32_t *__restrict__ count_total,
+    const int32_t *__restrict__ blocks, int64_t base, const uint8_t *__restrict__ extra_starts,
+    int64_t n_blocks, int64_t logical_numel, int S, int precomputed, int buffered) {
+    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ int32_t entry_offset[kLanes], entry_start[kLanes], entry_lane[kLanes];
+    const int64_t block = blockIdx.x;
+    const int32_t count = blocks[block];
+    const int32_t first = blocks[n_blocks + block];
+    const int32_t byte_base = blocks[2 * n_blocks + block];
+    const int32_t start = extra_starts[block * kLanes + threadIdx.x];
+    const int32_t status = buffered ? descriptor[2] : kStatusOk;
+    const int64_t arena = buffered ? descriptor[0] : 0;
+    const int64_t total = buffered ? count_total[0] : 0;
+    if (count == 0 || status != kStatusOk) return;   // uniform
+    const int64_t lane_off = buffered ? arena : 0;
+    const int64_t start_off = buffered ? arena + total : 0;
+    const int64_t tail_off = buffered ? arena + 2 * total : base;
+    const BlockEntries e = rank_block_start(start, block, S, scratch, entry_offset, entry_start,
+                                            entry_lane, source, logical_numel, precomputed);
+    write_block(source, lanes, starts, tail, lane_off, start_off, tail_off, first, byte_base, e,
+                block, logical_numel, S, precomputed, entry_offset, entry_start, entry_lane,
+                true);
 }
 
 // Waits of the compacting workgroups for workgroup 0's reservation: polls of
@@ -450,10 +491,17 @@ extern "C" int32_t lct_compact_extra(const void *source, uint8_t *lanes, uint8_t
         return LCT_E_SIZE;
     const int64_t n_blocks = size / g.block_symbols;
     if (n_blocks > 0x7FFFFFFF) return LCT_E_SIZE;
+    if (summaries == nullptr) {
+        hipLaunchKernelGGL(compact_blocks_kernel, dim3(static_cast<uint32_t>(n_blocks)),
+                           dim3(kLanes), 0, stream, source, lanes, starts, tail, descriptor, count,
+                           blocks, base, extra_starts, n_blocks, logical_numel, g.steps,
+                           precomputed, buffered);
+        return static_cast<int32_t>(hipGetLastError());
+    }
     const uint32_t grid = static_cast<uint32_t>(n_blocks < kCompactGrid ? n_blocks : kCompactGrid);
-    hipLaunchKernelGGL(compact_extra_kernel, dim3(grid), dim3(kLanes), 0, stream, source, lanes, starts, tail, descriptor, count, blocks, base,
-                       extra_starts, summaries, n_blocks, logical_numel, g.steps, precomputed,
-                       buffered);
+    hipLaunchKernelGGL(compact_extra_kernel, dim3(grid), dim3(kLanes), 0, stream, source, lanes,
+                       starts, tail, descriptor, count, blocks, base, extra_starts, summaries,
+                       n_blocks, logical_numel, g.steps, precomputed, buffered);
     return static_cast<int32_t>(hipGetLastError());
 }
 

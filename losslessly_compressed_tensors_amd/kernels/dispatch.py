@@ -303,7 +303,8 @@ def compact_extra(source, storage: FallbackStorage, n_blocks, n_elements, *, pre
                   summaries) -> None:
     """Overflow entries and tails (``dispatch.py:113-130``): of the blocks
     ``prefix_allocate`` listed, or, with ``summaries=None``, of every block
-    whose metadata ``compact_bad_streams`` wrote."""
+    whose metadata ``compact_bad_streams`` or ``encode_fused`` wrote (one
+    workgroup per block)."""
     _require_device(source, extra_starts)
     geometry = hip.Geometry(block_symbols, lanes, steps, 2)
     hip.call("lct_compact_extra", _ptr(source), _ptr(storage.lanes), _ptr(storage.starts),
