@@ -79,8 +79,15 @@ __device__ __forceinline__ BlockEntries rank_block_start(int32_t start, int64_t 
     BlockEntries e;
     e.start = start;
     const bool bad = e.start != 255;
-    const int32_t local = block_exclusive_scan(bad ? S - e.start : 0, scratch, &e.bytes);
-    e.rank = block_exclusive_scan(bad ? 1 : 0, scratch, &e.count);
+    // One scan of both counts: tail bytes in bits 0..19 (at most 256 x 256),
+    // entries from bit 20 (at most 256).
+    int32_t totals;
+    const int32_t packed = block_exclusive_scan(bad ? (S - e.start) | (1 << 20) : 0, scratch,
+                                                &totals);
+    const int32_t local = packed & 0xFFFFF;
+    e.rank = packed >> 20;
+    e.bytes = totals & 0xFFFFF;
+    e.count = totals >> 20;
     if (bad) {
         entry_offset[e.rank] = local;
         entry_start[e.rank] = e.start;
