@@ -44,7 +44,9 @@
 namespace lct {
 namespace {
 
-template <int kSidePolicy>
+// One kernel per input kind (BF16 bits or precomputed exponent bytes), so
+// each carries one encoder variant and its registers.
+template <int kSidePolicy, bool kPrecomputed>
 __global__ __launch_bounds__(kLanes) void compress_kernel(
     const void *__restrict__ source, uint8_t *__restrict__ side, int32_t *__restrict__ encoded,
     const int32_t *__restrict__ base_encode, const int32_t *__restrict__ base_decode,
@@ -54,7 +56,7 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
     int32_t *__restrict__ blocks, int32_t *__restrict__ counts, uint64_t *__restrict__ control,
     uint32_t epoch, int32_t *__restrict__ descriptor, int32_t *__restrict__ buffer_meta,
     int32_t max_free_regions, lct_pending_frees frees, int32_t n_blocks, int64_t logical_numel,
-    int S, int W, int precomputed, int32_t lock_spins, int32_t polls) {
+    int S, int W, int32_t lock_spins, int32_t polls) {
     extern __shared__ uint32_t stage[];   // (W + 2) rows x 256 lanes, or the free list
     __shared__ uint2 table[256];
     __shared__ __attribute__((aligned(16))) uint8_t slices[kWavesPerBlock * kSliceBytes];
@@ -72,7 +74,7 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
         int32_t exp = -127;
         if (active) {
             const int64_t pos = sample_position(i, logical_numel, sample_size, shift);
-            if (precomputed) {
+            if (kPrecomputed) {
                 exp = static_cast<int32_t>(static_cast<const uint8_t *>(source)[pos]) - 127;
             } else {
                 const uint32_t bits = static_cast<const uint16_t *>(source)[pos];
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
     const EncodeLds lds{stage, table, slices, scratch, shared};
     const BlockSummary s = encode_codec_block<kSidePolicy>(source, side, encoded, tables,
                                                            extra_starts, block, n_blocks,
-                                                           logical_numel, S, W, precomputed,
+                                                           logical_numel, S, W, kPrecomputed,
                                                            true, lds);
     if (threadIdx.x == 0) {
         // count <= 256 and bytes <= 256 * 256 fit 9 and 17 bits.
@@ -176,7 +178,10 @@ extern "C" int32_t lct_encode_fused(
         lds = static_cast<size_t>(max_free_regions) * 8;
     // Side bytes: non-temporal stores for 128-step blocks, the default policy
     // for 256-step blocks (the encoder's side-byte comment has the figures).
-    const auto kernel = g.steps == 128 ? compress_kernel<kStreaming> : compress_kernel<0>;
+    const auto kernel = g.steps == 128
+                            ? (precomputed ? compress_kernel<kStreaming, true>
+                                           : compress_kernel<kStreaming, false>)
+                            : (precomputed ? compress_kernel<0, true> : compress_kernel<0, false>);
     if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(kernel), lds))
         return static_cast<int32_t>(e);
     const uint32_t grid = static_cast<uint32_t>(n_blocks > n_groups ? n_blocks : n_groups);
@@ -186,6 +191,6 @@ extern "C" int32_t lct_encode_fused(
                        extra_starts, summaries, blocks, counts, control, epoch,
                        buffered ? descriptor : nullptr, buffer_meta, max_free_regions, pending,
                        static_cast<int32_t>(n_blocks), logical_numel, g.steps, g.fixed_words,
-                       precomputed, lock_spins(), ready_polls());
+                       lock_spins(), ready_polls());
     return static_cast<int32_t>(hipGetLastError());
 }

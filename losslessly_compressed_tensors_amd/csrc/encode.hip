@@ -8,12 +8,14 @@
 namespace lct {
 namespace {
 
+// One kernel per input kind (BF16 bits or precomputed exponent bytes), so
+// each carries one encoder variant and its registers.
+template <bool kPrecomputed>
 __global__ __launch_bounds__(kLanes) void encode_kernel(
     const void *__restrict__ source, uint8_t *__restrict__ side,
     int32_t *__restrict__ encoded, TableSource tables,
     uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
-    int64_t n_blocks, int64_t logical_numel, int S, int W, int precomputed,
-    int write_summary) {
+    int64_t n_blocks, int64_t logical_numel, int S, int W, int write_summary) {
     extern __shared__ uint32_t stage[];   // (W + 2) rows x 256 lanes
     __shared__ uint2 table[256];
     __shared__ __attribute__((aligned(16))) uint8_t slices[kWavesPerBlock * kSliceBytes];
@@ -22,7 +24,7 @@ __global__ __launch_bounds__(kLanes) void encode_kernel(
     const EncodeLds lds{stage, table, slices, scratch, shared};
     const int64_t block = blockIdx.x;
     const BlockSummary s = encode_codec_block(source, side, encoded, tables, extra_starts, block,
-                                              n_blocks, logical_numel, S, W, precomputed,
+                                              n_blocks, logical_numel, S, W, kPrecomputed,
                                               write_summary != 0, lds);
     if (write_summary && threadIdx.x == 0) {
         summaries[block] = s.count;
@@ -54,12 +56,13 @@ int32_t launch_encode(const void *source, uint8_t *side, int32_t *encoded,
           | reinterpret_cast<uintptr_t>(side)) & 15) != 0)
         return LCT_E_ARG;
     const size_t lds = static_cast<size_t>(g.fixed_words + 2) * kLanes * 4;
-    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&encode_kernel), lds))
+    const auto kernel = precomputed ? encode_kernel<true> : encode_kernel<false>;
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(kernel), lds))
         return static_cast<int32_t>(e);
-    hipLaunchKernelGGL(encode_kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes),
+    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes),
                        lds, stream, source, side, encoded, tables,
                        extra_starts, summaries, n_blocks, logical_numel, g.steps,
-                       g.fixed_words, precomputed, write_summary);
+                       g.fixed_words, write_summary);
     return static_cast<int32_t>(hipGetLastError());
 }
 

@@ -385,8 +385,11 @@ __device__ __forceinline__ BlockSummary encode_codec_block(
 
     BlockSummary summary{0, 0, failed};
     if (summarize) {
-        summary.count = block_sum(overflow ? 1 : 0, lds.scratch);
-        summary.bytes = block_sum(overflow ? S - extra : 0, lds.scratch);
+        // Both sums in one: tail bytes in bits 0..19 (at most 256 x 256),
+        // streams from bit 20 (at most 256).
+        const int32_t both = block_sum(overflow ? (S - extra) | (1 << 20) : 0, lds.scratch);
+        summary.count = both >> 20;
+        summary.bytes = both & 0xFFFFF;
     }
     return summary;
 }
