@@ -154,6 +154,17 @@ __device__ __forceinline__ void encode_block(
     // the chunk, bytes (j%4)*16.. of the wave's 64-byte segment.
     const uint32_t side_store_offset = side_fetch_offset();
     const uint32_t side_read = (j >> 2) * kInRowBytes + (j & 3) * 16;
+    // Non-temporal side stores go out as whole 128-byte lines: the waves of a
+    // pair (2p, 2p+1) hold the two halves of each row's line, so after a
+    // barrier wave 2p stores rows 0..7 of the chunk and wave 2p+1 rows 8..15,
+    // each lane 16 bytes read from the slice of the wave that encoded them.
+    constexpr bool kJoinLines = kSidePolicy == kStreaming;
+    const uint32_t wave = lane / kWave;
+    const uint32_t join_row = (wave & 1u) * 8u + (j >> 3);
+    const uint8_t *const join_read = in_slice - (wave & 1u) * kSliceBytes
+                                     + ((j >> 2) & 1u) * kSliceBytes + join_row * kInRowBytes
+                                     + (j & 3u) * 16u;
+    const uint32_t join_store_offset = join_row * kLanes + (wave >> 1) * 128u + (j & 7u) * 16u;
 
     uint32_t pos = 0;
     // Pairs that fit.  pos only grows, so they are exactly the pairs before the
@@ -212,7 +223,13 @@ __device__ __forceinline__ void encode_block(
             fits += over ? 0u : 1u;
             pos = after;
         }
-        if (!kPrecomputed) {
+        if (!kPrecomputed && kJoinLines) {
+            __syncthreads();   // the pair's side bytes of this chunk are in its slices
+            const u32x4 sides = *reinterpret_cast<const u32x4 *>(join_read);
+            __builtin_amdgcn_raw_buffer_store_b128(sides, side, join_store_offset + c * kLanes, 0,
+                                                   kSidePolicy);
+            __syncthreads();   // read before the partner's next chunk overwrites its slice
+        } else if (!kPrecomputed) {
             const u32x4 sides = *reinterpret_cast<const u32x4 *>(in_slice + side_read);
             __builtin_amdgcn_raw_buffer_store_b128(sides, side, side_store_offset + c * kLanes, 0,
                                                    kSidePolicy);
