@@ -809,8 +809,11 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     const bool overflow = writer.overflowed();
     const int32_t extra = writer.extra_start();
     extra_starts[block * kLanes + t] = static_cast<uint8_t>(overflow ? extra : 255);
-    const int32_t count = block_sum(overflow ? 1 : 0, scratch);
-    const int32_t bytes = block_sum(overflow ? S - extra : 0, scratch);
+    // Streams from bit 20 (at most 256), tail bytes in bits 0..19 (at most
+    // 256 x 256): one block scan.
+    const int32_t both = block_sum(overflow ? (S - extra) | (1 << 20) : 0, scratch);
+    const int32_t count = both >> 20;
+    const int32_t bytes = both & 0xFFFFF;
     if (t == 0) {
         summaries[block] = count;
         summaries[n_blocks + block] = bytes;
@@ -1360,8 +1363,11 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     const bool overflow = writer.overflowed();
     const int32_t extra = writer.extra_start();
     extra_starts[block * kLanes + t] = static_cast<uint8_t>(overflow ? extra : 255);
-    const int32_t count = block_sum(overflow ? 1 : 0, scratch);
-    const int32_t bytes = block_sum(overflow ? S - extra : 0, scratch);
+    // Streams from bit 20 (at most 256), tail bytes in bits 0..19 (at most
+    // 256 x 256): one block scan.
+    const int32_t both = block_sum(overflow ? (S - extra) | (1 << 20) : 0, scratch);
+    const int32_t count = both >> 20;
+    const int32_t bytes = both & 0xFFFFF;
     if (t == 0) {
         summaries[block] = count;
         summaries[n_blocks + block] = bytes;
