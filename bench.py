@@ -748,7 +748,7 @@ def main() -> int:
             "algorithmic_bytes": enc_alg,
             "achieved": round(enc_alg / (encode_kernel_ms * 1e-3) / 1e9, 1),
             "frac": round(enc_alg / (encode_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-            "traffic": measured_traffic("compress_kernel<2>", nb),
+            "traffic": measured_traffic("compress_kernel<2,false>", nb),
         },
     }
     result["config2"] = config2

@@ -14,14 +14,18 @@
 //    BF16, or 64 exponent bytes) per row, so a chunk is 2 KiB (1 KiB) per
 //    wave; it is fetched with 16-byte non-temporal buffer loads two chunks
 //    ahead of use and staged in a wave-private LDS slice;
-//  * side bytes: written as one 16-byte store per lane per chunk (16 rows x
-//    the wave's 64 bytes, half a cache line per row) with the cache policy
-//    the launch picks (kSidePolicy), measured with each call's outputs in
-//    fresh memory: the public compress at 4096 blocks of 128 steps takes 96 us
-//    with non-temporal stores and 103 us with the default policy, at 1024
-//    blocks of 256 steps (every block resident at once) 68 us against 64 us.
-//    The input loads are non-temporal (default-policy loads: 91 us against
-//    88 in the encoder alone at 4096 blocks);
+//  * side bytes: one 16-byte store per lane per chunk, with the cache policy
+//    the launch picks (kSidePolicy).  Non-temporal stores go out as whole
+//    128-byte lines: the waves of a pair hold the two 64-byte halves of each
+//    row's line, so after a barrier each wave stores 8 of the chunk's 16 rows
+//    (half-line stores wrote 208 MB against 186 MB of side bytes at 4096
+//    blocks of 128 steps, and the public compress took 94 us against 89).
+//    The default policy (its L2 merges the halves) stores each wave's own
+//    half lines: at 1024 blocks of 256 steps (every block resident at once)
+//    55 us against 57 us with the joined non-temporal lines.  Measured with
+//    each call's outputs in fresh memory.  The input loads are non-temporal
+//    (default-policy loads: 91 us against 88 in the encoder alone at 4096
+//    blocks);
 //  * payload: built in a zeroed LDS stage -- each pair ORs its code, placed at
 //    the lane's bit position, into stage rows pos/32 and pos/32 + 1 (two
 //    ds_or_b32, conflict-free: row stride 256 words), so no partial word is
