@@ -69,6 +69,27 @@ typedef struct {
     int32_t count;
 } lct_pending_frees;
 
+/* The overflow bookkeeping an encoder launch can do in its own workgroup 0
+ * after that workgroup's block (lct_pointwise_encode_fused,
+ * lct_dual_encode_fused), with the arrays of lct_encode_fused's:
+ * control: uint64[control_words >= 64 + nb], one array per stream, zeroed once
+ * when created and never again; epoch: a value != 0 that no earlier call with
+ * this control array used; counts: int32[4]; blocks: int32[3 * nb];
+ * buffer_meta: the TensorBuffer's metadata, or NULL for private storage;
+ * descriptor: int32[4] (buffered); max_free_regions: the buffer's R; frees:
+ * deferred frees applied first, as lct_allocate_compact applies them. */
+typedef struct {
+    uint64_t *control;
+    int64_t control_words;
+    uint32_t epoch;
+    int32_t *counts;
+    int32_t *blocks;
+    int32_t *descriptor;
+    int32_t *buffer_meta;
+    int32_t max_free_regions;
+    lct_pending_frees frees;
+} lct_bookkeeping;
+
 /* Pointwise operation selectors: LCT/codec/pointwise.py:289-304. */
 #define LCT_OP_ADD 0
 #define LCT_OP_MULTIPLY 1
@@ -423,6 +444,30 @@ int32_t lct_pointwise_encode(const int32_t *encoded, const uint8_t *side,
                              int32_t alpha_is_one, int32_t beta_is_one,
                              hipStream_t stream);
 
+/* ---- lct_pointwise_encode with the overflow bookkeeping of
+ * LCT/codec/encode.py:77-170 (dispatch.py:70-85, prefix + allocate) in the
+ * same launch: outputs as lct_pointwise_encode followed by
+ * lct_prefix_allocate (counts, blocks, and the overflow-block list
+ * summaries[4nb .. 5nb]; summaries[0 .. 4nb) are not written) or, with a
+ * buffer, by lct_allocate_compact's frees and reservation (descriptor); then
+ * lct_compact_extra (summaries NULL, precomputed = 1, source = exponents)
+ * writes the entries and tails.  A bounded wait that gives up marks the
+ * tensor incomplete as lct_encode_fused does (counts[3] = 1; status 7).
+ * summaries: int32[5*nb + 1]; encoded_out 16-byte aligned. */
+int32_t lct_pointwise_encode_fused(const int32_t *encoded, const uint8_t *side,
+                                   const int32_t *shifted_decode, const int32_t *center,
+                                   const lct_overflow *overflow, const void *other,
+                                   const float *alpha, const float *beta,
+                                   const int32_t *partials, int64_t sample_size,
+                                   const int32_t *base_encode, const int32_t *base_decode,
+                                   int32_t *center_out, int32_t *shifted_decode_out,
+                                   uint8_t *side_out, int32_t *encoded_out,
+                                   uint8_t *extra_starts, int32_t *summaries,
+                                   uint8_t *exponents, int64_t size, int64_t logical_numel,
+                                   lct_geometry geometry, int32_t rare_length, int32_t op,
+                                   int32_t alpha_is_one, int32_t beta_is_one,
+                                   const lct_bookkeeping *bookkeeping, hipStream_t stream);
+
 /* ---- single-pass compressed-output alpha*A + B over two compressed
  * operands, step 1 of 2: replaces the center estimate that dispatch.py:33-48
  * makes over the exponent bytes written by dispatch.py:215-286 (dual_mapped,
@@ -459,6 +504,21 @@ int32_t lct_dual_encode(const int32_t *a_encoded, const uint8_t *a_side,
                         int32_t *encoded_out, uint8_t *extra_starts, int32_t *summaries,
                         uint8_t *exponents, int64_t size, int64_t logical_numel,
                         lct_geometry geometry, int32_t rare_length, hipStream_t stream);
+
+/* ---- lct_dual_encode with the overflow bookkeeping in the same launch, as
+ * lct_pointwise_encode_fused adds it to lct_pointwise_encode. */
+int32_t lct_dual_encode_fused(const int32_t *a_encoded, const uint8_t *a_side,
+                              const int32_t *a_shifted_decode, const int32_t *a_center,
+                              const lct_overflow *a_overflow, const int32_t *b_encoded,
+                              const uint8_t *b_side, const int32_t *b_shifted_decode,
+                              const int32_t *b_center, const lct_overflow *b_overflow,
+                              const float *alpha, const int32_t *partials, int64_t sample_size,
+                              const int32_t *base_encode, const int32_t *base_decode,
+                              int32_t *center_out, int32_t *shifted_decode_out,
+                              uint8_t *side_out, int32_t *encoded_out, uint8_t *extra_starts,
+                              int32_t *summaries, uint8_t *exponents, int64_t size,
+                              int64_t logical_numel, lct_geometry geometry, int32_t rare_length,
+                              const lct_bookkeeping *bookkeeping, hipStream_t stream);
 
 /* ---- TensorBuffer allocator kernels: replace LCT/tensor_buffer.py:130-136
  * (_reset_kernel launch), :93-120 (_allocate_kernel launches) and

@@ -116,17 +116,12 @@ def _encode_fused(source_values, sign_mantissa, encoded, extra_starts, summaries
     private form reads the overflow totals once (as the reference does) to
     allocate exact-size lane/start/tail arrays."""
     device = encoded.device
-    stream_geometry = geometry(distribution)
-    block_symbols, lanes, steps, _ = stream_geometry
+    block_symbols = geometry(distribution)[0]
     blocks = _cdiv(size, block_symbols)
-    precomputed = launch["precomputed"]
-    logical_numel = launch["logical_numel"]
     counts = torch.empty(4, dtype=torch.int32, device=device)
     blocks_out = torch.empty(3 * blocks, dtype=torch.int32, device=device)
+    descriptor = None
     fused = dict(size=size, **launch)
-    compaction = dict(precomputed=precomputed, logical_numel=logical_numel,
-                      block_symbols=block_symbols, lanes=lanes, steps=steps,
-                      extra_starts=extra_starts, summaries=None)
     if buffer is not None:
         descriptor = torch.empty(4, dtype=torch.int32, device=device)
         frees = buffer._take_frees()
@@ -139,15 +134,42 @@ def _encode_fused(source_values, sign_mantissa, encoded, extra_starts, summaries
             # Nothing was launched: the deferred frees wait for the next call.
             buffer._restore_frees(frees)
             raise
-        arena = buffer.data
-        storage = FallbackStorage(tail=arena, count=counts[:1], lanes=arena, starts=arena,
-                                  blocks=blocks_out, descriptor=descriptor,
-                                  allocation=descriptor)
-        dispatch.compact_extra(source_values, storage, blocks, size, buffered=True, **compaction)
     else:
         dispatch.encode_fused(source_values, sign_mantissa, encoded, sample_size, encode_table,
                               decode_table, center, shifted_decode, sample_values, extra_starts,
                               summaries, blocks_out, counts, **fused)
+    return finish_fused(source_values, sign_mantissa, encoded, extra_starts, size, distribution,
+                        buffer, shape, precomputed=launch["precomputed"], center=center,
+                        shifted_decode=shifted_decode, logical_numel=launch["logical_numel"],
+                        sample_values=sample_values, counts=counts, blocks_out=blocks_out,
+                        descriptor=descriptor)
+
+
+def finish_fused(tail_source, sign_mantissa, encoded, extra_starts, size, distribution, buffer,
+                 shape, *, precomputed, center, shifted_decode, logical_numel, sample_values,
+                 counts, blocks_out, descriptor) -> CompressedTensor:
+    """After an encoder launch that made its own overflow bookkeeping
+    (``lct_encode_fused``, ``lct_pointwise_encode_fused``,
+    ``lct_dual_encode_fused``; ``LCT/codec/encode.py:77-186``): the compaction
+    (``lct_compact_extra`` over the block metadata that launch wrote) and the
+    CompressedTensor.  ``tail_source`` holds the tails' exponents (BF16 bits,
+    or exponent bytes in logical order when ``precomputed``).  With a buffer
+    nothing syncs; private storage reads the totals once to size exact
+    lane/start/tail arrays and raises if a device-side wait gave up."""
+    device = encoded.device
+    stream_geometry = geometry(distribution)
+    block_symbols, lanes, steps, _ = stream_geometry
+    blocks = _cdiv(size, block_symbols)
+    compaction = dict(precomputed=precomputed, logical_numel=logical_numel,
+                      block_symbols=block_symbols, lanes=lanes, steps=steps,
+                      extra_starts=extra_starts, summaries=None)
+    if buffer is not None:
+        arena = buffer.data
+        storage = FallbackStorage(tail=arena, count=counts[:1], lanes=arena, starts=arena,
+                                  blocks=blocks_out, descriptor=descriptor,
+                                  allocation=descriptor)
+        dispatch.compact_extra(tail_source, storage, blocks, size, buffered=True, **compaction)
+    else:
         count, tail_bytes, _, incomplete = (int(v) for v in counts.tolist())
         if incomplete:
             raise RuntimeError(
@@ -160,7 +182,7 @@ def _encode_fused(source_values, sign_mantissa, encoded, extra_starts, summaries
             starts=torch.empty(count, dtype=torch.uint8, device=device),
             blocks=blocks_out, allocation=counts[2:3], base=0)
         if count > 0:
-            dispatch.compact_extra(source_values, storage, blocks, size, buffered=False,
+            dispatch.compact_extra(tail_source, storage, blocks, size, buffered=False,
                                    **compaction)
     buffered = buffer is not None
     return CompressedTensor(

@@ -28,7 +28,7 @@ from ..kernels import dispatch, hip
 from ..tensor_buffer import TensorBuffer
 from .decode import decode as decode_dense
 from .decode import overlay_of, shifted_decode_table, storage_of
-from .encode import CENTER_SAMPLE_SIZE, finish_encode
+from .encode import CENTER_SAMPLE_SIZE, finish_encode, finish_fused
 from .encode import encode as compress_dense
 from .encode import encode_components as compress_components
 from .geometry import geometry
@@ -90,6 +90,44 @@ def _launch_pointwise_compressed_dense(data: CompressedTensor, other: torch.Tens
     return output, auxiliary
 
 
+def _encode_with_bookkeeping(launch_encoder, exponents, side, encoded, extra_starts, summaries,
+                             size, distribution, buffer, shape, *, center, shifted_decode,
+                             logical_numel, sample_values) -> CompressedTensor:
+    """Run a fused update's encoder launch, ``launch_encoder(record)``, with
+    the overflow bookkeeping in the same launch when the block count allows
+    (a ``dispatch.bookkeeping`` record: prefix scan and, for a shared buffer,
+    the deferred frees and the reservation), then the compaction; otherwise
+    the encoder alone followed by ``finish_encode``'s bookkeeping launches.
+    Either way the stored tensor is the same (``LCT/codec/encode.py:77-186``)."""
+    device = encoded.device
+    blocks = size // geometry(distribution)[0]
+    if not 0 < blocks <= dispatch.MAX_CODEC_BLOCKS:
+        launch_encoder(None)
+        return finish_encode(exponents, side, encoded, extra_starts, summaries, size,
+                             distribution, buffer, shape, precomputed=True, center=center,
+                             shifted_decode=shifted_decode, logical_numel=logical_numel,
+                             sample_values=sample_values)
+    counts = torch.empty(4, dtype=torch.int32, device=device)
+    blocks_out = torch.empty(3 * blocks, dtype=torch.int32, device=device)
+    descriptor = None
+    frees = ()
+    if buffer is not None:
+        descriptor = torch.empty(4, dtype=torch.int32, device=device)
+        frees = buffer._take_frees()
+    try:
+        launch_encoder(dispatch.bookkeeping(device, blocks, counts, blocks_out, buffer,
+                                            descriptor, frees))
+    except BaseException:
+        # Nothing was launched: the deferred frees wait for the next call.
+        if buffer is not None:
+            buffer._restore_frees(frees)
+        raise
+    return finish_fused(exponents, side, encoded, extra_starts, size, distribution, buffer,
+                        shape, precomputed=True, center=center, shifted_decode=shifted_decode,
+                        logical_numel=logical_numel, sample_values=sample_values,
+                        counts=counts, blocks_out=blocks_out, descriptor=descriptor)
+
+
 def _fused_compressed_output(data: CompressedTensor, other: torch.Tensor,
                              operation: PointwiseOp, result_distribution: Distribution,
                              buffer: TensorBuffer | None, *, alpha: torch.Tensor | None,
@@ -145,14 +183,18 @@ def _fused_compressed_output(data: CompressedTensor, other: torch.Tensor,
     # Only the rows of overflowing streams are written (and read back by the
     # compaction); the rest stays unwritten.
     exponents = torch.empty(n, dtype=torch.uint8, device=device)
-    dispatch.pointwise_encode(data.data, data.sign_mantissa, decode_table, data.center, other,
-                              alpha_arg, beta_arg, partials, base_encode,
-                              base_decode, center, shifted_decode, side, encoded, extra_starts,
-                              summaries, exponents, data.size, **launch)
-    return finish_encode(exponents, side, encoded, extra_starts, summaries, data.size,
-                         result_distribution, buffer, data.shape, precomputed=True,
-                         center=center, shifted_decode=shifted_decode, logical_numel=n,
-                         sample_values=result_samples)
+
+    def launch_encoder(record):
+        dispatch.pointwise_encode(data.data, data.sign_mantissa, decode_table, data.center,
+                                  other, alpha_arg, beta_arg, partials, base_encode,
+                                  base_decode, center, shifted_decode, side, encoded,
+                                  extra_starts, summaries, exponents, data.size, record=record,
+                                  **launch)
+
+    return _encode_with_bookkeeping(launch_encoder, exponents, side, encoded, extra_starts,
+                                    summaries, data.size, result_distribution, buffer,
+                                    data.shape, center=center, shifted_decode=shifted_decode,
+                                    logical_numel=n, sample_values=result_samples)
 
 
 def _fused_dual_compressed_output(data: CompressedTensor, other: CompressedTensor,
@@ -206,14 +248,18 @@ def _fused_dual_compressed_output(data: CompressedTensor, other: CompressedTenso
     # Only the rows of overflowing streams are written (and read back by the
     # compaction); the rest stays unwritten.
     exponents = torch.empty(n, dtype=torch.uint8, device=device)
-    dispatch.dual_encode(data.data, data.sign_mantissa, a_table, data.center, a_storage,
-                         other.data, other.sign_mantissa, b_table, other.center, b_storage,
-                         alpha, partials, base_encode, base_decode, center, shifted_decode,
-                         side, encoded, extra_starts, summaries, exponents, data.size, **launch)
-    return finish_encode(exponents, side, encoded, extra_starts, summaries, data.size,
-                         result_distribution, buffer, data.shape, precomputed=True,
-                         center=center, shifted_decode=shifted_decode, logical_numel=n,
-                         sample_values=result_samples)
+
+    def launch_encoder(record):
+        dispatch.dual_encode(data.data, data.sign_mantissa, a_table, data.center, a_storage,
+                             other.data, other.sign_mantissa, b_table, other.center, b_storage,
+                             alpha, partials, base_encode, base_decode, center, shifted_decode,
+                             side, encoded, extra_starts, summaries, exponents, data.size,
+                             record=record, **launch)
+
+    return _encode_with_bookkeeping(launch_encoder, exponents, side, encoded, extra_starts,
+                                    summaries, data.size, result_distribution, buffer,
+                                    data.shape, center=center, shifted_decode=shifted_decode,
+                                    logical_numel=n, sample_values=result_samples)
 
 
 def _launch_scalar_mul_add_compressed_compressed(data: CompressedTensor,

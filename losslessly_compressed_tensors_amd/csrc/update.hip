@@ -32,6 +32,7 @@
 // 73.6 MB against 62.9 MB per launch; with the default policy 63.3 MB, at
 // equal kernel time).
 #include "pointwise_ops.h"
+#include "reserve.h"
 
 namespace lct {
 namespace {
@@ -55,6 +56,61 @@ struct OpArgs {
     int32_t alpha_is_one;
     int32_t beta_is_one;
 };
+
+// The in-launch overflow bookkeeping of the *_encode_fused launches (control
+// == nullptr: the block summaries go to `summaries` for a later launch).
+struct KernelBookkeeping {
+    uint64_t *control;
+    uint32_t epoch;
+    int32_t *counts;
+    int32_t *blocks;
+    int32_t *descriptor;
+    int32_t *buffer_meta;
+    int32_t max_free_regions;
+    lct_pending_frees frees;
+    int32_t lock_spins;
+    int32_t polls;
+};
+
+// After a block (every thread, past the summary's barriers): its overflow
+// count and tail bytes go to `summaries`, or -- in a fused launch (kBooked:
+// its own kernel instantiation, so the separate launch's kernel holds none of
+// the bookkeeping's arguments in registers) -- to the control array as a
+// tagged word, and workgroup 0 then does the bookkeeping
+// of the one-launch compress: with a buffer the lock, the deferred frees and
+// the free list in `lds_free_list` (the payload stage, free by now), the
+// polled scan into the block metadata and the overflow-block list, and the
+// reservation (lct_prefix_allocate / lct_allocate_compact's results).
+template <bool kBooked>
+__device__ __forceinline__ void publish_block(const KernelBookkeeping &bk,
+                                              int32_t *__restrict__ summaries, int64_t block,
+                                              int64_t n_blocks, int32_t count, int32_t bytes,
+                                              int32_t *lds_free_list) {
+    if (!kBooked) {
+        if (threadIdx.x == 0) {
+            summaries[block] = count;
+            summaries[n_blocks + block] = bytes;
+        }
+        return;
+    }
+    if (threadIdx.x == 0) {
+        // count <= 256 and bytes <= 256 * 256 fit 9 and 17 bits.
+        const uint32_t value = (static_cast<uint32_t>(count) << 17) | static_cast<uint32_t>(bytes);
+        control_store(bk.control + kControlPartials + block, tagged_word(bk.epoch, value));
+    }
+    if (block != 0) return;
+    PolledSummaries polled{bk.control, bk.epoch, static_cast<int32_t>(n_blocks), bk.polls, false};
+    if (bk.buffer_meta != nullptr) {
+        LdsReserve<false> reserve{AllocatorMeta(bk.buffer_meta, bk.max_free_regions, bk.lock_spins),
+                                  bk.descriptor, bk.frees, lds_free_list, {}, -1, kStatusOk};
+        scan_allocate<false>(polled, summaries, bk.counts, bk.blocks,
+                             static_cast<int32_t>(n_blocks), reserve);
+    } else {
+        NoReserve reserve;
+        scan_allocate<false>(polled, summaries, bk.counts, bk.blocks,
+                             static_cast<int32_t>(n_blocks), reserve);
+    }
+}
 
 // Cursors of the fused encode kernels, over FloatDecodeTables: decoded
 // entries become FP32 operands with one v_perm and one v_bfi (join_float).
@@ -729,6 +785,7 @@ __device__ __forceinline__ void update_block(int32_t form, bool full, const Upda
     }
 }
 
+template <bool kBooked>
 __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     OperandA a, const uint16_t *__restrict__ other, OpArgs args,
     const int32_t *__restrict__ partials, int32_t n_groups,
@@ -737,7 +794,7 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     uint8_t *__restrict__ side_out, int32_t *__restrict__ encoded_out,
     uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
     uint8_t *__restrict__ exponents, int64_t n_blocks, int64_t logical_numel, int S, int W,
-    int rare) {
+    int rare, KernelBookkeeping bk) {
     extern __shared__ uint32_t stage[];   // A's payload: window_stage_bytes(W)
     __shared__ FloatDecodeTables tb;
     __shared__ uint2 enc[256];
@@ -812,12 +869,8 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     // Streams from bit 20 (at most 256), tail bytes in bits 0..19 (at most
     // 256 x 256): one block scan.
     const int32_t both = block_sum(overflow ? (S - extra) | (1 << 20) : 0, scratch);
-    const int32_t count = both >> 20;
-    const int32_t bytes = both & 0xFFFFF;
-    if (t == 0) {
-        summaries[block] = count;
-        summaries[n_blocks + block] = bytes;
-    }
+    publish_block<kBooked>(bk, summaries, block, n_blocks, both >> 20, both & 0xFFFFF,
+                           reinterpret_cast<int32_t *>(stage));
 }
 
 // ---- the two-compressed form: alpha * A + B with compressed output
@@ -1266,6 +1319,7 @@ __device__ __forceinline__ void dual_rows(UpdateCursor ca, const LaneOverlay &la
                                            alpha);
 }
 
+template <bool kBooked>
 __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     OperandA a, OperandA b, const float *__restrict__ alpha,
     const int32_t *__restrict__ partials, int32_t n_groups,
@@ -1274,7 +1328,7 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     uint8_t *__restrict__ side_out, int32_t *__restrict__ encoded_out,
     uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
     uint8_t *__restrict__ exponents, int64_t n_blocks, int64_t logical_numel, int S, int W,
-    int rare) {
+    int rare, KernelBookkeeping bk) {
     extern __shared__ uint32_t stages[];   // A's rows 3..W-1, then B's
     __shared__ FloatDecodeTables tba, tbb;
     __shared__ uint2 enc[256];
@@ -1366,12 +1420,8 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     // Streams from bit 20 (at most 256), tail bytes in bits 0..19 (at most
     // 256 x 256): one block scan.
     const int32_t both = block_sum(overflow ? (S - extra) | (1 << 20) : 0, scratch);
-    const int32_t count = both >> 20;
-    const int32_t bytes = both & 0xFFFFF;
-    if (t == 0) {
-        summaries[block] = count;
-        summaries[n_blocks + block] = bytes;
-    }
+    publish_block<kBooked>(bk, summaries, block, n_blocks, both >> 20, both & 0xFFFFF,
+                           reinterpret_cast<int32_t *>(stages));
 }
 
 int32_t check_operand(const int32_t *encoded, const uint8_t *side, const int32_t *shifted_decode,
@@ -1444,14 +1494,54 @@ extern "C" int32_t lct_pointwise_sample(const int32_t *encoded, const uint8_t *s
     return static_cast<int32_t>(hipGetLastError());
 }
 
-extern "C" int32_t lct_pointwise_encode(
+namespace {
+
+// The host side of lct_bookkeeping: validated against the launch's block
+// count, in the kernel's form (bk.control == nullptr without one).  Also
+// raises `lds` to the free list's LDS copy when buffered.
+int32_t prepare_bookkeeping(const lct_bookkeeping *in, int64_t n_blocks, KernelBookkeeping &bk,
+                            size_t &lds) {
+    bk = KernelBookkeeping{};
+    if (in == nullptr) return LCT_OK;
+    if (!in->control || !in->counts || !in->blocks) return LCT_E_NULL;
+    if (n_blocks > kMaxBlocks) return LCT_E_SIZE;
+    if (in->control_words < kControlPartials + n_blocks) return LCT_E_SIZE;
+    // Epoch 0 would match a control array's initial zeros.
+    if (in->epoch == 0) return LCT_E_ARG;
+    if ((reinterpret_cast<uintptr_t>(in->control) & 7) != 0) return LCT_E_ARG;
+    if (in->buffer_meta != nullptr) {
+        if (!in->descriptor) return LCT_E_NULL;
+        if (in->max_free_regions <= 0 || in->max_free_regions > 4096
+            || (in->max_free_regions & (in->max_free_regions - 1)) != 0)
+            return LCT_E_ARG;
+        if (in->frees.count < 0 || in->frees.count > LCT_MAX_PENDING_FREES) return LCT_E_ARG;
+        for (int i = 0; i < in->frees.count; ++i)
+            if (in->frees.descriptor[i] == nullptr) return LCT_E_NULL;
+        const size_t list = static_cast<size_t>(in->max_free_regions) * 8;
+        if (list > lds) lds = list;
+    }
+    bk.control = in->control;
+    bk.epoch = in->epoch;
+    bk.counts = in->counts;
+    bk.blocks = in->blocks;
+    bk.descriptor = in->buffer_meta != nullptr ? in->descriptor : nullptr;
+    bk.buffer_meta = in->buffer_meta;
+    bk.max_free_regions = in->max_free_regions;
+    if (in->buffer_meta != nullptr) bk.frees = in->frees;
+    bk.lock_spins = lock_spins();
+    bk.polls = ready_polls();
+    return LCT_OK;
+}
+
+int32_t launch_pointwise_encode(
     const int32_t *encoded, const uint8_t *side, const int32_t *shifted_decode,
     const int32_t *center, const lct_overflow *overflow, const void *other, const float *alpha,
     const float *beta, const int32_t *partials, int64_t sample_size, const int32_t *base_encode,
     const int32_t *base_decode, int32_t *center_out, int32_t *shifted_decode_out,
     uint8_t *side_out, int32_t *encoded_out, uint8_t *extra_starts, int32_t *summaries,
     uint8_t *exponents, int64_t size, int64_t logical_numel, lct_geometry g, int32_t rare_length,
-    int32_t op, int32_t alpha_is_one, int32_t beta_is_one, hipStream_t stream) {
+    int32_t op, int32_t alpha_is_one, int32_t beta_is_one, const lct_bookkeeping *bookkeeping,
+    hipStream_t stream) {
     if (int32_t e = check_operand(encoded, side, shifted_decode, center, overflow)) return e;
     if (!other || !partials || !base_encode || !base_decode || !center_out || !shifted_decode_out
         || !side_out || !encoded_out || !extra_starts || !summaries || !exponents)
@@ -1471,16 +1561,55 @@ extern "C" int32_t lct_pointwise_encode(
                      overflow ? *overflow : lct_overflow{}, overflow != nullptr};
     const OpArgs args{alpha, beta, op, alpha_is_one, beta_is_one};
     const int32_t groups = sample_groups(sample_size);
-    const size_t lds = static_cast<size_t>(window_stage_bytes(g.fixed_words));
-    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&pointwise_encode_kernel),
-                                           lds))
+    size_t lds = static_cast<size_t>(window_stage_bytes(g.fixed_words));
+    KernelBookkeeping bk;
+    if (int32_t e = prepare_bookkeeping(bookkeeping, n_blocks, bk, lds)) return e;
+    const auto kernel = bk.control != nullptr ? pointwise_encode_kernel<true>
+                                              : pointwise_encode_kernel<false>;
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(kernel), lds))
         return static_cast<int32_t>(e);
-    hipLaunchKernelGGL(pointwise_encode_kernel, dim3(static_cast<uint32_t>(n_blocks)),
+    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(n_blocks)),
                        dim3(kLanes), lds, stream, a, static_cast<const uint16_t *>(other), args,
                        partials, groups, base_encode, base_decode, center_out,
                        shifted_decode_out, side_out, encoded_out, extra_starts, summaries,
-                       exponents, n_blocks, logical_numel, g.steps, g.fixed_words, rare_length);
+                       exponents, n_blocks, logical_numel, g.steps, g.fixed_words, rare_length,
+                       bk);
     return static_cast<int32_t>(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" int32_t lct_pointwise_encode(
+    const int32_t *encoded, const uint8_t *side, const int32_t *shifted_decode,
+    const int32_t *center, const lct_overflow *overflow, const void *other, const float *alpha,
+    const float *beta, const int32_t *partials, int64_t sample_size, const int32_t *base_encode,
+    const int32_t *base_decode, int32_t *center_out, int32_t *shifted_decode_out,
+    uint8_t *side_out, int32_t *encoded_out, uint8_t *extra_starts, int32_t *summaries,
+    uint8_t *exponents, int64_t size, int64_t logical_numel, lct_geometry g, int32_t rare_length,
+    int32_t op, int32_t alpha_is_one, int32_t beta_is_one, hipStream_t stream) {
+    return launch_pointwise_encode(encoded, side, shifted_decode, center, overflow, other, alpha,
+                                   beta, partials, sample_size, base_encode, base_decode,
+                                   center_out, shifted_decode_out, side_out, encoded_out,
+                                   extra_starts, summaries, exponents, size, logical_numel, g,
+                                   rare_length, op, alpha_is_one, beta_is_one, nullptr, stream);
+}
+
+extern "C" int32_t lct_pointwise_encode_fused(
+    const int32_t *encoded, const uint8_t *side, const int32_t *shifted_decode,
+    const int32_t *center, const lct_overflow *overflow, const void *other, const float *alpha,
+    const float *beta, const int32_t *partials, int64_t sample_size, const int32_t *base_encode,
+    const int32_t *base_decode, int32_t *center_out, int32_t *shifted_decode_out,
+    uint8_t *side_out, int32_t *encoded_out, uint8_t *extra_starts, int32_t *summaries,
+    uint8_t *exponents, int64_t size, int64_t logical_numel, lct_geometry g, int32_t rare_length,
+    int32_t op, int32_t alpha_is_one, int32_t beta_is_one, const lct_bookkeeping *bookkeeping,
+    hipStream_t stream) {
+    if (!bookkeeping) return LCT_E_NULL;
+    return launch_pointwise_encode(encoded, side, shifted_decode, center, overflow, other, alpha,
+                                   beta, partials, sample_size, base_encode, base_decode,
+                                   center_out, shifted_decode_out, side_out, encoded_out,
+                                   extra_starts, summaries, exponents, size, logical_numel, g,
+                                   rare_length, op, alpha_is_one, beta_is_one, bookkeeping,
+                                   stream);
 }
 
 extern "C" int32_t lct_dual_sample(const int32_t *a_encoded, const uint8_t *a_side,
@@ -1514,7 +1643,9 @@ extern "C" int32_t lct_dual_sample(const int32_t *a_encoded, const uint8_t *a_si
     return static_cast<int32_t>(hipGetLastError());
 }
 
-extern "C" int32_t lct_dual_encode(
+namespace {
+
+int32_t launch_dual_encode(
     const int32_t *a_encoded, const uint8_t *a_side, const int32_t *a_shifted_decode,
     const int32_t *a_center, const lct_overflow *a_overflow, const int32_t *b_encoded,
     const uint8_t *b_side, const int32_t *b_shifted_decode, const int32_t *b_center,
@@ -1522,7 +1653,8 @@ extern "C" int32_t lct_dual_encode(
     int64_t sample_size, const int32_t *base_encode, const int32_t *base_decode,
     int32_t *center_out, int32_t *shifted_decode_out, uint8_t *side_out, int32_t *encoded_out,
     uint8_t *extra_starts, int32_t *summaries, uint8_t *exponents, int64_t size,
-    int64_t logical_numel, lct_geometry g, int32_t rare_length, hipStream_t stream) {
+    int64_t logical_numel, lct_geometry g, int32_t rare_length,
+    const lct_bookkeeping *bookkeeping, hipStream_t stream) {
     if (int32_t e = check_operand(a_encoded, a_side, a_shifted_decode, a_center, a_overflow))
         return e;
     if (int32_t e = check_operand(b_encoded, b_side, b_shifted_decode, b_center, b_overflow))
@@ -1549,14 +1681,54 @@ extern "C" int32_t lct_dual_encode(
     // Rows 0..2 of every stream start in registers (W = 2 or 3 never occurs in
     // a reference geometry).
     if (g.fixed_words <= kRegisterRows) return LCT_E_GEOMETRY;
-    const size_t lds = 2 * static_cast<size_t>(register_stage_bytes(g.fixed_words));
-    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&dual_encode_kernel),
-                                           lds))
+    size_t lds = 2 * static_cast<size_t>(register_stage_bytes(g.fixed_words));
+    KernelBookkeeping bk;
+    if (int32_t e = prepare_bookkeeping(bookkeeping, n_blocks, bk, lds)) return e;
+    const auto kernel = bk.control != nullptr ? dual_encode_kernel<true>
+                                              : dual_encode_kernel<false>;
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(kernel), lds))
         return static_cast<int32_t>(e);
-    hipLaunchKernelGGL(dual_encode_kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes),
+    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes),
                        lds, stream, a, b, alpha, partials, sample_groups(sample_size),
                        base_encode, base_decode, center_out, shifted_decode_out, side_out,
                        encoded_out, extra_starts, summaries, exponents, n_blocks, logical_numel,
-                       g.steps, g.fixed_words, rare_length);
+                       g.steps, g.fixed_words, rare_length, bk);
     return static_cast<int32_t>(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" int32_t lct_dual_encode(
+    const int32_t *a_encoded, const uint8_t *a_side, const int32_t *a_shifted_decode,
+    const int32_t *a_center, const lct_overflow *a_overflow, const int32_t *b_encoded,
+    const uint8_t *b_side, const int32_t *b_shifted_decode, const int32_t *b_center,
+    const lct_overflow *b_overflow, const float *alpha, const int32_t *partials,
+    int64_t sample_size, const int32_t *base_encode, const int32_t *base_decode,
+    int32_t *center_out, int32_t *shifted_decode_out, uint8_t *side_out, int32_t *encoded_out,
+    uint8_t *extra_starts, int32_t *summaries, uint8_t *exponents, int64_t size,
+    int64_t logical_numel, lct_geometry g, int32_t rare_length, hipStream_t stream) {
+    return launch_dual_encode(a_encoded, a_side, a_shifted_decode, a_center, a_overflow,
+                              b_encoded, b_side, b_shifted_decode, b_center, b_overflow, alpha,
+                              partials, sample_size, base_encode, base_decode, center_out,
+                              shifted_decode_out, side_out, encoded_out, extra_starts, summaries,
+                              exponents, size, logical_numel, g, rare_length, nullptr, stream);
+}
+
+extern "C" int32_t lct_dual_encode_fused(
+    const int32_t *a_encoded, const uint8_t *a_side, const int32_t *a_shifted_decode,
+    const int32_t *a_center, const lct_overflow *a_overflow, const int32_t *b_encoded,
+    const uint8_t *b_side, const int32_t *b_shifted_decode, const int32_t *b_center,
+    const lct_overflow *b_overflow, const float *alpha, const int32_t *partials,
+    int64_t sample_size, const int32_t *base_encode, const int32_t *base_decode,
+    int32_t *center_out, int32_t *shifted_decode_out, uint8_t *side_out, int32_t *encoded_out,
+    uint8_t *extra_starts, int32_t *summaries, uint8_t *exponents, int64_t size,
+    int64_t logical_numel, lct_geometry g, int32_t rare_length,
+    const lct_bookkeeping *bookkeeping, hipStream_t stream) {
+    if (!bookkeeping) return LCT_E_NULL;
+    return launch_dual_encode(a_encoded, a_side, a_shifted_decode, a_center, a_overflow,
+                              b_encoded, b_side, b_shifted_decode, b_center, b_overflow, alpha,
+                              partials, sample_size, base_encode, base_decode, center_out,
+                              shifted_decode_out, side_out, encoded_out, extra_starts, summaries,
+                              exponents, size, logical_numel, g, rare_length, bookkeeping,
+                              stream);
 }

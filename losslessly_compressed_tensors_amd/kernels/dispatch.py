@@ -246,6 +246,28 @@ def control_array(device: torch.device, n_blocks: int) -> torch.Tensor:
         return array
 
 
+def bookkeeping(device, n_blocks, counts, blocks_out, buffer=None, descriptor=None, frees=()):
+    """The ``lct_bookkeeping`` record of a fused update encoder launch on the
+    current stream of ``device``: its control array and a fresh epoch, the
+    totals and block metadata outputs and, for a shared ``buffer``, the
+    reservation's descriptor and the deferred ``frees``."""
+    control = control_array(device, n_blocks)
+    record = hip.Bookkeeping()
+    record.control = _ptr(control)
+    record.control_words = int(control.numel())
+    record.epoch = _next_fused_epoch()
+    record.counts = _ptr(counts)
+    record.blocks = _ptr(blocks_out)
+    if buffer is not None:
+        record.descriptor = _ptr(descriptor)
+        record.buffer_meta = _ptr(buffer.storage)
+        record.max_free_regions = int(buffer.max_free_regions)
+        record.frees.count = len(frees)
+        for i, freed in enumerate(frees):
+            record.frees.descriptor[i] = freed.data_ptr()
+    return record
+
+
 def encode_fused(source, side, encoded, sample_size, encode_table, decode_table, center,
                  shifted_decode, sample_values, extra_starts, summaries, blocks_out, counts,
                  size, *, precomputed, logical_numel, block_symbols, lanes, steps, fixed_words,
@@ -463,20 +485,27 @@ def pointwise_encode(encoded, sign_mantissa, shifted_decode, center, other, alph
                      side_out, encoded_out, extra_starts, summaries, exponents, size, *,
                      rare_length, logical_numel, block_symbols, lanes, steps, fixed_words, op,
                      alpha_is_one, beta_is_one, sample_size,
-                     overflow: FallbackStorage | None = None) -> None:
+                     overflow: FallbackStorage | None = None, record=None) -> None:
     """Decode + op + re-encode in one pass: the single-pass form of the
     compressed-output ``pointwise_dense`` launch followed by the encoder
-    launch of ``encode_components(precomputed=True)``."""
+    launch of ``encode_components(precomputed=True)``; with a ``record``
+    (``bookkeeping()``) also the prefix scan and reservation of
+    ``encode_components`` in the same launch (``lct_pointwise_encode_fused``)."""
     _require_device(encoded, sign_mantissa, other, partials, encoded_out)
     geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
     ov = overflow.as_overflow() if overflow is not None else None
-    hip.call("lct_pointwise_encode", _ptr(encoded), _ptr(sign_mantissa), _ptr(shifted_decode),
-             _ptr(center), ov if ov is None else hip.ctypes.byref(ov), _ptr(other), _ptr(alpha),
-             _ptr(beta), _ptr(partials), int(sample_size), _ptr(base_encode), _ptr(base_decode),
-             _ptr(center_out), _ptr(shifted_decode_out), _ptr(side_out), _ptr(encoded_out),
-             _ptr(extra_starts), _ptr(summaries), _ptr(exponents), int(size),
-             int(logical_numel), geometry, int(rare_length), int(op), int(bool(alpha_is_one)),
-             int(bool(beta_is_one)), _stream(encoded))
+    args = [_ptr(encoded), _ptr(sign_mantissa), _ptr(shifted_decode), _ptr(center),
+            ov if ov is None else hip.ctypes.byref(ov), _ptr(other), _ptr(alpha), _ptr(beta),
+            _ptr(partials), int(sample_size), _ptr(base_encode), _ptr(base_decode),
+            _ptr(center_out), _ptr(shifted_decode_out), _ptr(side_out), _ptr(encoded_out),
+            _ptr(extra_starts), _ptr(summaries), _ptr(exponents), int(size), int(logical_numel),
+            geometry, int(rare_length), int(op), int(bool(alpha_is_one)),
+            int(bool(beta_is_one))]
+    if record is None:
+        hip.call("lct_pointwise_encode", *args, _stream(encoded))
+    else:
+        hip.call("lct_pointwise_encode_fused", *args, hip.ctypes.byref(record),
+                 _stream(encoded))
 
 
 def dual_sample(a_encoded, a_sign_mantissa, a_shifted_decode, a_center, a_storage, b_encoded,
@@ -502,19 +531,24 @@ def dual_encode(a_encoded, a_sign_mantissa, a_shifted_decode, a_center, a_storag
                 b_sign_mantissa, b_shifted_decode, b_center, b_storage, alpha, partials,
                 base_encode, base_decode, center_out, shifted_decode_out, side_out,
                 encoded_out, extra_starts, summaries, exponents, size, *, rare_length,
-                logical_numel, block_symbols, lanes, steps, fixed_words, sample_size) -> None:
+                logical_numel, block_symbols, lanes, steps, fixed_words, sample_size,
+                record=None) -> None:
     """Decode A and B, ``fma(a, alpha, b)`` and re-encode in one pass: the
     single-pass form of the compressed-output ``dual_mapped`` launch followed
-    by the encoder launch of ``encode_components(precomputed=True)``."""
+    by the encoder launch of ``encode_components(precomputed=True)``; with a
+    ``record`` also the prefix scan and reservation (``lct_dual_encode_fused``)."""
     _require_device(a_encoded, b_encoded, alpha, partials, encoded_out)
     geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
-    hip.call("lct_dual_encode", _ptr(a_encoded), _ptr(a_sign_mantissa), _ptr(a_shifted_decode),
-             _ptr(a_center), _byref(a_storage), _ptr(b_encoded), _ptr(b_sign_mantissa),
-             _ptr(b_shifted_decode), _ptr(b_center), _byref(b_storage), _ptr(alpha),
-             _ptr(partials), int(sample_size), _ptr(base_encode), _ptr(base_decode),
-             _ptr(center_out), _ptr(shifted_decode_out), _ptr(side_out), _ptr(encoded_out),
-             _ptr(extra_starts), _ptr(summaries), _ptr(exponents), int(size),
-             int(logical_numel), geometry, int(rare_length), _stream(a_encoded))
+    args = [_ptr(a_encoded), _ptr(a_sign_mantissa), _ptr(a_shifted_decode), _ptr(a_center),
+            _byref(a_storage), _ptr(b_encoded), _ptr(b_sign_mantissa), _ptr(b_shifted_decode),
+            _ptr(b_center), _byref(b_storage), _ptr(alpha), _ptr(partials), int(sample_size),
+            _ptr(base_encode), _ptr(base_decode), _ptr(center_out), _ptr(shifted_decode_out),
+            _ptr(side_out), _ptr(encoded_out), _ptr(extra_starts), _ptr(summaries),
+            _ptr(exponents), int(size), int(logical_numel), geometry, int(rare_length)]
+    if record is None:
+        hip.call("lct_dual_encode", *args, _stream(a_encoded))
+    else:
+        hip.call("lct_dual_encode_fused", *args, hip.ctypes.byref(record), _stream(a_encoded))
 
 
 # ---------------------------------------------------------------------------

@@ -60,6 +60,23 @@ class PendingFrees(ctypes.Structure):
     ]
 
 
+class Bookkeeping(ctypes.Structure):
+    """``lct_bookkeeping``: the in-launch overflow bookkeeping of the fused
+    update encoders."""
+
+    _fields_ = [
+        ("control", _ptr),
+        ("control_words", _c_int64),
+        ("epoch", ctypes.c_uint32),
+        ("counts", _ptr),
+        ("blocks", _ptr),
+        ("descriptor", _ptr),
+        ("buffer_meta", _ptr),
+        ("max_free_regions", _c_int32),
+        ("frees", PendingFrees),
+    ]
+
+
 # name -> argument types (all entry points return int32).
 _SIGNATURES = {
     "lct_estimate_and_shift_tables": [_ptr, _c_int32, _c_int64, _c_int64, _ptr, _ptr, _ptr, _ptr,
@@ -89,6 +106,10 @@ _SIGNATURES = {
                              _ptr, _c_int64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
                              _c_int64, _c_int64, Geometry, _c_int32, _c_int32, _c_int32, _c_int32,
                              _ptr],
+    "lct_pointwise_encode_fused": [_ptr, _ptr, _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr,
+                                   _ptr, _ptr, _c_int64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
+                                   _ptr, _ptr, _c_int64, _c_int64, Geometry, _c_int32, _c_int32,
+                                   _c_int32, _c_int32, ctypes.POINTER(Bookkeeping), _ptr],
     "lct_dual_sample": [_ptr, _ptr, _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _ptr,
                         _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _c_int64, _c_int64,
                         Geometry, _c_int32, _c_int64, _ptr, _ptr, _ptr],
@@ -96,6 +117,10 @@ _SIGNATURES = {
                         _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _c_int64, _ptr, _ptr, _ptr,
                         _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64, _c_int64, Geometry,
                         _c_int32, _ptr],
+    "lct_dual_encode_fused": [_ptr, _ptr, _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr,
+                              _ptr, _ptr, ctypes.POINTER(Overflow), _ptr, _ptr, _c_int64, _ptr,
+                              _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64, _c_int64,
+                              Geometry, _c_int32, ctypes.POINTER(Bookkeeping), _ptr],
     "lct_allocate_compact": [_ptr, _ptr, _ptr, _ptr, _ptr, _c_int32, _ptr, _ptr, _ptr,
                              ctypes.POINTER(PendingFrees), _ptr, ctypes.c_uint64, _c_int64,
                              _c_int64, Geometry, _c_int32, _ptr],

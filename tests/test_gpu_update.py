@@ -463,3 +463,70 @@ def test_weight_update_sequence_single_pass():
         assert_matches_oracle(tensor.x, state)
     tensor.free()
     verify_buffer(buffer)
+
+
+# The fused updates make their overflow bookkeeping inside the encoder launch
+# (lct_pointwise_encode_fused / lct_dual_encode_fused) whenever the block count
+# allows; the separate launches (lct_pointwise_encode / lct_dual_encode, then
+# lct_allocate_compact or lct_prefix_allocate + lct_compact_extra) serve the
+# rest.  Both must store the oracle's tensor.
+SEPARATE = [("fused", None), ("separate", 0)]
+
+
+@pytest.mark.parametrize("case", [CASES[0], CASES[1], CASES[4]],
+                         ids=[CASES[0][0], CASES[1][0], CASES[4][0]])
+@pytest.mark.parametrize("path", SEPARATE, ids=[p[0] for p in SEPARATE])
+@pytest.mark.parametrize("buffered", [False, True], ids=["private", "buffered"])
+def test_bookkeeping_paths_store_the_oracle_tensor(case, path, buffered, monkeypatch):
+    require_gpu()
+    name, dist, make_a, make_b = case
+    path_name, limit = path
+    print(f"case bookkeeping {name} {path_name} buffered={buffered}", flush=True)
+    if limit is not None:
+        monkeypatch.setattr(dispatch, "MAX_CODEC_BLOCKS", limit)
+    op = OPS[2]
+    _, code, call, alpha, beta, alpha_is_one, beta_is_one = op
+    a, b = make_a(), make_b()
+    buffer = TensorBuffer(8 << 20, max_free_regions=64, device="cuda") if buffered else None
+    host = oracle.Buffer(8 << 20, 64) if buffered else None
+    ct = compress(a.cuda(), dist, buffer=buffer)
+    o = oracle_compress(a, dist, buffer=host)
+    # A deferred free rides on the update's reservation on both paths.
+    spare = compress(b.cuda(), dist, buffer=buffer)
+    spare_oracle = oracle_compress(b, dist, buffer=host)
+    spare.free()
+    if buffered:
+        host.free(spare_oracle.descriptor)
+    result = call(ct, b.cuda(), dense_output=False, buffer=buffer)
+    side, exponents = oracle.pointwise(o, bits_of(b), code, alpha, beta, alpha_is_one,
+                                       beta_is_one, policy=1)
+    expected = oracle_from_components(side, exponents, dist, buffer=host)
+    assert_matches_oracle(result, expected)
+    if buffered:
+        result.free()
+        ct.free()
+        verify_buffer(buffer)
+
+
+@pytest.mark.parametrize("case", [DUAL_CASES[1], DUAL_CASES[2]],
+                         ids=[DUAL_CASES[1][0], DUAL_CASES[2][0]])
+@pytest.mark.parametrize("path", SEPARATE, ids=[p[0] for p in SEPARATE])
+@pytest.mark.parametrize("buffered", [False, True], ids=["private", "buffered"])
+def test_dual_bookkeeping_paths_store_the_oracle_tensor(case, path, buffered, monkeypatch):
+    require_gpu()
+    path_name, limit = path
+    print(f"case dual bookkeeping {case[0]} {path_name} buffered={buffered}", flush=True)
+    if limit is not None:
+        monkeypatch.setattr(dispatch, "MAX_CODEC_BLOCKS", limit)
+    buffer = TensorBuffer(8 << 20, max_free_regions=64, device="cuda") if buffered else None
+    host = oracle.Buffer(8 << 20, 64) if buffered else None
+    ca, cb, oa, ob = _dual_operands(case, buffer, host)
+    result = a_compA_add_compB(ca, _scalar(ALPHA), cb, dense_output=False, buffer=buffer)
+    side, exponents = oracle.dual(oa, ob, ALPHA, policy=1)
+    expected = oracle_from_components(side, exponents, ca.distribution, buffer=host)
+    assert_matches_oracle(result, expected)
+    if buffered:
+        result.free()
+        cb.free()
+        ca.free()
+        verify_buffer(buffer)
