@@ -171,3 +171,46 @@ def test_encode_fused_rejects_bad_arguments_before_launch(lib):
     missing = hip.PendingFrees()
     missing.count = 1
     assert call(meta=fake, frees=ctypes.byref(missing)) == LCT_E_NULL
+
+
+def test_fused_update_encoders_reject_bad_bookkeeping_before_launch(lib):
+    """lct_pointwise_encode_fused and lct_dual_encode_fused check their
+    bookkeeping record (control array, epoch, buffer, frees) before anything
+    is launched (the fake pointers are never dereferenced)."""
+    fake = ctypes.c_void_p(1 << 20)
+    geometry = hip.Geometry(65536, 256, 256, 25)
+    size = 4 * 65536
+
+    def record(words=64 + 4, epoch=7, control=1 << 20, meta=None, regions=256, frees=0):
+        r = hip.Bookkeeping()
+        r.control = control
+        r.control_words = words
+        r.epoch = epoch
+        r.counts = 1 << 20
+        r.blocks = 1 << 20
+        r.descriptor = 1 << 20
+        r.buffer_meta = meta
+        r.max_free_regions = regions
+        r.frees.count = frees
+        return r
+
+    def pointwise(r):
+        return lib.lct_pointwise_encode_fused(
+            fake, fake, fake, fake, None, fake, None, None, fake, 4096, fake, fake, fake, fake,
+            fake, fake, fake, fake, fake, size, size, geometry, 5, 0, 0, 1,
+            None if r is None else ctypes.byref(r), None)
+
+    def dual(r):
+        return lib.lct_dual_encode_fused(
+            fake, fake, fake, fake, None, fake, fake, fake, fake, None, fake, fake, 4096, fake,
+            fake, fake, fake, fake, fake, fake, fake, fake, size, size, geometry, 5,
+            None if r is None else ctypes.byref(r), None)
+
+    for call in (pointwise, dual):
+        assert call(None) == LCT_E_NULL                                  # no record
+        assert call(record(epoch=0)) == LCT_E_ARG                        # 0 matches a fresh array
+        assert call(record(words=64 + 3)) == LCT_E_SIZE                  # no word for the last block
+        assert call(record(control=(1 << 20) + 4)) == LCT_E_ARG          # not 8-byte aligned
+        assert call(record(meta=1 << 20, regions=100)) == LCT_E_ARG      # not a power of two
+        assert call(record(meta=1 << 20, frees=hip.MAX_PENDING_FREES + 1)) == LCT_E_ARG
+        assert call(record(meta=1 << 20, frees=1)) == LCT_E_NULL         # a missing descriptor
