@@ -312,7 +312,7 @@ def time_update(args, torch, device):
             "algorithmic_bytes": fused_alg,
             "achieved": round(fused_alg / (fused_ms * 1e-3) / 1e9, 1),
             "frac": round(fused_alg / (fused_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-            "traffic": measured_traffic("pointwise_encode_kernel", nb),
+            "traffic": measured_traffic("pointwise_encode_kernel<false>", nb),
         },
     }
 
@@ -411,7 +411,7 @@ def time_weight_update(args, torch, device):
             "algorithmic_bytes": fused_alg,
             "achieved": round(fused_alg / (fused_ms * 1e-3) / 1e9, 1),
             "frac": round(fused_alg / (fused_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-            "traffic": measured_traffic("dual_encode_kernel", nb),
+            "traffic": measured_traffic("dual_encode_kernel<false>", nb),
         },
     }
 
