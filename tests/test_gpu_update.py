@@ -28,7 +28,7 @@ from gpu_util import (
 from losslessly_compressed_tensors_amd.codec.decode import overlay_of, shifted_decode_table
 from losslessly_compressed_tensors_amd.comp_format import DistType, Distribution, NoiseLevel
 from losslessly_compressed_tensors_amd.compression.huffman_tables import get_distribution_tables
-from losslessly_compressed_tensors_amd.kernels import dispatch
+from losslessly_compressed_tensors_amd.kernels import dispatch, hip
 from losslessly_compressed_tensors_amd.LCTensor import LCTTensor
 from losslessly_compressed_tensors_amd.operations import (
     a_compA_add_B,
@@ -39,7 +39,10 @@ from losslessly_compressed_tensors_amd.operations import (
     compress,
     decompress,
 )
-from losslessly_compressed_tensors_amd.tensor_buffer import TensorBuffer, verify_buffer
+from losslessly_compressed_tensors_amd.tensor_buffer import (
+    FAIL_INCOMPLETE, STATUS_INCOMPLETE, BufferReservationError, TensorBuffer,
+    _free_regions_snapshot, verify_buffer,
+)
 
 pytestmark = pytest.mark.gpu
 
@@ -530,3 +533,52 @@ def test_dual_bookkeeping_paths_store_the_oracle_tensor(case, path, buffered, mo
         cb.free()
         ca.free()
         verify_buffer(buffer)
+
+
+@pytest.mark.parametrize("kind", ["pointwise", "dual"])
+def test_update_bookkeeping_that_stops_waiting_marks_the_result_incomplete(kind):
+    """The fused update's workgroup 0 gives up polling the block summaries (one
+    poll round, 3000 blocks: more than the device holds at once, so later
+    blocks have not run when workgroup 0 finishes its own): the buffered result
+    reads status 7 and raises at memory_size(), its region comes back on free,
+    the private form raises at its sync, and with the default bounds both forms
+    store the oracle-checked result again."""
+    require_gpu()
+    print(f"case update incomplete {kind}", flush=True)
+    dist = Distribution(DistType.GAUSSIAN)
+    g = torch.Generator(device="cuda").manual_seed(52)
+    x = torch.randn(3000 * 32768, generator=g, device="cuda").to(torch.bfloat16)
+    y = (torch.randn(3000 * 32768, generator=g, device="cuda") * 0.5).to(torch.bfloat16)
+    ca = compress(x, dist)
+    cb = compress(y, dist) if kind == "dual" else None
+    alpha = _scalar(ALPHA)
+
+    def update(buffer):
+        if kind == "dual":
+            return a_compA_add_compB(ca, alpha, cb, dense_output=False, buffer=buffer)
+        return a_compA_add_B(ca, alpha, y, dense_output=False, buffer=buffer)
+
+    expected = decompress(update(None)).view(torch.int16)
+    buffer = TensorBuffer(16 << 20, device="cuda")
+    before = _free_regions_snapshot(buffer)
+    hip.call("lct_set_wait_limits", 0, 1)
+    try:
+        result = update(buffer)
+        torch.cuda.synchronize()
+        with pytest.raises(RuntimeError, match="gave up"):
+            update(None)
+    finally:
+        hip.call("lct_set_wait_limits", 0, 0)
+    assert int(result.fallback_descriptor[2].item()) == STATUS_INCOMPLETE
+    with pytest.raises(BufferReservationError, match="status 7"):
+        result.memory_size()
+    assert buffer.failures() & FAIL_INCOMPLETE
+    result.free()
+    buffer._flush_frees()
+    assert _free_regions_snapshot(buffer) == before
+    assert torch.equal(decompress(update(None)).view(torch.int16), expected)
+    buffer.reset()
+    ok = update(buffer)
+    assert torch.equal(decompress(ok).view(torch.int16), expected)
+    ok.free()
+    verify_buffer(buffer)
