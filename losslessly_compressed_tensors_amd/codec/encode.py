@@ -3,16 +3,18 @@
 Host sequencing of ``LCT/codec/encode.py:22-218`` on the gfx950 library.  A
 compress (the center sampled from the input) is two launches:
 
-1. ``lct_encode_fused``: sampling workgroups publish the center's partial
-   sums; every encoding workgroup reduces them to the center, shifts the
-   tables, splits fields, writes its block's fixed payload and per-stream
-   overflow starts and publishes its block's overflow summary; one
-   bookkeeping workgroup scans the summaries into the block metadata and the
-   overflow-block list and, for a shared ``TensorBuffer``, applies the
+1. ``lct_encode_fused``, one workgroup per codec block: the first 64 first
+   publish the center's partial sums; every workgroup reduces them to the
+   center, shifts the tables, splits fields, writes its block's fixed payload
+   and per-stream overflow starts and publishes its block's overflow summary;
+   workgroup 0, after its block, scans the summaries into the block metadata
+   and the overflow-block list and, for a shared ``TensorBuffer``, applies the
    buffer's deferred frees and reserves the overflow region;
 2. private storage only: one device->host sync reads the overflow totals so
    exact-size lane/start/tail arrays can be allocated (as the reference does);
-3. ``lct_compact_extra`` writes the per-block overflow entries and tails.
+3. ``lct_compact_extra`` (one workgroup per block, from the block metadata)
+   writes the per-block overflow entries and tails (``finish_fused``, shared
+   with the fused pointwise updates).
 
 With a given center (``lct_shift_tables`` then ``lct_encode``), the
 bookkeeping runs as its own launches after the encoder (``finish_encode``).
