@@ -571,7 +571,8 @@ def main() -> int:
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the codec path has no multi-GPU form here "
-              "(see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+              "(codec blocks are independent; a sharded tensor would need only its center "
+              "and its overflow totals exchanged). Run with --gpus 1.", file=sys.stderr)
         return 2
 
     import torch
