@@ -17,15 +17,35 @@ namespace {
 // at 65536), which bounds the array at about 2.2 MiB per GPU.
 constexpr int64_t kNoAllocMaxBlocks = 8192;
 
-// Layout of the array: the ready word, the partial sums (int32[2 * 64]), the
-// summaries (int32[5 * nb + 1]) and the extra starts (uint8[nb * 256]), each
-// at a 256-byte boundary.
+constexpr size_t round_up_256(size_t bytes) { return (bytes + 255) / 256 * 256; }
+
+// Layout of the array: the ready word, the partial sums (int32[2 * 64]: a
+// kept-exponent sum and a count per 64-sample group), the summaries
+// (int32[5 * nb + 1]) and the extra starts (uint8[nb * 256]), each at a
+// 256-byte boundary and each sized for its largest use, so that no region's
+// writes reach another's (the encoders read the partial sums while finished
+// blocks store their summaries).
+constexpr size_t kReadyBytes = round_up_256(sizeof(uint64_t));
+constexpr size_t kPartialsBytes = round_up_256(2 * kControlPartials * sizeof(int32_t));
+constexpr size_t kSummariesBytes = round_up_256((5 * kNoAllocMaxBlocks + 1) * sizeof(int32_t));
+constexpr size_t kExtraBytes = round_up_256(kNoAllocMaxBlocks * kLanes);
 constexpr size_t kReadyOffset = 0;
-constexpr size_t kPartialsOffset = 256;
-constexpr size_t kSummariesOffset = kPartialsOffset + 256;
-constexpr size_t kSummariesBytes = ((5 * kNoAllocMaxBlocks + 1) * 4 + 255) / 256 * 256;
+constexpr size_t kPartialsOffset = kReadyOffset + kReadyBytes;
+constexpr size_t kSummariesOffset = kPartialsOffset + kPartialsBytes;
 constexpr size_t kExtraOffset = kSummariesOffset + kSummariesBytes;
-constexpr size_t kScratchBytes = kExtraOffset + kNoAllocMaxBlocks * kLanes;
+constexpr size_t kScratchBytes = kExtraOffset + kExtraBytes;
+
+static_assert(kMaxSamples / kSampleGroup <= kControlPartials,
+              "the sampler writes two int32 per group for at most kControlPartials groups");
+static_assert(kPartialsOffset - kReadyOffset >= sizeof(uint64_t), "ready word");
+static_assert(kSummariesOffset - kPartialsOffset >= 2 * kControlPartials * sizeof(int32_t),
+              "partial sums");
+static_assert(kExtraOffset - kSummariesOffset >= (5 * kNoAllocMaxBlocks + 1) * sizeof(int32_t),
+              "summaries");
+static_assert(kScratchBytes - kExtraOffset >= kNoAllocMaxBlocks * kLanes, "extra starts");
+static_assert(kPartialsOffset % 256 == 0 && kSummariesOffset % 256 == 0
+                  && kExtraOffset % 256 == 0,
+              "regions start at 256-byte boundaries");
 
 }  // namespace
 

@@ -39,6 +39,12 @@ def _gaussian(seed, n):
     return x.view(torch.int16).cuda()
 
 
+def _gaussian_device(seed, n):
+    """Large inputs drawn on the device (the CPU draw of 2^28 values is slow)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return torch.randn(n, generator=g, device="cuda").to(torch.bfloat16).view(torch.int16)
+
+
 def _outputs(n, dist):
     B, L, S, W = geometry(dist)
     nb = -(-n // B)
@@ -104,7 +110,11 @@ def _same(a, b, written_words):
 @pytest.mark.parametrize("dist,first,second", [
     (SPARSE, lambda: _patterns(1, 37 * 65536 + 999), lambda: _patterns(2, 5 * 65536 + 3)),
     (GAUSS, lambda: _gaussian(3, 300 * 32768 + 17), lambda: _gaussian(4, 3000)),
-], ids=["overflowing-sparse", "gaussian"])
+    # The size limit: 8192 blocks run in several rounds of workgroups, so
+    # blocks that finish (and store their summaries) precede blocks that start
+    # (and read the sampler's partial sums); the working regions must not meet.
+    (GAUSS, lambda: _gaussian_device(5, 8192 * 32768), lambda: _gaussian_device(6, 5000 * 32768 - 9)),
+], ids=["overflowing-sparse", "gaussian", "gaussian-8192-blocks"])
 def test_no_alloc_compress_equals_the_sequence_twice(dist, first, second):
     require_gpu()
     print(f"case no-alloc compress {dist.family.value}", flush=True)
