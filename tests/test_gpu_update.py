@@ -535,6 +535,75 @@ def test_dual_bookkeeping_paths_store_the_oracle_tensor(case, path, buffered, mo
         verify_buffer(buffer)
 
 
+def _scattered_patterns(n_blocks, block_symbols, seed, std=1.0):
+    """A Gaussian tensor of ``n_blocks`` codec blocks (the last one ragged)
+    with 4096 random bit patterns in a dozen scattered blocks and in the last
+    one, so that streams overflow early, late and at the very end."""
+    n = n_blocks * block_symbols - 77
+    x = _gaussian((n,), seed, std)
+    bits = x.view(torch.int16).numpy()
+    rng = np.random.default_rng(seed)
+    chosen = sorted(set(rng.choice(n_blocks - 1, 12, replace=False).tolist()) | {n_blocks - 1})
+    for k in chosen:
+        lo = k * block_symbols + int(rng.integers(0, block_symbols - 8192))
+        bits[lo:lo + 4096] = rng.integers(-32768, 32768, 4096, dtype=np.int16)
+    return x
+
+
+@pytest.mark.parametrize("buffered", [False, True], ids=["private", "buffered"])
+def test_fused_update_beyond_one_summary_pass(buffered):
+    """lct_pointwise_encode_fused over 3000 codec blocks: workgroup 0 polls the
+    block summaries in several passes of 1024 and carries the totals across
+    them, with blocks still running when it starts; every stored field equals
+    the oracle's."""
+    require_gpu()
+    print(f"case fused update 3000 blocks buffered={buffered}", flush=True)
+    dist = Distribution(DistType.GAUSSIAN)
+    a = _scattered_patterns(3000, 32768, 60)
+    b = _gaussian((a.numel(),), 61, 0.5)
+    buffer = TensorBuffer(32 << 20, max_free_regions=64, device="cuda") if buffered else None
+    host = oracle.Buffer(32 << 20, 64) if buffered else None
+    ct = compress(a.cuda(), dist, buffer=buffer)
+    o = oracle_compress(a, dist, buffer=host)
+    assert o.n_blocks == 3000 and o.counts[0] > 0
+    result = a_compA_add_B(ct, _scalar(ALPHA), b.cuda(), dense_output=False, buffer=buffer)
+    side, exponents = oracle.pointwise(o, bits_of(b), oracle.OP_SCALAR_MUL_ADD, ALPHA, policy=1)
+    expected = oracle_from_components(side, exponents, dist, buffer=host)
+    assert expected.counts[0] > 0
+    assert expected.blocks[expected.n_blocks - 1] > 0, "the last block overflows"
+    assert_matches_oracle(result, expected)
+    if buffered:
+        result.free()
+        ct.free()
+        verify_buffer(buffer)
+
+
+@pytest.mark.parametrize("buffered", [False, True], ids=["private", "buffered"])
+def test_fused_dual_update_beyond_one_summary_pass(buffered):
+    """lct_dual_encode_fused over 3000 codec blocks, both operands overflowing
+    in scattered blocks: every stored field equals the oracle's."""
+    require_gpu()
+    print(f"case fused dual 3000 blocks buffered={buffered}", flush=True)
+    dist = Distribution(DistType.GAUSSIAN)
+    a = _scattered_patterns(3000, 32768, 62, 1e-3)
+    b = _scattered_patterns(3000, 32768, 63, 0.02)
+    buffer = TensorBuffer(64 << 20, max_free_regions=64, device="cuda") if buffered else None
+    host = oracle.Buffer(64 << 20, 64) if buffered else None
+    ca, cb = compress(a.cuda(), dist, buffer=buffer), compress(b.cuda(), dist, buffer=buffer)
+    oa, ob = oracle_compress(a, dist, buffer=host), oracle_compress(b, dist, buffer=host)
+    assert oa.counts[0] > 0 and ob.counts[0] > 0
+    result = a_compA_add_compB(ca, _scalar(ALPHA), cb, dense_output=False, buffer=buffer)
+    side, exponents = oracle.dual(oa, ob, ALPHA, policy=1)
+    expected = oracle_from_components(side, exponents, dist, buffer=host)
+    assert expected.blocks[expected.n_blocks - 1] > 0, "the last block overflows"
+    assert_matches_oracle(result, expected)
+    if buffered:
+        result.free()
+        cb.free()
+        ca.free()
+        verify_buffer(buffer)
+
+
 @pytest.mark.parametrize("kind", ["pointwise", "dual"])
 def test_update_bookkeeping_that_stops_waiting_marks_the_result_incomplete(kind):
     """The fused update's workgroup 0 gives up polling the block summaries (one
