@@ -238,7 +238,13 @@ int32_t lct_allocate_compact(const void *source, int32_t *summaries, int32_t *co
  * sample_size as lct_sample_center; sample_values may be NULL.  A bounded
  * device-side wait that gives up marks the tensor incomplete instead of
  * hanging: counts[3] = 1 and, with a buffer, status 7 and the failure word's
- * LCT_FAIL_INCOMPLETE bit.  source, side and encoded 16-byte aligned. */
+ * LCT_FAIL_INCOMPLETE bit.  source, side and encoded 16-byte aligned.
+ * host_totals (private storage only, else NULL): uint64[2] in pinned host
+ * memory, 8-byte aligned.  Once the bookkeeping has the totals, word 0
+ * becomes epoch << 32 | entries | incomplete << 31 and word 1 epoch << 32 |
+ * tail bytes (system-scope stores), so a host that sizes the exact overflow
+ * arrays (the reference's sync on counts, LCT/codec/encode.py:137-171) can
+ * poll them instead of waiting for the launch to end. */
 int32_t lct_encode_fused(const void *source, uint8_t *side, int32_t *encoded,
                          int64_t sample_size, const int32_t *base_encode,
                          const int32_t *base_decode, int32_t *center_out,
@@ -247,8 +253,8 @@ int32_t lct_encode_fused(const void *source, uint8_t *side, int32_t *encoded,
                          int32_t *counts, uint64_t *control, int64_t control_words,
                          uint32_t epoch, int32_t *descriptor, int32_t *buffer_meta,
                          int32_t max_free_regions, const lct_pending_frees *frees,
-                         int64_t size, int64_t logical_numel, lct_geometry g,
-                         int32_t precomputed, hipStream_t stream);
+                         uint64_t *host_totals, int64_t size, int64_t logical_numel,
+                         lct_geometry g, int32_t precomputed, hipStream_t stream);
 
 /* ---- replaces dispatch.py:88-95 (count_bad_streams, the atomic path's
  * totals, LCT/kernels/generic/compaction.py:31-51): adds the number of

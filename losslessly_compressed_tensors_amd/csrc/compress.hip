@@ -55,8 +55,8 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
     uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
     int32_t *__restrict__ blocks, int32_t *__restrict__ counts, uint64_t *__restrict__ control,
     uint32_t epoch, int32_t *__restrict__ descriptor, int32_t *__restrict__ buffer_meta,
-    int32_t max_free_regions, lct_pending_frees frees, int32_t n_blocks, int64_t logical_numel,
-    int S, int W, int32_t lock_spins, int32_t polls) {
+    int32_t max_free_regions, lct_pending_frees frees, uint64_t *host_totals, int32_t n_blocks,
+    int64_t logical_numel, int S, int W, int32_t lock_spins, int32_t polls) {
     extern __shared__ uint32_t stage[];   // (W + 2) rows x 256 lanes, or the free list
     __shared__ uint2 table[256];
     __shared__ __attribute__((aligned(16))) uint8_t slices[kWavesPerBlock * kSliceBytes];
@@ -120,7 +120,17 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
         scan_allocate<false>(polled, summaries, counts, blocks, n_blocks, reserve);
     } else {
         NoReserve reserve;
-        scan_allocate<false>(polled, summaries, counts, blocks, n_blocks, reserve);
+        const ScanTotals totals =
+            scan_allocate<false>(polled, summaries, counts, blocks, n_blocks, reserve);
+        if (host_totals != nullptr && threadIdx.x == 0) {
+            // The totals a private compress sizes its overflow arrays by, for
+            // a host waiting on this word instead of on the launch's end.
+            host_word_store(host_totals,
+                            tagged_word(epoch, static_cast<uint32_t>(totals.entries)
+                                                   | (totals.incomplete ? 0x80000000u : 0u)));
+            host_word_store(host_totals + 1,
+                            tagged_word(epoch, static_cast<uint32_t>(totals.bytes)));
+        }
     }
 }
 
@@ -135,13 +145,16 @@ extern "C" int32_t lct_encode_fused(
     int32_t *shifted_decode_out, uint16_t *sample_values, uint8_t *extra_starts,
     int32_t *summaries, int32_t *blocks, int32_t *counts, uint64_t *control,
     int64_t control_words, uint32_t epoch, int32_t *descriptor, int32_t *buffer_meta,
-    int32_t max_free_regions, const lct_pending_frees *frees, int64_t size,
-    int64_t logical_numel, lct_geometry g, int32_t precomputed, hipStream_t stream) {
+    int32_t max_free_regions, const lct_pending_frees *frees, uint64_t *host_totals,
+    int64_t size, int64_t logical_numel, lct_geometry g, int32_t precomputed,
+    hipStream_t stream) {
     if (!source || !side || !encoded || !base_encode || !base_decode || !center_out
         || !shifted_decode_out || !extra_starts || !summaries || !blocks || !counts || !control)
         return LCT_E_NULL;
     const bool buffered = buffer_meta != nullptr;
     if (buffered && !descriptor) return LCT_E_NULL;
+    if (host_totals != nullptr && (buffered || (reinterpret_cast<uintptr_t>(host_totals) & 7) != 0))
+        return LCT_E_ARG;
     if (!geometry_ok(g)) return LCT_E_GEOMETRY;
     if (logical_numel <= 0 || size <= 0 || size % g.block_symbols != 0
         || logical_numel > size || logical_numel <= size - g.block_symbols)
@@ -190,7 +203,8 @@ extern "C" int32_t lct_encode_fused(
                        precomputed ? nullptr : sample_values, sample_size, n_groups,
                        extra_starts, summaries, blocks, counts, control, epoch,
                        buffered ? descriptor : nullptr, buffer_meta, max_free_regions, pending,
-                       static_cast<int32_t>(n_blocks), logical_numel, g.steps, g.fixed_words,
+                       host_totals, static_cast<int32_t>(n_blocks), logical_numel, g.steps,
+                       g.fixed_words,
                        lock_spins(), ready_polls());
     return static_cast<int32_t>(hipGetLastError());
 }

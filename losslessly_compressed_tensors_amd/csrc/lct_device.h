@@ -223,6 +223,14 @@ __device__ __forceinline__ void control_store(uint64_t *p, uint64_t value) {
     __hip_atomic_store(p, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A word for the host, in pinned host memory: one system-scope store of the
+// whole 64-bit word (no fence: the host reads only this word, which carries
+// its call's epoch in the high half, so it is current exactly when the tag
+// matches).
+__device__ __forceinline__ void host_word_store(uint64_t *p, uint64_t value) {
+    __hip_atomic_store(p, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // The center from the partial sums the sampling workgroups of the same launch
 // publish in control[0, n_groups), computed by wave 0 of the block: lane g
 // polls word g until it carries `epoch` (at most `polls` times).  Writes the

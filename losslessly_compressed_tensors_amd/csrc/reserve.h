@@ -63,10 +63,17 @@ __device__ __forceinline__ void block_exclusive_scan3(const int32_t (&v)[3], int
 // a source of loads, once the first pass's loads are in flight, so those
 // latencies overlap), `reserve.finish(request, scratch, incomplete)` at the
 // end.  kWriteScans = false leaves the exclusive scans of summaries[2nb, 4nb)
-// unwritten (the block metadata holds the same values).
+// unwritten (the block metadata holds the same values).  Returns the totals
+// written to counts (the same in every thread).
 // Workgroup-wide; contains barriers.
+struct ScanTotals {
+    int32_t entries;
+    int32_t bytes;
+    bool incomplete;
+};
+
 template <bool kWriteScans, class Source, class Reserve>
-__device__ __forceinline__ void scan_allocate(Source &source, int32_t *__restrict__ summaries,
+__device__ __forceinline__ ScanTotals scan_allocate(Source &source, int32_t *__restrict__ summaries,
                                               int32_t *__restrict__ counts,
                                               int32_t *__restrict__ blocks, int32_t n_blocks,
                                               Reserve &reserve) {
@@ -165,6 +172,7 @@ __device__ __forceinline__ void scan_allocate(Source &source, int32_t *__restric
     }
     // Two metadata bytes per overflowing stream: lane, then start step.
     reserve.finish(carry[1] + 2 * carry[0], scratch, incomplete);
+    return ScanTotals{carry[0], carry[1], incomplete};
 }
 
 // Per-block overflow counts and tail bytes from summaries[0, nb) and

@@ -42,10 +42,14 @@ def _byref(storage: FallbackStorage | None):
     return hip.ctypes.byref(storage.as_overflow())
 
 
-def _require_device(*tensors: torch.Tensor) -> None:
+def require_device(*tensors: torch.Tensor) -> None:
+    """Raise ``ValueError`` for any host tensor among ``tensors`` (None skipped)."""
     for tensor in tensors:
         if tensor is not None and tensor.device.type != "cuda":
             raise ValueError(f"LCT kernels require GPU tensors, got {tensor.device}")
+
+
+_require_device = require_device
 
 
 @dataclass
@@ -271,29 +275,154 @@ def bookkeeping(device, n_blocks, counts, blocks_out, buffer=None, descriptor=No
 def encode_fused(source, side, encoded, sample_size, encode_table, decode_table, center,
                  shifted_decode, sample_values, extra_starts, summaries, blocks_out, counts,
                  size, *, precomputed, logical_numel, block_symbols, lanes, steps, fixed_words,
-                 buffer=None, descriptor=None, frees=()) -> None:
+                 buffer=None, descriptor=None, frees=(), host_totals=None) -> int:
     """Center sampling, encoder and overflow bookkeeping in one launch
     (``dispatch.py:33-48``, ``:294-316`` and ``:70-85`` as
     ``LCT/codec/encode.py:22-186`` sequences them): for a shared ``buffer``
     also the deferred ``frees`` and the arena reservation into
-    ``descriptor``.  ``compact_extra`` then writes the entries and tails."""
+    ``descriptor``.  ``compact_extra`` then writes the entries and tails.
+    ``host_totals`` (private storage only): a :class:`HostTotals` the launch
+    also posts the overflow totals to.  Returns the launch's epoch."""
     _require_device(source, side, encoded, summaries, counts)
     n_blocks = size // block_symbols
     control = control_array(source.device, n_blocks)
     geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
-    pending = hip.PendingFrees()
-    pending.count = len(frees)
-    for i, freed in enumerate(frees):
-        pending.descriptor[i] = freed.data_ptr()
     buffered = buffer is not None
+    pending = None
+    if buffered:
+        pending = hip.PendingFrees()
+        pending.count = len(frees)
+        for i, freed in enumerate(frees):
+            pending.descriptor[i] = freed.data_ptr()
+    epoch = _next_fused_epoch()
     hip.call("lct_encode_fused", _ptr(source), _ptr(side), _ptr(encoded), int(sample_size),
              _ptr(encode_table), _ptr(decode_table), _ptr(center), _ptr(shifted_decode),
              _ptr(sample_values), _ptr(extra_starts), _ptr(summaries), _ptr(blocks_out),
-             _ptr(counts), _ptr(control), int(control.numel()), _next_fused_epoch(),
+             _ptr(counts), _ptr(control), int(control.numel()), epoch,
              _ptr(descriptor) if buffered else None, _ptr(buffer.storage) if buffered else None,
              int(buffer.max_free_regions) if buffered else 0,
-             hip.ctypes.byref(pending) if buffered else None, int(size), int(logical_numel),
-             geometry, int(bool(precomputed)), _stream(source))
+             hip.ctypes.byref(pending) if buffered else None,
+             host_totals.address if host_totals is not None else None, int(size),
+             int(logical_numel), geometry, int(bool(precomputed)), _stream(source))
+    return epoch
+
+
+def encode_fused_pointers(source, side, encoded, sample_size, encode_table, decode_table,
+                          center, shifted_decode, sample_values, extra_starts, summaries,
+                          blocks_out, counts, size, logical_numel, geometry, device, stream, *,
+                          descriptor=None, buffer=None, frees=(), host_totals=None) -> int:
+    """``encode_fused`` with every array given as a device address (int) and
+    the stream as its raw handle, for the public compress, which places
+    several arrays in one allocation and checks its tensors itself.  Returns
+    the launch's epoch."""
+    control = control_array(device, size // geometry.block_symbols)
+    pending = None
+    if buffer is not None:
+        pending = hip.PendingFrees()
+        pending.count = len(frees)
+        for i, freed in enumerate(frees):
+            pending.descriptor[i] = freed.data_ptr()
+    epoch = _next_fused_epoch()
+    hip.call("lct_encode_fused", source, side, encoded, sample_size, encode_table, decode_table,
+             center, shifted_decode, sample_values, extra_starts, summaries, blocks_out, counts,
+             control.data_ptr(), control.numel(), epoch, descriptor,
+             None if buffer is None else buffer.storage.data_ptr(),
+             0 if buffer is None else buffer.max_free_regions,
+             None if pending is None else hip.ctypes.byref(pending),
+             None if host_totals is None else host_totals.address, size, logical_numel,
+             geometry, 0, stream)
+    return epoch
+
+
+def compact_extra_pointers(source, lanes, starts, tail, descriptor, count, blocks, extra_starts,
+                           size, logical_numel, geometry, buffered, stream) -> None:
+    """``compact_extra`` over every block whose metadata ``encode_fused`` wrote
+    (no summaries, tail base 0), with device addresses (ints) and a raw
+    stream handle; BF16 tail source."""
+    hip.call("lct_compact_extra", source, lanes, starts, tail, descriptor, count, blocks, 0,
+             extra_starts, None, size, logical_numel, geometry, 0, int(buffered), stream)
+
+
+class HostTotals:
+    """Two uint64 words of pinned host memory that ``lct_encode_fused`` posts a
+    private compress's overflow totals to (``epoch << 32 | entries |
+    incomplete << 31`` and ``epoch << 32 | tail bytes``).  The reference reads
+    the totals with a blocking device->host copy after the launch
+    (``LCT/codec/encode.py:137-171``); polling these words instead lets the
+    host size the exact overflow arrays and enqueue the compaction as soon as
+    the launch's bookkeeping has the totals, before the launch ends."""
+
+    def __init__(self):
+        self.words = torch.zeros(2, dtype=torch.int64, pin_memory=True)
+        self.address = self.words.data_ptr()
+        self._view = self.words.numpy().view("uint64")
+
+    def wait(self, epoch: int, counts: torch.Tensor, device) -> tuple[int, int, int]:
+        """(entries, tail bytes, incomplete) of the launch with ``epoch``, made
+        on the current stream of ``device``.  Polls the words; once that
+        stream has no work left and they still do not carry the epoch, reads
+        ``counts`` from the device instead."""
+        view = self._view
+        spins = 0
+        stream = None
+        while True:
+            w0 = int(view[0])
+            w1 = int(view[1])
+            if w0 >> 32 == epoch and w1 >> 32 == epoch:
+                return w0 & 0x7FFFFFFF, w1 & 0xFFFFFFFF, (w0 >> 31) & 1
+            spins += 1
+            if spins % 64 != 0:
+                continue
+            if stream is None:
+                stream = torch.cuda.current_stream(device)
+            if stream.query():
+                w0 = int(view[0])
+                w1 = int(view[1])
+                if w0 >> 32 == epoch and w1 >> 32 == epoch:
+                    return w0 & 0x7FFFFFFF, w1 & 0xFFFFFFFF, (w0 >> 31) & 1
+                count, tail_bytes, _, incomplete = (int(v) for v in counts.tolist())
+                return count, tail_bytes, incomplete
+
+
+class _ThreadState(threading.local):
+    def __init__(self):
+        self.workspaces = {}
+        self.host_totals = None
+
+
+_thread_state = _ThreadState()
+
+
+def host_totals() -> HostTotals:
+    """This thread's :class:`HostTotals` (a compress waits on it before it
+    returns, so one per thread serves every stream)."""
+    state = _thread_state
+    if state.host_totals is None:
+        state.host_totals = HostTotals()
+    return state.host_totals
+
+
+def compress_workspace(device: torch.device, n_blocks: int, n_streams: int):
+    """``(extra_starts uint8[n_streams], summaries int32[summaries_length(n_blocks)])``
+    for a compress on the current stream of ``device``: working arrays that no
+    stored tensor keeps, held per thread and stream and grown on demand.  The
+    next compress of the same thread on the same stream reuses them; stream
+    order puts its writes after every read of this one."""
+    stream = torch._C._cuda_getCurrentRawStream(device.index)
+    key = (device.index, stream)
+    cached = _thread_state.workspaces.get(key)
+    if cached is not None and cached[0] == (n_blocks, n_streams):
+        return cached[2]
+    need_extra, need_summaries = n_streams, summaries_length(n_blocks)
+    arrays = None if cached is None else cached[1]
+    if arrays is None or arrays[0].numel() < need_extra or arrays[1].numel() < need_summaries:
+        arrays = (torch.empty(max(need_extra, 0 if arrays is None else arrays[0].numel()),
+                              dtype=torch.uint8, device=device),
+                  torch.empty(max(need_summaries, 0 if arrays is None else arrays[1].numel()),
+                              dtype=torch.int32, device=device))
+    views = (arrays[0][:need_extra], arrays[1][:need_summaries])
+    _thread_state.workspaces[key] = ((n_blocks, n_streams), arrays, views)
+    return views
 
 
 def count_bad_streams(extra_starts, count, total, streams, steps) -> None:

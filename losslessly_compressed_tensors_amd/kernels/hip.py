@@ -126,8 +126,8 @@ _SIGNATURES = {
                              _c_int64, Geometry, _c_int32, _ptr],
     "lct_encode_fused": [_ptr, _ptr, _ptr, _c_int64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
                          _ptr, _ptr, _ptr, _c_int64, ctypes.c_uint32, _ptr, _ptr, _c_int32,
-                         ctypes.POINTER(PendingFrees), _c_int64, _c_int64, Geometry, _c_int32,
-                         _ptr],
+                         ctypes.POINTER(PendingFrees), _ptr, _c_int64, _c_int64, Geometry,
+                         _c_int32, _ptr],
     "lct_count_bad_streams": [_ptr, _ptr, _ptr, _c_int64, _c_int32, _ptr],
     "lct_compact_bad_streams": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64,
                                 _c_int32, _c_int64, _c_int32, _ptr],

@@ -153,12 +153,15 @@ def test_encode_fused_rejects_bad_arguments_before_launch(lib):
     size = 4 * 32768
 
     def call(sample_size=4096, control=fake, words=64 + 4, epoch=7, meta=None,
-             regions=256, frees=None, logical=size):
+             regions=256, frees=None, logical=size, host_totals=None):
         return lib.lct_encode_fused(fake, fake, fake, sample_size, fake, fake, fake, fake, None,
                                     fake, fake, fake, fake, control, words, epoch, fake, meta,
-                                    regions, frees, size, logical, geometry, 0, None)
+                                    regions, frees, host_totals, size, logical, geometry, 0,
+                                    None)
 
     assert call(epoch=0) == LCT_E_ARG                       # 0 matches a fresh array
+    assert call(meta=fake, host_totals=fake) == LCT_E_ARG   # host totals: private only
+    assert call(host_totals=ctypes.c_void_p((1 << 20) + 4)) == LCT_E_ARG   # not 8-byte aligned
     assert call(words=64 + 3) == LCT_E_SIZE                 # no word for the last block
     assert call(control=ctypes.c_void_p((1 << 20) + 4)) == LCT_E_ARG   # not 8-byte aligned
     assert call(sample_size=3000) == LCT_E_ARG              # neither n nor a power of two
