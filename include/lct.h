@@ -589,6 +589,16 @@ int32_t lct_compress_buffered_noalloc(const void *source, int64_t logical_numel,
  * drive the give-up paths from the host without long waits. */
 int32_t lct_set_wait_limits(int32_t lock_polls, int32_t ready_polls);
 
+/* ---- which decoder kernel lct_decode launches: LCT_DECODER_AUTO (the
+ * default: the wide-tile kernel, or the compact one when only it holds the
+ * whole grid at once), LCT_DECODER_WIDE or LCT_DECODER_COMPACT.  Both write
+ * the same output.  Applies to launches made after the call.  No counterpart
+ * in the reference: tests pin each kernel on the same inputs. */
+#define LCT_DECODER_AUTO 0
+#define LCT_DECODER_WIDE 1
+#define LCT_DECODER_COMPACT 2
+int32_t lct_set_decoder(int32_t mode);
+
 #ifdef __cplusplus
 }
 #endif

@@ -147,6 +147,7 @@ _SIGNATURES = {
     "lct_buffer_allocate": [_ptr, _c_int32, _ptr, _ptr, _c_int32, _ptr, _ptr],
     "lct_buffer_free": [_ptr, _c_int32, _ptr, _ptr, _ptr],
     "lct_set_wait_limits": [_c_int32, _c_int32],
+    "lct_set_decoder": [_c_int32],
     "lct_compress_buffered_noalloc": [_ptr, _c_int64, _c_int64, Geometry, _ptr, _ptr, _ptr, _ptr,
                                       _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int32, _ptr,
                                       ctypes.POINTER(PendingFrees), _ptr],

@@ -73,7 +73,7 @@ def _nulls(name):
 
 
 # Entry points that take no pointer.
-_NO_POINTERS = {"lct_set_wait_limits"}
+_NO_POINTERS = {"lct_set_wait_limits", "lct_set_decoder"}
 
 
 @pytest.mark.parametrize("name", sorted(set(hip._SIGNATURES) - _NO_POINTERS))
@@ -86,6 +86,13 @@ def test_wait_limits_reject_negative_bounds_and_restore_defaults(lib):
     assert lib.lct_set_wait_limits(0, -1) == LCT_E_ARG
     assert lib.lct_set_wait_limits(16, 16) == 0
     assert lib.lct_set_wait_limits(0, 0) == 0   # the defaults again
+
+
+def test_decoder_choice_accepts_only_its_modes(lib):
+    assert lib.lct_set_decoder(3) == LCT_E_ARG
+    assert lib.lct_set_decoder(-1) == LCT_E_ARG
+    for mode in (1, 2, 0):   # ends on the default (automatic)
+        assert lib.lct_set_decoder(mode) == 0
 
 
 def test_bad_geometry_is_rejected_before_launch(lib):

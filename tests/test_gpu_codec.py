@@ -138,3 +138,35 @@ def test_large_block_count_metadata():
     assert np.array_equal(ct.fallback_lanes.cpu().numpy(), o.lanes)
     assert np.array_equal(ct.fallback_buffer.cpu().numpy(), o.tail)
     assert torch.equal(decompress(ct).view(torch.int16), x.view(torch.int16))
+
+
+@pytest.mark.parametrize("mode", ["wide", "compact"])
+@pytest.mark.parametrize("family,noise", LAYOUTS)
+def test_both_decoders_restore_every_case(family, noise, mode):
+    """lct_decode has two kernels (a 16-byte-tile one and a compact one that
+    keeps 8 workgroups per CU at larger W); each, forced, restores every bit
+    pattern (escapes, overflow in LDS and in HBM), a ragged last block and a
+    buffered tensor, on every layout."""
+    require_gpu()
+    from losslessly_compressed_tensors_amd.kernels import hip
+    print(f"case decoder {mode} {family.name} {noise.name}", flush=True)
+    dist = Distribution(family, noise_level=noise)
+    rng = np.random.default_rng(17)
+    bits = np.arange(65536, dtype=np.uint16)
+    rng.shuffle(bits)
+    inputs = [
+        torch.from_numpy(np.resize(bits, 5 * 65536 + 777).view(np.int16).copy())
+        .view(torch.bfloat16),
+        _gaussian((3, 50001), 2) if family == DistType.GAUSSIAN else _laplace((3, 50001), 3),
+    ]
+    buffer = TensorBuffer(16 << 20, device="cuda")
+    hip.call("lct_set_decoder", 2 if mode == "compact" else 1)
+    try:
+        for x in inputs:
+            for buf in (None, buffer):
+                ct = compress(x.cuda(), dist, buffer=buf)
+                assert np.array_equal(bits_of(decompress(ct)), bits_of(x))
+                ct.free()
+    finally:
+        hip.call("lct_set_decoder", 0)
+    verify_buffer(buffer)

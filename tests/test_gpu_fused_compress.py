@@ -290,3 +290,25 @@ def test_bookkeeping_that_stops_waiting_marks_the_tensor_incomplete():
         buffer.check()
     buffer.reset()
     buffer.check()
+
+
+def test_private_compress_host_totals():
+    """A private compress's launch posts its overflow totals to the thread's
+    pinned host words (tagged with the launch's epoch) and they equal the
+    stored counts; a wait for an epoch that never posts falls back to reading
+    the counts once the stream is idle."""
+    require_gpu()
+    print("case host totals", flush=True)
+    x = _patterns(90, 7 * 65536 + 4321)
+    ct = compress(x.cuda(), SPARSE)
+    torch.cuda.synchronize()
+    w0, w1 = (int(v) & 0xFFFFFFFFFFFFFFFF for v in dispatch.host_totals().words.tolist())
+    assert w0 >> 32 == w1 >> 32 != 0, "both words carry the launch's epoch"
+    count, used = int(ct.fallback_count.item()), int(ct.fallback_used.item())
+    assert count > 0
+    assert (w0 & 0x7FFFFFFF, (w0 >> 31) & 1, w1 & 0xFFFFFFFF) == (count, 0, used)
+    counts = torch.tensor([count, used, 0, 0], dtype=torch.int32, device="cuda")
+    stale = (w0 >> 32) ^ 0x5A5A5A5A
+    assert dispatch.host_totals().wait(stale, counts, counts.device) == (count, used, 0)
+    restored = decompress(ct)
+    assert torch.equal(restored.cpu().view(torch.int16), x.view(torch.int16))
