@@ -33,9 +33,10 @@ from torch import Tensor, nn
 from torch.utils.checkpoint import checkpoint
 
 from losslessly_compressed_tensors_amd.comp_format import Distribution, DistType, NoiseLevel
+from losslessly_compressed_tensors_amd.LCTensor import LCTTensor
 from losslessly_compressed_tensors_amd.components.layers import (
     Embedding, FlashAttention, Linear, RMSLinear, RMSNormFunction, Relu2Linear,
-    compress_weight, dense_weight, named_trainable_tensors, rms_norm_qkv,
+    compress_weight, dense_weight, named_trainable_tensors, prefetch_weights, rms_norm_qkv,
 )
 from losslessly_compressed_tensors_amd.components.sparse_utils import SparseAdamW, SparseMuon
 from losslessly_compressed_tensors_amd.tensor_buffer import TensorBuffer, _free_regions_snapshot
@@ -195,9 +196,22 @@ class Block(nn.Module):
         self.mlp = MLP(dim, compress_activations, min_compress_elements)
         self.norm1, self.norm2 = RMSNorm(dim), RMSNorm(dim)
 
+    def weights(self):
+        attn, mlp = self.attn, self.mlp
+        return [attn.q.weight, attn.k.weight, attn.v.weight, attn.proj.weight, mlp.fc.weight,
+                mlp.proj.weight]
+
     def forward(self, x: Tensor):
+        # The block's compressed weights are decoded together, once before its
+        # forward and once when its backward starts (the hook on its output),
+        # instead of one decode launch per use.
+        weights = self.weights()
+        prefetch_weights(weights)
         x = x + self.attn(x, self.norm1.gains)
-        return x + self.mlp(x, self.norm2.gains)
+        out = x + self.mlp(x, self.norm2.gains)
+        if out.requires_grad and any(isinstance(w, LCTTensor) for w in weights):
+            out.register_hook(lambda grad: prefetch_weights(self.weights()))
+        return out
 
 
 class GPT(nn.Module):

@@ -309,6 +309,29 @@ int32_t lct_decode(const int32_t *encoded, const uint8_t *side, int16_t *output,
                    int32_t rare_length, const lct_overflow *overflow,
                    hipStream_t stream);
 
+/* ---- several lct_decode calls in one launch: each job's arguments mean what
+ * lct_decode's do (overflow: has_overflow != 0), and each job's output equals
+ * its lct_decode's.  No counterpart in the reference, which decodes one tensor
+ * per launch (dispatch.py:319-361): for tensors of a few codec blocks (a
+ * layer's weights), whose decodes are bound by one block's latency, one launch
+ * serves them all.  At most LCT_MAX_DECODE_BATCH jobs, 2^31 - 1 blocks in
+ * all; the outputs must not overlap. */
+#define LCT_MAX_DECODE_BATCH 16
+typedef struct {
+    const int32_t *encoded;
+    const uint8_t *side;
+    int16_t *output;
+    const int32_t *shifted_decode;
+    const int32_t *center;
+    int64_t size;
+    int64_t logical_numel;
+    lct_geometry geometry;
+    int32_t rare_length;
+    int32_t has_overflow;
+    lct_overflow overflow;
+} lct_decode_job;
+int32_t lct_decode_batch(const lct_decode_job *jobs, int32_t n_jobs, hipStream_t stream);
+
 /* ---- replaces dispatch.py:146-165 (scatter_fallback,
  * LCT/kernels/generic/compaction.py:238-306): after a decode without the
  * overlay, rebuilds every overflow tail byte into BF16 with its side byte
@@ -598,6 +621,18 @@ int32_t lct_set_wait_limits(int32_t lock_polls, int32_t ready_polls);
 #define LCT_DECODER_WIDE 1
 #define LCT_DECODER_COMPACT 2
 int32_t lct_set_decoder(int32_t mode);
+
+/* ---- attainable HBM bandwidth with the codec kernels' access shape (16-byte
+ * non-temporal buffer accesses, `workgroups` workgroups of 256 threads each
+ * walking 16 KiB passes).  kind 0: copy src -> dst (src_bytes = dst_bytes);
+ * 1: read src (dst: at least 4 KiB, scratch); 2: write dst (src unused, may
+ * be NULL); 3: read src and write dst together, each pass covering the same
+ * fraction of both (0 < src_bytes <= dst_bytes).  Sizes are multiples of 16,
+ * at most 2^31; dst at least 4 KiB; pointers 16-byte aligned.  No counterpart
+ * in the reference: bench.py reports these ceilings beside the roofline
+ * fractions. */
+int32_t lct_bandwidth_probe(int32_t kind, const void *src, int64_t src_bytes, void *dst,
+                            int64_t dst_bytes, int32_t workgroups, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -28,6 +28,7 @@ SOURCES = [
     "pointwise.hip",
     "update.hip",
     "noalloc.hip",
+    "bandwidth.hip",
 ]
 
 # Packed FP32 instructions are kept out of the device code: the feature is

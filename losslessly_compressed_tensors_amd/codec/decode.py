@@ -67,3 +67,30 @@ def decode(data: CompressedTensor) -> torch.Tensor:
             steps=steps, fixed_words=fixed_words, rare_length=rare_length,
             overflow=overlay_of(data))
     return output.view(torch.bfloat16).reshape(data.shape)
+
+
+def decode_batch(tensors: list[CompressedTensor]) -> list[torch.Tensor]:
+    """Decode several compressed tensors with as few launches as possible: one
+    ``lct_decode_batch`` launch per ``MAX_DECODE_BATCH`` non-empty tensors.
+    Each result equals ``decode`` of its tensor.  For tensors of a few codec
+    blocks each (a layer's weights), whose decodes are bound by one block's
+    latency, one launch replaces one per tensor."""
+    from ..kernels import hip
+
+    outputs = []
+    jobs = []
+    for data in tensors:
+        if data.layout != data.layout.COMPRESSED:
+            outputs.append(data.data.reshape(data.shape))
+            continue
+        output = torch.empty(data.logical_numel, dtype=torch.int16, device=data.data.device)
+        outputs.append(output.view(torch.bfloat16).reshape(data.shape))
+        if not data.logical_numel:
+            continue
+        _, _, rare_length = get_distribution_tables(data.distribution, data.data.device)
+        jobs.append((data.data, data.sign_mantissa, output, shifted_decode_table(data),
+                     data.center, data.size, data.logical_numel, data.codec_geometry,
+                     rare_length, overlay_of(data)))
+    for start in range(0, len(jobs), hip.MAX_DECODE_BATCH):
+        dispatch.decode_batch(jobs[start:start + hip.MAX_DECODE_BATCH])
+    return outputs

@@ -21,22 +21,48 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 
 from ..LCTensor import LCTTensor
+from ..codec.decode import decode_batch
 from ..operations import compress, decompress
 from .dist_configs import act_dist, act_relu_dist, weight_dist
 from .ops import rms_norm, rms_norm_backward
 
 __all__ = [
-    "dense_weight", "RMSLinear", "rms_norm_qkv", "RMSNormFunction", "Relu2Linear",
-    "FlashAttention", "compress_weight", "Linear", "Embedding", "named_trainable_tensors",
+    "dense_weight", "prefetch_weights", "RMSLinear", "rms_norm_qkv", "RMSNormFunction",
+    "Relu2Linear", "FlashAttention", "compress_weight", "Linear", "Embedding",
+    "named_trainable_tensors",
 ]
 
 # Causal attention scale of the trainer (LCT/components/layers.py:232-236).
 ATTENTION_SCALE = 0.12
 
 
+# Dense copies of compressed weights decoded ahead of their use, keyed by the
+# LCTTensor's id: (the CompressedTensor decoded, its dense copy).  Each copy is
+# handed to the next dense_weight() of its weight and dropped.
+_prefetched: dict[int, tuple] = {}
+
+
+def prefetch_weights(weights) -> None:
+    """Decode the compressed ones among ``weights`` in as few launches as
+    possible (``decode_batch``: one per 16 tensors), for their next
+    ``dense_weight``.  A block's weights are a few codec blocks each, so one
+    decode each would be bound by one block's latency per tensor."""
+    pending = [w for w in weights if isinstance(w, LCTTensor)]
+    if not pending:
+        return
+    for w, dense in zip(pending, decode_batch([w.x for w in pending])):
+        _prefetched[id(w)] = (w.x, dense)
+
+
 def dense_weight(weight):
-    """The weight as a dense BF16 tensor (decoded if it is an ``LCTTensor``)."""
-    return weight.decompress() if isinstance(weight, LCTTensor) else weight
+    """The weight as a dense BF16 tensor (decoded if it is an ``LCTTensor``:
+    the copy ``prefetch_weights`` made of its current value, or a decode now)."""
+    if not isinstance(weight, LCTTensor):
+        return weight
+    entry = _prefetched.pop(id(weight), None)
+    if entry is not None and entry[0] is weight.x:
+        return entry[1]
+    return weight.decompress()
 
 
 class _SavedActivation:

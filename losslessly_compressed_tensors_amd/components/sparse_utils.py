@@ -46,6 +46,7 @@ import torch
 from torch import Tensor
 
 from ..LCTensor import LCTTensor
+from ..codec.decode import decode_batch
 from ..operations import a_compA_add_B
 from ..tensor_buffer import TensorBuffer
 from .dist_configs import momentum_dist, momentum_first_dist
@@ -90,6 +91,19 @@ class _StateBank(list):
         if value is None and like is not None:
             return torch.zeros_like(like, dtype=torch.bfloat16)
         return value
+
+    def check_out_many(self, indices, likes) -> list:
+        """``check_out`` of several slots, the compressed values decoded with
+        one launch per 16 (``decode_batch``)."""
+        values = [self[i] for i in indices]
+        for i in indices:
+            self[i] = None
+        packed = [k for k, v in enumerate(values) if isinstance(v, LCTTensor)]
+        for k, dense in zip(packed, decode_batch([values[k].x for k in packed])):
+            values[k].free()   # ordered after the decode on this stream
+            values[k] = dense
+        return [torch.zeros_like(like, dtype=torch.bfloat16) if v is None and like is not None
+                else v for v, like in zip(values, likes)]
 
     def check_in(self, index: int, value: Tensor, distribution) -> None:
         if self.compressed and value.dtype == torch.bfloat16:
@@ -228,19 +242,23 @@ class SparseMuon:
         dist = momentum_first_dist if self.first_step else self.distribution
         # Matrices grouped by wide shape: (rows, cols) with rows <= cols.
         groups: dict[tuple, list[tuple[int, Tensor, bool]]] = {}
-        for index, param in enumerate(self.params):
-            grad = param.grad
-            if grad is None:
-                continue
-            momentum = self.momentums.check_out(index, like=grad)
-            direction = _nesterov(grad, momentum, self.mu, nesterov=True)
-            # The momentum goes back (compressed) before the GEMMs: only the
-            # directions stay dense.
-            self.momentums.check_in(index, momentum, dist)
-            del momentum
-            tall = direction.size(-2) > direction.size(-1)
-            wide = direction.transpose(-2, -1) if tall else direction
-            groups.setdefault(tuple(wide.shape), []).append((index, wide, tall))
+        active = [(index, param.grad) for index, param in enumerate(self.params)
+                  if param.grad is not None]
+        # Momenta are checked out 16 at a time: one decode launch for the 16
+        # (each is a few codec blocks, so its own decode would be bound by one
+        # block's latency), and at most 16 dense momenta at once.
+        for start in range(0, len(active), 16):
+            part = active[start:start + 16]
+            momenta = self.momentums.check_out_many([i for i, _ in part], [g for _, g in part])
+            for (index, grad), momentum in zip(part, momenta):
+                direction = _nesterov(grad, momentum, self.mu, nesterov=True)
+                # The momentum goes back (compressed) before the GEMMs: only the
+                # directions stay dense.
+                self.momentums.check_in(index, momentum, dist)
+                tall = direction.size(-2) > direction.size(-1)
+                wide = direction.transpose(-2, -1) if tall else direction
+                groups.setdefault(tuple(wide.shape), []).append((index, wide, tall))
+            del momenta
         for shape, members in groups.items():
             stacked = torch.stack([wide.reshape(-1, *shape[-2:]) for _, wide, _ in members])
             polar = _orthogonalize_wide(stacked.reshape(-1, *shape[-2:]), self.ns_iters)

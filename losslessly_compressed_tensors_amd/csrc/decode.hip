@@ -144,11 +144,12 @@ __device__ __forceinline__ void decode_rows(StreamCursor cursor, const LaneOverl
 }
 
 // 8 waves per SIMD: the compiler keeps to 64 VGPRs (65 unconstrained).
-__global__ __launch_bounds__(kLanes, 8) void decode_kernel(
+// Codec block `block` of one tensor, by the workgroup.
+__device__ __forceinline__ void decode_block_wide(
     const int32_t *__restrict__ encoded, const uint8_t *__restrict__ side,
     uint16_t *__restrict__ output, const int32_t *__restrict__ shifted_decode,
     const int32_t *__restrict__ center_ptr, int64_t n_blocks, int64_t logical_numel, int S,
-    int W, int rare, lct_overflow ov, int has_overlay) {
+    int W, int rare, const lct_overflow &ov, int has_overlay, int64_t block) {
     extern __shared__ uint32_t stage[];   // register_stage_bytes(W): rows 3..W-1
     __shared__ DecodeTables tb;
     __shared__ int32_t scratch[kWavesPerBlock];
@@ -159,7 +160,6 @@ __global__ __launch_bounds__(kLanes, 8) void decode_kernel(
     __shared__ __attribute__((aligned(16))) uint8_t side_slices[kWavesPerBlock][kChunkSteps * kWave];
     int32_t *map_start = reinterpret_cast<int32_t *>(&side_slices[0][0]);
     int32_t *map_offset = map_start + kLanes;
-    const int64_t block = blockIdx.x;
     const int64_t row_base = block * S;
     const int64_t logical_base = row_base * kLanes;
     const uint32_t block_elems = static_cast<uint32_t>(S) * kLanes;
@@ -201,6 +201,52 @@ __global__ __launch_bounds__(kLanes, 8) void decode_kernel(
             decode_rows<false, 256>(cursor, lane, tail_lds, slice, tile, side_rsrc, first,
                                     out_rsrc, row_base, valid);
     }
+}
+
+__global__ __launch_bounds__(kLanes, 8) void decode_kernel(
+    const int32_t *__restrict__ encoded, const uint8_t *__restrict__ side,
+    uint16_t *__restrict__ output, const int32_t *__restrict__ shifted_decode,
+    const int32_t *__restrict__ center_ptr, int64_t n_blocks, int64_t logical_numel, int S,
+    int W, int rare, lct_overflow ov, int has_overlay) {
+    decode_block_wide(encoded, side, output, shifted_decode, center_ptr, n_blocks, logical_numel,
+                      S, W, rare, ov, has_overlay, blockIdx.x);
+}
+
+// Several tensors in one launch (LCT_MAX_DECODE_BATCH at most): workgroup b
+// decodes block b - first_block[j] of job j, the last job whose first block
+// is at most b.  For tensors of a few codec blocks each (a layer's weights),
+// whose decodes are bound by one block's latency, one launch replaces one per
+// tensor.  The job table travels in the kernel arguments.
+struct DecodeBatchJob {
+    const int32_t *encoded;
+    const uint8_t *side;
+    uint16_t *output;
+    const int32_t *shifted_decode;
+    const int32_t *center;
+    int64_t n_blocks;
+    int64_t logical_numel;
+    int32_t steps;
+    int32_t fixed_words;
+    int32_t rare;
+    int32_t has_overlay;
+    lct_overflow ov;
+};
+
+struct DecodeBatch {
+    int32_t n_jobs;
+    int32_t first_block[LCT_MAX_DECODE_BATCH + 1];
+    DecodeBatchJob jobs[LCT_MAX_DECODE_BATCH];
+};
+
+__global__ __launch_bounds__(kLanes, 8) void decode_batch_kernel(DecodeBatch batch) {
+    const int32_t b = static_cast<int32_t>(blockIdx.x);
+    int j = 0;
+    for (int k = 1; k < batch.n_jobs; ++k)
+        if (b >= batch.first_block[k]) j = k;
+    const DecodeBatchJob &job = batch.jobs[j];
+    decode_block_wide(job.encoded, job.side, job.output, job.shifted_decode, job.center,
+                      job.n_blocks, job.logical_numel, job.steps, job.fixed_words, job.rare,
+                      job.ov, job.has_overlay, b - batch.first_block[j]);
 }
 
 // ---- the compact decoder: 8 workgroups per CU for payloads of 13 to 19 words
@@ -517,4 +563,58 @@ extern "C" int32_t lct_set_decoder(int32_t mode) {
         return LCT_E_ARG;
     g_decoder_mode.store(mode, std::memory_order_relaxed);
     return LCT_OK;
+}
+
+extern "C" int32_t lct_decode_batch(const lct_decode_job *jobs, int32_t n_jobs,
+                                    hipStream_t stream) {
+    if (!jobs) return LCT_E_NULL;
+    if (n_jobs <= 0 || n_jobs > LCT_MAX_DECODE_BATCH) return LCT_E_ARG;
+    DecodeBatch batch{};
+    batch.n_jobs = n_jobs;
+    int64_t total = 0;
+    size_t lds = 0;
+    for (int32_t j = 0; j < n_jobs; ++j) {
+        const lct_decode_job &in = jobs[j];
+        if (!in.encoded || !in.side || !in.output || !in.shifted_decode || !in.center)
+            return LCT_E_NULL;
+        const lct_geometry &g = in.geometry;
+        if (!geometry_ok(g)) return LCT_E_GEOMETRY;
+        if (in.logical_numel <= 0 || in.size <= 0 || in.size % g.block_symbols != 0
+            || in.logical_numel > in.size || in.logical_numel <= in.size - g.block_symbols)
+            return LCT_E_SIZE;
+        if (in.rare_length < 0 || in.rare_length > 8) return LCT_E_ARG;
+        if ((reinterpret_cast<uintptr_t>(in.encoded) & 15) != 0) return LCT_E_ARG;
+        if (g.fixed_words <= kRegisterRows) return LCT_E_GEOMETRY;
+        if (in.has_overflow) {
+            const lct_overflow &o = in.overflow;
+            if (!o.lanes || !o.starts || !o.tail || !o.blocks) return LCT_E_NULL;
+            if (o.descriptor != nullptr && o.count == nullptr) return LCT_E_NULL;
+        }
+        const int64_t n_blocks = in.size / g.block_symbols;
+        batch.first_block[j] = static_cast<int32_t>(total);
+        total += n_blocks;
+        if (total > 0x7FFFFFFF) return LCT_E_SIZE;
+        DecodeBatchJob &out = batch.jobs[j];
+        out.encoded = in.encoded;
+        out.side = in.side;
+        out.output = reinterpret_cast<uint16_t *>(in.output);
+        out.shifted_decode = in.shifted_decode;
+        out.center = in.center;
+        out.n_blocks = n_blocks;
+        out.logical_numel = in.logical_numel;
+        out.steps = g.steps;
+        out.fixed_words = g.fixed_words;
+        out.rare = in.rare_length;
+        out.has_overlay = in.has_overflow ? 1 : 0;
+        out.ov = in.has_overflow ? in.overflow : lct_overflow{};
+        const size_t job_lds = static_cast<size_t>(register_stage_bytes(g.fixed_words));
+        lds = job_lds > lds ? job_lds : lds;
+    }
+    batch.first_block[n_jobs] = static_cast<int32_t>(total);
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(&decode_batch_kernel),
+                                           lds))
+        return static_cast<int32_t>(e);
+    hipLaunchKernelGGL(decode_batch_kernel, dim3(static_cast<uint32_t>(total)), dim3(kLanes), lds,
+                       stream, batch);
+    return static_cast<int32_t>(hipGetLastError());
 }

@@ -482,6 +482,26 @@ def decode_kernel(encoded, side, output, shifted_decode, center, size, *, logica
              ov if ov is None else hip.ctypes.byref(ov), _stream(encoded))
 
 
+def decode_batch(jobs) -> None:
+    """Several decodes in one launch (``lct_decode_batch``).  ``jobs``: at most
+    ``hip.MAX_DECODE_BATCH`` tuples ``(encoded, side, output, shifted_decode,
+    center, size, logical_numel, (B, L, S, W), rare_length, overflow)`` with
+    ``decode_kernel``'s meanings, all on the current stream's device."""
+    array = (hip.DecodeJob * len(jobs))()
+    for job, (encoded, side, output, shifted_decode, center, size, logical_numel, geometry,
+              rare_length, overflow) in zip(array, jobs):
+        _require_device(encoded, side, output)
+        job.encoded, job.side, job.output = _ptr(encoded), _ptr(side), _ptr(output)
+        job.shifted_decode, job.center = _ptr(shifted_decode), _ptr(center)
+        job.size, job.logical_numel = int(size), int(logical_numel)
+        job.geometry = hip.Geometry(*(int(v) for v in geometry))
+        job.rare_length = int(rare_length)
+        job.has_overflow = int(overflow is not None)
+        if overflow is not None:
+            job.overflow = overflow.as_overflow()
+    hip.call("lct_decode_batch", array, len(jobs), _stream(jobs[0][0]))
+
+
 def scatter_fallback(storage: FallbackStorage, sign_mantissa, output, n_elements,
                      logical_numel, block_symbols, lanes, steps) -> None:
     """Overflow rows of a decode made without the overlay

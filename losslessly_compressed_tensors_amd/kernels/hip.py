@@ -77,6 +77,27 @@ class Bookkeeping(ctypes.Structure):
     ]
 
 
+MAX_DECODE_BATCH = 16   # LCT_MAX_DECODE_BATCH
+
+
+class DecodeJob(ctypes.Structure):
+    """``lct_decode_job``: one tensor of a batched decode."""
+
+    _fields_ = [
+        ("encoded", _ptr),
+        ("side", _ptr),
+        ("output", _ptr),
+        ("shifted_decode", _ptr),
+        ("center", _ptr),
+        ("size", _c_int64),
+        ("logical_numel", _c_int64),
+        ("geometry", Geometry),
+        ("rare_length", _c_int32),
+        ("has_overflow", _c_int32),
+        ("overflow", Overflow),
+    ]
+
+
 # name -> argument types (all entry points return int32).
 _SIGNATURES = {
     "lct_estimate_and_shift_tables": [_ptr, _c_int32, _c_int64, _c_int64, _ptr, _ptr, _ptr, _ptr,
@@ -90,6 +111,7 @@ _SIGNATURES = {
                           _c_int64, _c_int64, Geometry, _c_int32, _c_int32, _ptr],
     "lct_decode": [_ptr, _ptr, _ptr, _ptr, _ptr, _c_int64, _c_int64, Geometry, _c_int32,
                    ctypes.POINTER(Overflow), _ptr],
+    "lct_decode_batch": [ctypes.POINTER(DecodeJob), _c_int32, _ptr],
     "lct_pointwise_dense": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64,
                             _c_int64, Geometry, _c_int32, _c_int32, _c_int32, _c_int32, _c_int32,
                             ctypes.POINTER(Overflow), _ptr],
@@ -148,6 +170,7 @@ _SIGNATURES = {
     "lct_buffer_free": [_ptr, _c_int32, _ptr, _ptr, _ptr],
     "lct_set_wait_limits": [_c_int32, _c_int32],
     "lct_set_decoder": [_c_int32],
+    "lct_bandwidth_probe": [_c_int32, _ptr, _c_int64, _ptr, _c_int64, _c_int32, _ptr],
     "lct_compress_buffered_noalloc": [_ptr, _c_int64, _c_int64, Geometry, _ptr, _ptr, _ptr, _ptr,
                                       _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int32, _ptr,
                                       ctypes.POINTER(PendingFrees), _ptr],

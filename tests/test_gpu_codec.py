@@ -170,3 +170,34 @@ def test_both_decoders_restore_every_case(family, noise, mode):
     finally:
         hip.call("lct_set_decoder", 0)
     verify_buffer(buffer)
+
+
+def test_decode_batch_equals_single_decodes():
+    """decode_batch (lct_decode_batch: up to 16 tensors per launch) restores
+    every tensor bit for bit: 20 tensors (two launches) of every layout, private
+    and buffered, with escapes and overflow, ragged and single-block sizes."""
+    require_gpu()
+    from losslessly_compressed_tensors_amd.codec.decode import decode_batch
+    print("case decode batch", flush=True)
+    rng = np.random.default_rng(23)
+    buffer = TensorBuffer(16 << 20, device="cuda")
+    inputs, tensors = [], []
+    for i in range(20):
+        family, noise = LAYOUTS[i % len(LAYOUTS)]
+        n = int(rng.integers(1, 4 * 65536))
+        if i % 3 == 0:
+            bits = rng.integers(0, 65536, size=n, dtype=np.uint16)
+            x = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16)
+        else:
+            x = _gaussian((n,), 100 + i, 0.02)
+        inputs.append(x)
+        tensors.append(compress(x.cuda(), Distribution(family, noise_level=noise),
+                                buffer=buffer if i % 2 else None))
+    outputs = decode_batch(tensors)
+    for x, ct, y in zip(inputs, tensors, outputs):
+        assert y.shape == x.shape and y.dtype == torch.bfloat16
+        assert np.array_equal(bits_of(y), bits_of(x))
+        assert torch.equal(y.view(torch.int16), decompress(ct).view(torch.int16))
+    for ct in tensors:
+        ct.free()
+    verify_buffer(buffer)
