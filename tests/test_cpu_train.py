@@ -121,11 +121,12 @@ def test_rotary_rotates_first_half_pairs():
     assert torch.allclose(pair(y), pair(x), atol=1e-5)
 
 
-def test_softcap_cross_entropy_matches_autograd():
+@pytest.mark.parametrize("rows", [6, 1100])   # one row group, three (512 rows each)
+def test_softcap_cross_entropy_matches_autograd(rows):
     from examples.nanogpt import train_gpt_lct as gpt
     g = torch.Generator().manual_seed(3)
-    logits = (torch.randn(6, 40, generator=g) * 20).bfloat16().requires_grad_()
-    targets = torch.randint(0, 40, (6,), generator=g)
+    logits = (torch.randn(rows, 40, generator=g) * 20).bfloat16().requires_grad_()
+    targets = torch.randint(0, 40, (rows,), generator=g)
     loss = gpt.SoftcapCrossEntropy.apply(logits, targets)
     loss.backward()
     x = logits.detach().double().requires_grad_()
