@@ -36,7 +36,8 @@ from losslessly_compressed_tensors_amd.comp_format import Distribution, DistType
 from losslessly_compressed_tensors_amd.LCTensor import LCTTensor
 from losslessly_compressed_tensors_amd.components.layers import (
     Embedding, FlashAttention, Linear, RMSLinear, RMSNormFunction, Relu2Linear,
-    compress_weight, dense_weight, named_trainable_tensors, prefetch_weights, rms_norm_qkv,
+    compress_weight, dense_weight, flush_saved, named_trainable_tensors, prefetch_saved,
+    prefetch_weights, rms_norm_qkv,
 )
 from losslessly_compressed_tensors_amd.components.sparse_utils import SparseAdamW, SparseMuon
 from losslessly_compressed_tensors_amd.tensor_buffer import TensorBuffer, _free_regions_snapshot
@@ -225,12 +226,24 @@ class Block(nn.Module):
         # The block's compressed weights are decoded together, once before its
         # forward and once when its backward starts (the hook on its output),
         # instead of one decode launch per use.
+        # Likewise the activations the attention and the MLP save: compressed
+        # together when each part's forward ends (flush_saved), decoded
+        # together when its backward starts (the hooks on the parts' outputs).
         weights = self.weights()
         prefetch_weights(weights)
-        x = x + self.attn(x, self.norm1.gains)
-        out = x + self.mlp(x, self.norm2.gains)
-        if out.requires_grad and any(isinstance(w, LCTTensor) for w in weights):
-            out.register_hook(lambda grad: prefetch_weights(self.weights()))
+        a = self.attn(x, self.norm1.gains)
+        saved_attn = flush_saved()
+        x = x + a
+        m = self.mlp(x, self.norm2.gains)
+        saved_mlp = flush_saved()
+        out = x + m
+        if out.requires_grad:
+            if any(isinstance(w, LCTTensor) for w in weights):
+                out.register_hook(lambda grad: prefetch_weights(self.weights()))
+            if saved_attn:
+                a.register_hook(lambda grad: prefetch_saved(saved_attn))
+            if saved_mlp:
+                m.register_hook(lambda grad: prefetch_saved(saved_mlp))
         return out
 
 

@@ -256,6 +256,47 @@ int32_t lct_encode_fused(const void *source, uint8_t *side, int32_t *encoded,
                          uint64_t *host_totals, int64_t size, int64_t logical_numel,
                          lct_geometry g, int32_t precomputed, hipStream_t stream);
 
+/* ---- lct_encode_fused with a buffer, then lct_compact_extra (buffered = 1),
+ * for up to LCT_MAX_COMPRESS_BATCH BF16 tensors in two launches: one fused
+ * compress whose workgroups are the jobs' single-launch grids laid end to
+ * end, and one compaction of every job's blocks.  No counterpart in the
+ * reference, which compresses one tensor per call (LCT/codec/encode.py:189-218):
+ * a tensor of a few codec blocks (a layer's activations, a weight's optimizer
+ * state) is bound by one block's latency, so one launch serves several.
+ * Each job's outputs are those of its own lct_encode_fused +
+ * lct_compact_extra, except where in the arena its overflow region lies
+ * (the jobs reserve in the order their bookkeeping takes the arena lock).
+ * `frees` are applied before any job's reservation.  All jobs share
+ * geometry.steps.  Working arrays, shared by the jobs and partitioned in job
+ * order: extra_starts uint8[sum nb*256], summaries int32[sum (5*nb + 1)],
+ * control uint64[1 + sum (64 + nb)] (the array of lct_encode_fused, with the
+ * same zeroing and epoch rules).  arena: the buffer's payload arena (the
+ * descriptors' offsets index into it).  A bounded wait that gives up marks
+ * its tensor incomplete (status 7), as in lct_encode_fused. */
+#define LCT_MAX_COMPRESS_BATCH 16
+typedef struct {
+    const void *source;          /* BF16 bits, logical_numel, 16-byte aligned */
+    uint8_t *side;               /* uint8[size], 16-byte aligned */
+    int32_t *encoded;            /* int32[nb*256*W + 4], 16-byte aligned */
+    const int32_t *base_encode;
+    const int32_t *base_decode;
+    int32_t *center_out;         /* int32[1] */
+    int32_t *shifted_decode_out; /* int32[1024] */
+    uint16_t *sample_values;     /* uint16[sample_size], or NULL */
+    int32_t *blocks;             /* int32[3*nb] */
+    int32_t *counts;             /* int32[4] */
+    int32_t *descriptor;         /* int32[4] */
+    int64_t sample_size;
+    int64_t size;
+    int64_t logical_numel;
+    lct_geometry geometry;
+} lct_compress_job;
+int32_t lct_compress_batch(const lct_compress_job *jobs, int32_t n_jobs,
+                           uint8_t *extra_starts, int64_t extra_bytes, int32_t *summaries,
+                           int64_t summary_words, uint64_t *control, int64_t control_words,
+                           uint32_t epoch, int32_t *buffer_meta, int32_t max_free_regions,
+                           uint8_t *arena, const lct_pending_frees *frees, hipStream_t stream);
+
 /* ---- replaces dispatch.py:88-95 (count_bad_streams, the atomic path's
  * totals, LCT/kernels/generic/compaction.py:31-51): adds the number of
  * overflowing streams (extra_starts[s] != 255) to count[0] and their tail

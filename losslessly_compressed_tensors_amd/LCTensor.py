@@ -19,6 +19,7 @@ from .operations import (
     a_compA_add_compB,
     compA_add_B,
     compress,
+    compress_batch,
     decompress,
 )
 from .tensor_buffer import TensorBuffer
@@ -37,6 +38,18 @@ class LCTTensor(Tensor):
 
     def __init__(self, x: Tensor, buffer: TensorBuffer | None, dist: Distribution):
         self.x: CompressedTensor = compress(x, buffer=buffer, distribution=dist)
+
+    @classmethod
+    def compress_many(cls, tensors, buffer: TensorBuffer, dist: Distribution) -> list:
+        """``LCTTensor(t, buffer, dist)`` of each tensor, compressed into
+        ``buffer`` with one launch per 16 tensors (``compress_batch``)."""
+        records = compress_batch(tensors, dist, buffer=buffer)
+        out = []
+        for tensor, record in zip(tensors, records):
+            wrapper = cls.__new__(cls, tensor, buffer, dist)
+            wrapper.x = record
+            out.append(wrapper)
+        return out
 
     @classmethod
     def __torch_dispatch__(cls, func, types, args=(), kwargs=None):

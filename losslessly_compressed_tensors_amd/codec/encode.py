@@ -476,3 +476,88 @@ def _compress_bf16(source: torch.Tensor, shape, distribution: Distribution,
         shape=shape, layout=StorageLayout.COMPRESSED, stream_geometry=stream_geometry,
         sample_values=sample_values,
     )
+
+
+def encode_batch(tensors, distributions, buffer: TensorBuffer) -> list[CompressedTensor]:
+    """``encode`` of several BF16 tensors into ``buffer``: one fused compress
+    launch and one compaction launch (``lct_compress_batch``) per
+    ``hip.MAX_COMPRESS_BATCH`` tensors of one step count.  Each record equals
+    the one ``encode`` makes, except where in the arena its overflow region
+    lies.  The buffer's deferred frees are applied before the first
+    reservation.  Empty tensors take ``encode``."""
+    if buffer is None:
+        raise ValueError("encode_batch stores into a TensorBuffer")
+    if buffer.capacity_bytes % 4:
+        raise ValueError("TensorBuffer capacity must be divisible by 4")
+    results: list[CompressedTensor | None] = [None] * len(tensors)
+    # (index, job, record pieces) per launchable tensor, grouped by step count.
+    pending: dict[int, list] = {}
+    for index, (data, distribution) in enumerate(zip(tensors, distributions)):
+        shape = tuple(data.shape)
+        source = data.contiguous().view(-1)
+        if source.element_size() != 2:
+            raise TypeError(f"LCT compresses 16-bit (bfloat16) tensors, got {source.dtype}")
+        if source.device.type != "cuda":
+            raise ValueError(f"LCT kernels require GPU tensors, got {source.device}")
+        if source.device != buffer.device:
+            raise ValueError("tensors must be on the buffer's device")
+        logical_numel = source.numel()
+        if logical_numel == 0:
+            results[index] = encode(data, distribution, buffer)
+            continue
+        if source.data_ptr() % 16:
+            source = source.clone()
+        stream_geometry = geometry(distribution)
+        block_symbols, lanes, steps, fixed_words = stream_geometry
+        blocks = _cdiv(logical_numel, block_symbols)
+        if blocks > MAX_CODEC_BLOCKS:
+            raise ValueError(f"tensor too large: {blocks} codec blocks (at most "
+                             f"{MAX_CODEC_BLOCKS})")
+        storage_numel = blocks * block_symbols
+        payload_bytes = 4 * (blocks * lanes * fixed_words + 4)
+        device = source.device
+        packed = torch.empty(storage_numel + payload_bytes, dtype=torch.uint8, device=device)
+        record = torch.empty(1033 + 3 * blocks, dtype=torch.int32, device=device)
+        sample_size = min(logical_numel, CENTER_SAMPLE_SIZE)
+        sample_values = torch.empty(sample_size, dtype=torch.int16, device=device)
+        encode_table, decode_table, _ = get_distribution_tables(distribution, device)
+        p_side, p_record = packed.data_ptr(), record.data_ptr()
+        job = hip.CompressJob(
+            source.data_ptr(), p_side, p_side + storage_numel, encode_table.data_ptr(),
+            decode_table.data_ptr(), p_record + 4 * 1032, p_record, sample_values.data_ptr(),
+            p_record + 4 * 1033, p_record + 4 * 1024, p_record + 4 * 1028, sample_size,
+            storage_numel, logical_numel, hip.Geometry(*stream_geometry))
+        pending.setdefault(steps, []).append(
+            (index, job, source, packed, record, sample_values, shape, distribution,
+             stream_geometry, storage_numel, payload_bytes, blocks))
+    device = buffer.device
+    stream = torch._C._cuda_getCurrentRawStream(device.index)
+    for members in pending.values():
+        for start in range(0, len(members), hip.MAX_COMPRESS_BATCH):
+            part = members[start:start + hip.MAX_COMPRESS_BATCH]
+            frees = buffer._take_frees()
+            try:
+                dispatch.compress_batch_pointers([m[1] for m in part], buffer, frees, device,
+                                                 stream)
+            except BaseException:
+                buffer._restore_frees(frees)
+                raise
+            for (index, _, source, packed, record, sample_values, shape, distribution,
+                 stream_geometry, storage_numel, payload_bytes, blocks) in part:
+                side, payload = packed.split_with_sizes((storage_numel, payload_bytes))
+                shifted_decode, counts, descriptor, center, blocks_out = record.split_with_sizes(
+                    (1024, 4, 4, 1, 3 * blocks))
+                count_view, used_view = counts.split_with_sizes((1, 1, 2))[:2]
+                results[index] = CompressedTensor(
+                    payload.view(torch.int32), storage_numel, side,
+                    fallback_blocks=blocks_out,
+                    fallback_buffer=buffer.data,
+                    fallback_descriptor=descriptor,
+                    buffer=buffer,
+                    fallback_count=count_view,
+                    fallback_used=used_view,
+                    distribution=distribution, center=center, decode_table=shifted_decode,
+                    shape=shape, layout=StorageLayout.COMPRESSED,
+                    stream_geometry=stream_geometry, sample_values=sample_values,
+                )
+    return results

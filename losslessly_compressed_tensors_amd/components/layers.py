@@ -22,14 +22,14 @@ from torch import Tensor, nn
 
 from ..LCTensor import LCTTensor
 from ..codec.decode import decode_batch
-from ..operations import compress, decompress
+from ..operations import compress, compress_batch, decompress
 from .dist_configs import act_dist, act_relu_dist, weight_dist
 from .ops import rms_norm, rms_norm_backward
 
 __all__ = [
     "dense_weight", "prefetch_weights", "RMSLinear", "rms_norm_qkv", "RMSNormFunction",
     "Relu2Linear", "FlashAttention", "compress_weight", "Linear", "Embedding",
-    "named_trainable_tensors",
+    "named_trainable_tensors", "flush_saved", "prefetch_saved", "batch_saved_compression",
 ]
 
 # Causal attention scale of the trainer (LCT/components/layers.py:232-236).
@@ -65,17 +65,83 @@ def dense_weight(weight):
     return weight.decompress()
 
 
+# Saved activations wait here, dense, until they can be compressed together:
+# flush_saved() compresses the queue with one launch per 16 tensors
+# (compress_batch), and runs when the queue is full, when a queued tensor is
+# taken, and wherever a caller ends a group (a block's attention or MLP).  A
+# layer's activations are a few codec blocks per tensor, so one compress
+# launch each would be bound by one block's latency.
+_MAX_QUEUE = 16
+_queue: list["_SavedActivation"] = []
+_batching = {"enabled": True}
+
+
+def batch_saved_compression(enabled: bool) -> bool:
+    """Queue saved activations for batched compression (``True``, the default)
+    or compress each in its layer's forward; returns the previous setting.
+    The compressed records are the same either way."""
+    previous, _batching["enabled"] = _batching["enabled"], bool(enabled)
+    if not enabled:
+        flush_saved()
+    return previous
+
+
+def flush_saved() -> list:
+    """Compress the queued saved activations and return them (one
+    ``compress_batch`` per buffer).  A queued tensor modified in place since
+    it was saved raises, as autograd's saved-tensor check would."""
+    global _queue
+    queued, _queue = _queue, []
+    by_buffer: dict[int, list] = {}
+    for saved in queued:
+        if saved.value._version != saved.version:
+            raise RuntimeError(
+                "a tensor saved for backward was modified in place before it was compressed")
+        by_buffer.setdefault(id(saved.buffer), []).append(saved)
+    for members in by_buffer.values():
+        values = compress_batch([s.value for s in members], [s.distribution for s in members],
+                                buffer=members[0].buffer)
+        for saved, value in zip(members, values):
+            saved.value, saved.queued, saved.distribution, saved.buffer = value, False, None, None
+    return queued
+
+
+def prefetch_saved(saved) -> None:
+    """Decode the still-compressed members of ``saved`` (the list a
+    ``flush_saved`` returned) with one launch per 16 (``decode_batch``) and
+    free their storage; each one's ``take()`` then returns its dense copy."""
+    pending = [s for s in saved if s.compressed and s.value is not None and not s.queued]
+    if not pending:
+        return
+    for s, dense in zip(pending, decode_batch([s.value for s in pending])):
+        s.value.free()
+        s.value, s.compressed = dense, False
+
+
 class _SavedActivation:
     """One saved tensor, compressed into ``buffer`` or kept as is."""
 
-    __slots__ = ("value", "compressed")
+    __slots__ = ("value", "compressed", "queued", "version", "distribution", "buffer")
 
     def __init__(self, tensor: Tensor, compressed: bool, distribution, buffer):
         self.compressed = compressed
-        self.value = compress(tensor, distribution=distribution, buffer=buffer) if compressed else tensor
+        self.queued = False
+        self.value = tensor
+        if not compressed:
+            return
+        if _batching["enabled"] and buffer is not None and tensor.is_cuda:
+            self.queued, self.version = True, tensor._version
+            self.distribution, self.buffer = distribution, buffer
+            _queue.append(self)
+            if len(_queue) >= _MAX_QUEUE:
+                flush_saved()
+        else:
+            self.value = compress(tensor, distribution=distribution, buffer=buffer)
 
     def take(self) -> Tensor:
         """The saved tensor; a compressed one is decoded and its storage freed."""
+        if self.queued:
+            flush_saved()
         value, self.value = self.value, None
         if not self.compressed:
             return value

@@ -110,6 +110,21 @@ class _StateBank(list):
             value = LCTTensor(value, buffer=self.buffer, dist=distribution)
         self[index] = value
 
+    def check_in_many(self, indices, values, distribution) -> None:
+        """``check_in`` of several slots; with a buffer the BF16 values are
+        compressed with one launch per 16 (``LCTTensor.compress_many``)."""
+        if not (self.compressed and self.buffer is not None):
+            for index, value in zip(indices, values):
+                self.check_in(index, value, distribution)
+            return
+        packed = [k for k, v in enumerate(values) if v.dtype == torch.bfloat16]
+        stored = list(values)
+        for k, value in zip(packed, LCTTensor.compress_many([values[k] for k in packed],
+                                                            self.buffer, distribution)):
+            stored[k] = value
+        for index, value in zip(indices, stored):
+            self[index] = value
+
 
 class SparseSGDM:
     """Heavy-ball SGD; the velocity stays compressed between steps
@@ -252,12 +267,12 @@ class SparseMuon:
             momenta = self.momentums.check_out_many([i for i, _ in part], [g for _, g in part])
             for (index, grad), momentum in zip(part, momenta):
                 direction = _nesterov(grad, momentum, self.mu, nesterov=True)
-                # The momentum goes back (compressed) before the GEMMs: only the
-                # directions stay dense.
-                self.momentums.check_in(index, momentum, dist)
                 tall = direction.size(-2) > direction.size(-1)
                 wide = direction.transpose(-2, -1) if tall else direction
                 groups.setdefault(tuple(wide.shape), []).append((index, wide, tall))
+            # The momenta go back (compressed, one launch for the 16) before
+            # the GEMMs: only the directions stay dense.
+            self.momentums.check_in_many([i for i, _ in part], momenta, dist)
             del momenta
         for shape, members in groups.items():
             stacked = torch.stack([wide.reshape(-1, *shape[-2:]) for _, wide, _ in members])

@@ -8,6 +8,7 @@
 // at entries [first, first+count), their exponent tails int8(e-127) for steps
 // start..S-1 concatenated from byte_base, and blocks[3*nb] = {count, first,
 // byte_base} so every reader walks the list one block at a time.
+#include "batch.h"
 #include "overflow_walk.h"
 #include "reserve.h"
 
@@ -197,15 +198,17 @@ __global__ __launch_bounds__(kLanes) void compact_extra_kernel(
 // reservation and its lanes' extra starts at once -- one memory round trip
 // before the ranking -- and leaves if the block has no overflow.  The entries
 // a block rewrites are the ones already there.
-__global__ __launch_bounds__(kLanes) void compact_blocks_kernel(
+// Entries and tails of codec block `block`, at the offsets the block
+// metadata holds (one workgroup).
+__device__ __forceinline__ void compact_block(
     const void *__restrict__ source, uint8_t *__restrict__ lanes,
     uint8_t *__restrict__ starts, uint8_t *__restrict__ tail,
     const int32_t *__restrict__ descriptor, const int32_t *__restrict__ count_total,
     const int32_t *__restrict__ blocks, int64_t base, const uint8_t *__restrict__ extra_starts,
-    int64_t n_blocks, int64_t logical_numel, int S, int precomputed, int buffered) {
+    int64_t n_blocks, int64_t logical_numel, int S, int precomputed, int buffered,
+    int64_t block) {
     __shared__ int32_t scratch[kWavesPerBlock];
     __shared__ int32_t entry_offset[kLanes], entry_start[kLanes], entry_lane[kLanes];
-    const int64_t block = blockIdx.x;
     const int32_t count = blocks[block];
     const int32_t first = blocks[n_blocks + block];
     const int32_t byte_base = blocks[2 * n_blocks + block];
@@ -222,6 +225,29 @@ __global__ __launch_bounds__(kLanes) void compact_blocks_kernel(
     write_block(source, lanes, starts, tail, lane_off, start_off, tail_off, first, byte_base, e,
                 block, logical_numel, S, precomputed, entry_offset, entry_start, entry_lane,
                 true);
+}
+
+__global__ __launch_bounds__(kLanes) void compact_blocks_kernel(
+    const void *__restrict__ source, uint8_t *__restrict__ lanes,
+    uint8_t *__restrict__ starts, uint8_t *__restrict__ tail,
+    const int32_t *__restrict__ descriptor, const int32_t *__restrict__ count_total,
+    const int32_t *__restrict__ blocks, int64_t base, const uint8_t *__restrict__ extra_starts,
+    int64_t n_blocks, int64_t logical_numel, int S, int precomputed, int buffered) {
+    compact_block(source, lanes, starts, tail, descriptor, count_total, blocks, base,
+                  extra_starts, n_blocks, logical_numel, S, precomputed, buffered, blockIdx.x);
+}
+
+// The compaction of a batched compress: workgroup w compacts block
+// w - first_block[j] of job j into job j's reservation.
+__global__ __launch_bounds__(kLanes) void compact_batch_kernel(CompactBatch batch) {
+    const int32_t w = static_cast<int32_t>(blockIdx.x);
+    int j = 0;
+    for (int k = 1; k < batch.n_jobs; ++k)
+        if (w >= batch.first_block[k]) j = k;
+    const CompactBatchJob &job = batch.jobs[j];
+    compact_block(job.source, batch.arena, batch.arena, batch.arena, job.descriptor, job.counts,
+                  job.blocks, 0, job.extra_starts, job.n_blocks, job.logical_numel, batch.steps,
+                  0, 1, w - batch.first_block[j]);
 }
 
 // Waits of the compacting workgroups for workgroup 0's reservation: polls of
@@ -463,6 +489,12 @@ __global__ __launch_bounds__(kLanes) void scatter_fallback_kernel(
 }
 
 }  // namespace
+
+hipError_t launch_compact_batch(const CompactBatch &batch, uint32_t grid, hipStream_t stream) {
+    hipLaunchKernelGGL(compact_batch_kernel, dim3(grid), dim3(kLanes), 0, stream, batch);
+    return hipGetLastError();
+}
+
 }  // namespace lct
 
 using namespace lct;

@@ -38,16 +38,57 @@
 // Cross-workgroup values travel in a control array of 64-bit words tagged with
 // the call's epoch (lct_device.h), one array per stream, never cleared: a word
 // is current exactly when its tag is this call's epoch.
+#include "batch.h"
 #include "encode_core.h"
 #include "reserve.h"
 
 namespace lct {
 namespace {
 
-// One kernel per input kind (BF16 bits or precomputed exponent bytes), so
-// each carries one encoder variant and its registers.
+// The arena reservation of one tensor of a batch.  The batch's deferred frees
+// belong to job 0, whose bookkeeping applies them right after it takes the
+// lock and then posts `gate`; the other jobs' bookkeeping waits for that word
+// (bounded) before it asks for the lock, so every reservation of the batch
+// follows the frees, as the reservations of consecutive single launches would.
+// Job 0 is dispatched first and waits for nothing of the later jobs.  A gate
+// that does not arrive marks the tensor incomplete.  gate == nullptr (no
+// frees): plain LdsReserve.
+struct GatedReserve {
+    LdsReserve<false> inner;
+    uint64_t *gate;
+    bool post;
+    uint32_t epoch;
+    int32_t polls;
+    bool late;
+
+    __device__ void begin(int32_t *scratch) {
+        __shared__ int32_t arrived;
+        if (gate != nullptr && !post) {
+            if (threadIdx.x == 0) {
+                uint64_t word = control_load(gate);
+                for (int i = 0; !tagged_with(word, epoch) && i < polls; ++i) {
+                    __builtin_amdgcn_s_sleep(8);
+                    word = control_load(gate);
+                }
+                arrived = tagged_with(word, epoch) ? 1 : 0;
+            }
+            __syncthreads();
+            late = arrived == 0;
+        }
+        inner.begin(scratch);
+        if (gate != nullptr && post && threadIdx.x == 0) control_store(gate, tagged_word(epoch, 1));
+    }
+
+    __device__ void finish(int32_t request, int32_t *scratch, bool incomplete) {
+        inner.finish(request, scratch, incomplete || late);
+    }
+};
+
+// Workgroup `group` of one tensor's fused compress (the launch layout above):
+// the single launch runs it for blockIdx.x, the batched launch for its job's
+// share of the grid.  gate: GatedReserve's word (batched launches only).
 template <int kSidePolicy, bool kPrecomputed>
-__global__ __launch_bounds__(kLanes) void compress_kernel(
+__device__ __forceinline__ void compress_group(
     const void *__restrict__ source, uint8_t *__restrict__ side, int32_t *__restrict__ encoded,
     const int32_t *__restrict__ base_encode, const int32_t *__restrict__ base_decode,
     int32_t *__restrict__ center_out, int32_t *__restrict__ shifted_decode_out,
@@ -55,14 +96,13 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
     uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
     int32_t *__restrict__ blocks, int32_t *__restrict__ counts, uint64_t *__restrict__ control,
     uint32_t epoch, int32_t *__restrict__ descriptor, int32_t *__restrict__ buffer_meta,
-    int32_t max_free_regions, lct_pending_frees frees, uint64_t *host_totals, int32_t n_blocks,
-    int64_t logical_numel, int S, int W, int32_t lock_spins, int32_t polls) {
-    extern __shared__ uint32_t stage[];   // (W + 2) rows x 256 lanes, or the free list
+    int32_t max_free_regions, const lct_pending_frees &frees, uint64_t *host_totals,
+    int32_t n_blocks, int64_t logical_numel, int S, int W, int32_t lock_spins, int32_t polls,
+    int64_t group, uint64_t *gate, bool post_gate, uint32_t *stage) {
     __shared__ uint2 table[256];
     __shared__ __attribute__((aligned(16))) uint8_t slices[kWavesPerBlock * kSliceBytes];
     __shared__ int32_t scratch[kWavesPerBlock];
     __shared__ int32_t shared[2];
-    const int64_t group = blockIdx.x;
 
     if (group < n_groups && threadIdx.x < kWave) {
         // Samples group * 64 + lane (tables.py:15-49): the kept exponents' sum
@@ -114,9 +154,11 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
     // barriers, so it can hold the free list.
     PolledSummaries polled{control, epoch, n_blocks, polls, false};
     if (buffer_meta != nullptr) {
-        LdsReserve<false> reserve{AllocatorMeta(buffer_meta, max_free_regions, lock_spins),
-                                  descriptor, frees, reinterpret_cast<int32_t *>(stage), {}, -1,
-                                  kStatusOk};
+        GatedReserve reserve{
+            LdsReserve<false>{AllocatorMeta(buffer_meta, max_free_regions, lock_spins),
+                              descriptor, frees, reinterpret_cast<int32_t *>(stage), {}, -1,
+                              kStatusOk},
+            gate, post_gate, epoch, polls, false};
         scan_allocate<false>(polled, summaries, counts, blocks, n_blocks, reserve);
     } else {
         NoReserve reserve;
@@ -134,7 +176,62 @@ __global__ __launch_bounds__(kLanes) void compress_kernel(
     }
 }
 
+// One kernel per input kind (BF16 bits or precomputed exponent bytes), so
+// each carries one encoder variant and its registers.
+template <int kSidePolicy, bool kPrecomputed>
+__global__ __launch_bounds__(kLanes) void compress_kernel(
+    const void *__restrict__ source, uint8_t *__restrict__ side, int32_t *__restrict__ encoded,
+    const int32_t *__restrict__ base_encode, const int32_t *__restrict__ base_decode,
+    int32_t *__restrict__ center_out, int32_t *__restrict__ shifted_decode_out,
+    uint16_t *__restrict__ sample_values, int64_t sample_size, int32_t n_groups,
+    uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
+    int32_t *__restrict__ blocks, int32_t *__restrict__ counts, uint64_t *__restrict__ control,
+    uint32_t epoch, int32_t *__restrict__ descriptor, int32_t *__restrict__ buffer_meta,
+    int32_t max_free_regions, lct_pending_frees frees, uint64_t *host_totals, int32_t n_blocks,
+    int64_t logical_numel, int S, int W, int32_t lock_spins, int32_t polls) {
+    extern __shared__ uint32_t stage[];   // (W + 2) rows x 256 lanes, or the free list
+    compress_group<kSidePolicy, kPrecomputed>(
+        source, side, encoded, base_encode, base_decode, center_out, shifted_decode_out,
+        sample_values, sample_size, n_groups, extra_starts, summaries, blocks, counts, control,
+        epoch, descriptor, buffer_meta, max_free_regions, frees, host_totals, n_blocks,
+        logical_numel, S, W, lock_spins, polls, blockIdx.x, nullptr, false, stage);
+}
+
+// Several BF16 tensors into one TensorBuffer: job j takes workgroups
+// [first_group[j], first_group[j + 1]) and runs the single launch's layout
+// over them with its own control words.  Every wait stays inside one job
+// (plus the gate on job 0, dispatched first), so each job's waits end as in
+// its own launch.
+template <int kSidePolicy>
+__global__ __launch_bounds__(kLanes) void compress_batch_kernel(CompressBatch batch) {
+    extern __shared__ uint32_t stage[];
+    const int32_t w = static_cast<int32_t>(blockIdx.x);
+    int j = 0;
+    for (int k = 1; k < batch.n_jobs; ++k)
+        if (w >= batch.first_group[k]) j = k;
+    const CompressBatchJob &job = batch.jobs[j];
+    lct_pending_frees frees = batch.frees;
+    if (j != 0) frees.count = 0;
+    compress_group<kSidePolicy, false>(
+        job.source, job.side, job.encoded, job.base_encode, job.base_decode, job.center_out,
+        job.shifted_decode_out, job.sample_values, job.sample_size, job.n_groups,
+        job.extra_starts, job.summaries, job.blocks, job.counts, job.control, batch.epoch,
+        job.descriptor, batch.buffer_meta, batch.max_free_regions, frees, nullptr, job.n_blocks,
+        job.logical_numel, batch.steps, job.fixed_words, batch.lock_spins, batch.polls,
+        w - batch.first_group[j], batch.gate, j == 0, stage);
+}
+
 }  // namespace
+
+hipError_t launch_compress_batch(const CompressBatch &batch, uint32_t grid, size_t lds,
+                                 hipStream_t stream) {
+    const auto kernel = batch.steps == 128 ? compress_batch_kernel<kStreaming>
+                                     : compress_batch_kernel<0>;
+    if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(kernel), lds)) return e;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kLanes), lds, stream, batch);
+    return hipGetLastError();
+}
+
 }  // namespace lct
 
 using namespace lct;
@@ -207,4 +304,110 @@ extern "C" int32_t lct_encode_fused(
                        g.fixed_words,
                        lock_spins(), ready_polls());
     return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_compress_batch(const lct_compress_job *jobs, int32_t n_jobs,
+                                      uint8_t *extra_starts, int64_t extra_bytes,
+                                      int32_t *summaries, int64_t summary_words,
+                                      uint64_t *control, int64_t control_words, uint32_t epoch,
+                                      int32_t *buffer_meta, int32_t max_free_regions,
+                                      uint8_t *arena, const lct_pending_frees *frees,
+                                      hipStream_t stream) {
+    if (!jobs || !extra_starts || !summaries || !control || !buffer_meta || !arena)
+        return LCT_E_NULL;
+    if (n_jobs <= 0 || n_jobs > LCT_MAX_COMPRESS_BATCH) return LCT_E_ARG;
+    if (epoch == 0 || (reinterpret_cast<uintptr_t>(control) & 7) != 0) return LCT_E_ARG;
+    if (max_free_regions <= 0 || max_free_regions > 4096
+        || (max_free_regions & (max_free_regions - 1)) != 0)
+        return LCT_E_ARG;
+    CompressBatch batch{};
+    CompactBatch compact{};
+    batch.n_jobs = compact.n_jobs = n_jobs;
+    batch.buffer_meta = buffer_meta;
+    batch.max_free_regions = max_free_regions;
+    if (frees != nullptr) {
+        if (frees->count < 0 || frees->count > LCT_MAX_PENDING_FREES) return LCT_E_ARG;
+        for (int i = 0; i < frees->count; ++i)
+            if (frees->descriptor[i] == nullptr) return LCT_E_NULL;
+        batch.frees = *frees;
+    }
+    batch.epoch = epoch;
+    batch.steps = compact.steps = jobs[0].geometry.steps;
+    batch.lock_spins = lock_spins();
+    batch.polls = ready_polls();
+    // Word 0 of the control array is the frees' gate; job j's words follow
+    // those of jobs before it.
+    batch.gate = batch.frees.count > 0 ? control : nullptr;
+    int64_t groups = 0, blocks_total = 0, extra_used = 0, summary_used = 0, control_used = 1;
+    size_t lds = static_cast<size_t>(max_free_regions) * 8;
+    for (int j = 0; j < n_jobs; ++j) {
+        const lct_compress_job &in = jobs[j];
+        const lct_geometry &g = in.geometry;
+        if (!in.source || !in.side || !in.encoded || !in.base_encode || !in.base_decode
+            || !in.center_out || !in.shifted_decode_out || !in.blocks || !in.counts
+            || !in.descriptor)
+            return LCT_E_NULL;
+        if (!geometry_ok(g)) return LCT_E_GEOMETRY;
+        if (g.steps != batch.steps) return LCT_E_ARG;
+        if (in.logical_numel <= 0 || in.size <= 0 || in.size % g.block_symbols != 0
+            || in.logical_numel > in.size || in.logical_numel <= in.size - g.block_symbols)
+            return LCT_E_SIZE;
+        const int64_t nb = in.size / g.block_symbols;
+        if (nb > kMaxBlocks) return LCT_E_SIZE;
+        if (in.sample_size <= 0 || in.sample_size > kMaxSamples
+            || in.sample_size > in.logical_numel)
+            return LCT_E_SIZE;
+        if (in.sample_size != in.logical_numel && (in.sample_size & (in.sample_size - 1)) != 0)
+            return LCT_E_ARG;
+        if (((reinterpret_cast<uintptr_t>(in.encoded) | reinterpret_cast<uintptr_t>(in.source)
+              | reinterpret_cast<uintptr_t>(in.side)) & 15) != 0)
+            return LCT_E_ARG;
+        const int32_t n_groups = sample_groups(in.sample_size);
+        CompressBatchJob &job = batch.jobs[j];
+        job.source = in.source;
+        job.side = in.side;
+        job.encoded = in.encoded;
+        job.base_encode = in.base_encode;
+        job.base_decode = in.base_decode;
+        job.center_out = in.center_out;
+        job.shifted_decode_out = in.shifted_decode_out;
+        job.sample_values = in.sample_values;
+        job.extra_starts = extra_starts + extra_used;
+        job.summaries = summaries + summary_used;
+        job.blocks = in.blocks;
+        job.counts = in.counts;
+        job.descriptor = in.descriptor;
+        job.control = control + control_used;
+        job.sample_size = in.sample_size;
+        job.logical_numel = in.logical_numel;
+        job.n_groups = n_groups;
+        job.n_blocks = static_cast<int32_t>(nb);
+        job.fixed_words = g.fixed_words;
+        CompactBatchJob &c = compact.jobs[j];
+        c.source = in.source;
+        c.blocks = in.blocks;
+        c.counts = in.counts;
+        c.descriptor = in.descriptor;
+        c.extra_starts = job.extra_starts;
+        c.n_blocks = nb;
+        c.logical_numel = in.logical_numel;
+        batch.first_group[j] = static_cast<int32_t>(groups);
+        compact.first_block[j] = static_cast<int32_t>(blocks_total);
+        groups += nb > n_groups ? nb : n_groups;
+        blocks_total += nb;
+        extra_used += nb * kLanes;
+        summary_used += 5 * nb + 1;
+        control_used += kControlPartials + nb;
+        const size_t stage = static_cast<size_t>(g.fixed_words + 2) * kLanes * 4;
+        if (stage > lds) lds = stage;
+    }
+    if (extra_used > extra_bytes || summary_used > summary_words || control_used > control_words)
+        return LCT_E_SIZE;
+    batch.first_group[n_jobs] = static_cast<int32_t>(groups);
+    compact.first_block[n_jobs] = static_cast<int32_t>(blocks_total);
+    compact.arena = arena;
+    if (hipError_t e = launch_compress_batch(batch, static_cast<uint32_t>(groups), lds, stream))
+        return static_cast<int32_t>(e);
+    return static_cast<int32_t>(
+        launch_compact_batch(compact, static_cast<uint32_t>(blocks_total), stream));
 }

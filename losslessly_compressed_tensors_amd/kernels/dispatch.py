@@ -334,6 +334,29 @@ def encode_fused_pointers(source, side, encoded, sample_size, encode_table, deco
     return epoch
 
 
+def compress_batch_pointers(jobs, buffer, frees, device, stream) -> None:
+    """``lct_compress_batch``: the buffered compress of ``jobs`` (at most
+    ``hip.MAX_COMPRESS_BATCH`` ``hip.CompressJob``s with device addresses,
+    all of one step count) into ``buffer``, applying the deferred ``frees``
+    first, on the raw stream handle ``stream`` of ``device``."""
+    n_blocks = [job.size // job.geometry.block_symbols for job in jobs]
+    total = sum(n_blocks)
+    # One working array each, partitioned by the entry point in job order:
+    # extra starts (256 per block), summaries (5 nb + 1 per job) and control
+    # words (a gate word, then 64 + nb per job).
+    extra_starts, summaries = compress_workspace(device, total + len(jobs), total * 256)
+    control = control_array(device, total + (CONTROL_PARTIALS + 1) * len(jobs))
+    pending = hip.PendingFrees()
+    pending.count = len(frees)
+    for i, freed in enumerate(frees):
+        pending.descriptor[i] = freed.data_ptr()
+    array = (hip.CompressJob * len(jobs))(*jobs)
+    hip.call("lct_compress_batch", array, len(jobs), extra_starts.data_ptr(),
+             extra_starts.numel(), summaries.data_ptr(), summaries.numel(), control.data_ptr(),
+             control.numel(), _next_fused_epoch(), buffer.storage.data_ptr(),
+             buffer.max_free_regions, buffer.data.data_ptr(), hip.ctypes.byref(pending), stream)
+
+
 def compact_extra_pointers(source, lanes, starts, tail, descriptor, count, blocks, extra_starts,
                            size, logical_numel, geometry, buffered, stream) -> None:
     """``compact_extra`` over every block whose metadata ``encode_fused`` wrote

@@ -98,6 +98,31 @@ class DecodeJob(ctypes.Structure):
     ]
 
 
+MAX_COMPRESS_BATCH = 16   # LCT_MAX_COMPRESS_BATCH
+
+
+class CompressJob(ctypes.Structure):
+    """``lct_compress_job``: one tensor of a batched buffered compress."""
+
+    _fields_ = [
+        ("source", _ptr),
+        ("side", _ptr),
+        ("encoded", _ptr),
+        ("base_encode", _ptr),
+        ("base_decode", _ptr),
+        ("center_out", _ptr),
+        ("shifted_decode_out", _ptr),
+        ("sample_values", _ptr),
+        ("blocks", _ptr),
+        ("counts", _ptr),
+        ("descriptor", _ptr),
+        ("sample_size", _c_int64),
+        ("size", _c_int64),
+        ("logical_numel", _c_int64),
+        ("geometry", Geometry),
+    ]
+
+
 # name -> argument types (all entry points return int32).
 _SIGNATURES = {
     "lct_estimate_and_shift_tables": [_ptr, _c_int32, _c_int64, _c_int64, _ptr, _ptr, _ptr, _ptr,
@@ -150,6 +175,9 @@ _SIGNATURES = {
                          _ptr, _ptr, _ptr, _c_int64, ctypes.c_uint32, _ptr, _ptr, _c_int32,
                          ctypes.POINTER(PendingFrees), _ptr, _c_int64, _c_int64, Geometry,
                          _c_int32, _ptr],
+    "lct_compress_batch": [ctypes.POINTER(CompressJob), _c_int32, _ptr, _c_int64, _ptr, _c_int64,
+                           _ptr, _c_int64, ctypes.c_uint32, _ptr, _c_int32, _ptr,
+                           ctypes.POINTER(PendingFrees), _ptr],
     "lct_count_bad_streams": [_ptr, _ptr, _ptr, _c_int64, _c_int32, _ptr],
     "lct_compact_bad_streams": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _c_int64,
                                 _c_int32, _c_int64, _c_int32, _ptr],

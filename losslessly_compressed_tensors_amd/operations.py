@@ -10,6 +10,7 @@ from torch import Tensor
 
 from .codec.decode import decode as decode_dense
 from .codec.encode import encode as compress_dense
+from .codec.encode import encode_batch
 from .codec.pointwise import (
     ADD,
     MULTIPLY,
@@ -29,6 +30,22 @@ def compress(data: Tensor, distribution: Distribution | None = None,
     if distribution is None:
         distribution = Distribution()
     return compress_dense(data.detach(), distribution, buffer, allow_raw=allow_raw)
+
+
+def compress_batch(tensors, distribution=None, buffer: TensorBuffer | None = None) -> list:
+    """:func:`compress` of several GPU bfloat16 tensors into ``buffer``, one
+    fused compress launch and one compaction launch per 16 tensors (the
+    reference compresses one tensor per call).  ``distribution``: one for all,
+    or one per tensor.  The records equal those of :func:`compress` except
+    where in the buffer's arena each overflow region lies."""
+    tensors = [t.detach() for t in tensors]
+    if distribution is None or isinstance(distribution, Distribution):
+        distributions = [distribution or Distribution()] * len(tensors)
+    else:
+        distributions = [Distribution() if d is None else d for d in distribution]
+        if len(distributions) != len(tensors):
+            raise ValueError("one distribution per tensor")
+    return encode_batch(tensors, distributions, buffer)
 
 
 @torch.compiler.disable

@@ -183,6 +183,50 @@ def test_encode_fused_rejects_bad_arguments_before_launch(lib):
     assert call(meta=fake, frees=ctypes.byref(missing)) == LCT_E_NULL
 
 
+def test_compress_batch_rejects_bad_jobs_before_launch(lib):
+    """lct_compress_batch checks the job count, every job and the working
+    arrays' sizes before anything is launched (the fake pointers are never
+    dereferenced)."""
+    base = 1 << 20
+
+    def job(steps=128, words=12, blocks=4, logical=None, source=base, side=base, sample=4096):
+        size = blocks * 256 * steps
+        return hip.CompressJob(source, side, base, base, base, base, base, None, base, base,
+                               base, sample, size, size if logical is None else logical,
+                               hip.Geometry(256 * steps, 256, steps, words))
+
+    def call(jobs, extra=1 << 20, summaries=1 << 20, control=1 << 20, epoch=7, regions=256,
+             frees=None, control_address=base):
+        array = (hip.CompressJob * max(len(jobs), 1))(*jobs)
+        return lib.lct_compress_batch(array, len(jobs), base, extra, base, summaries,
+                                      control_address, control, epoch, base, regions, base,
+                                      frees, None)
+
+    two = [job(), job(blocks=9, logical=9 * 32768 - 5)]
+    assert call([]) == LCT_E_ARG                                       # no job
+    assert call([job()] * (hip.MAX_COMPRESS_BATCH + 1)) == LCT_E_ARG   # more than the table
+    assert call(two, epoch=0) == LCT_E_ARG                             # 0 matches a fresh array
+    assert call(two, control_address=base + 4) == LCT_E_ARG            # not 8-byte aligned
+    assert call(two, regions=100) == LCT_E_ARG                         # not a power of two
+    assert call([job(), job(steps=256, words=25)]) == LCT_E_ARG        # two step counts
+    assert call([job(), job(source=base + 2)]) == LCT_E_ARG            # not 16-byte aligned
+    assert call([job(), job(side=None)]) == LCT_E_NULL                 # a missing array
+    assert call([job(), job(sample=3000)]) == LCT_E_ARG                # neither n nor 2^k
+    assert call([job(), job(logical=3 * 32768)]) == LCT_E_SIZE         # a block of padding
+    assert call([job(), job(words=1)]) == LCT_E_GEOMETRY
+    # Working arrays: 256 extra starts per block, 5 nb + 1 summary words per
+    # job, a gate word and 64 + nb control words per job.
+    assert call(two, extra=13 * 256 - 1) == LCT_E_SIZE
+    assert call(two, summaries=5 * 13 + 2 - 1) == LCT_E_SIZE
+    assert call(two, control=1 + 2 * 64 + 13 - 1) == LCT_E_SIZE
+    too_many = hip.PendingFrees()
+    too_many.count = hip.MAX_PENDING_FREES + 1
+    assert call(two, frees=ctypes.byref(too_many)) == LCT_E_ARG
+    missing = hip.PendingFrees()
+    missing.count = 1
+    assert call(two, frees=ctypes.byref(missing)) == LCT_E_NULL
+
+
 def test_fused_update_encoders_reject_bad_bookkeeping_before_launch(lib):
     """lct_pointwise_encode_fused and lct_dual_encode_fused check their
     bookkeeping record (control array, epoch, buffer, frees) before anything

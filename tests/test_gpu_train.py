@@ -34,16 +34,22 @@ def _f32(*shape, seed, scale=1.0):
 
 @pytest.fixture()
 def layers_counting(monkeypatch):
-    """The layers module with its ``compress`` counted."""
+    """The layers module with the tensors it compresses counted (one
+    ``compress`` each, or one ``compress_batch`` for the queued ones)."""
     from losslessly_compressed_tensors_amd.components import layers
     calls = []
-    real = layers.compress
+    real, real_batch = layers.compress, layers.compress_batch
 
     def counting(x, *args, **kwargs):
         calls.append(tuple(x.shape))
         return real(x, *args, **kwargs)
 
+    def counting_batch(xs, *args, **kwargs):
+        calls.extend(tuple(x.shape) for x in xs)
+        return real_batch(xs, *args, **kwargs)
+
     monkeypatch.setattr(layers, "compress", counting)
+    monkeypatch.setattr(layers, "compress_batch", counting_batch)
     return layers, calls
 
 
