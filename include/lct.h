@@ -538,6 +538,62 @@ int32_t lct_pointwise_encode_fused(const int32_t *encoded, const uint8_t *side,
                                    int32_t alpha_is_one, int32_t beta_is_one,
                                    const lct_bookkeeping *bookkeeping, hipStream_t stream);
 
+/* ---- several fused updates of one operation with compressed output into one
+ * TensorBuffer, in three launches: the samplers of up to LCT_MAX_UPDATE_BATCH
+ * tensors (lct_pointwise_sample), their encoders with the in-launch
+ * bookkeeping (lct_pointwise_encode_fused, buffered) and their compactions
+ * (lct_compact_extra, buffered, precomputed = 1, source = exponents).  No
+ * counterpart in the reference, which updates one tensor per call
+ * (LCT/LCTensor.py:91-99 -> codec/pointwise.py:262-278): an update of a few
+ * codec blocks (a layer's weight) is bound by one block's latency per launch.
+ * Each job's outputs are those of its own sequence, except where in the
+ * arena its overflow region lies (the jobs reserve in the order their
+ * bookkeeping takes the arena lock); `frees` are applied before any job's
+ * reservation.  op/alpha/beta/flags as lct_pointwise_sample, shared by the
+ * jobs.  Working arrays, partitioned in job order: partials int32[sum 2 *
+ * ceil(sample_size / 64)], extra_starts uint8[sum nb*256], summaries
+ * int32[sum (5*nb + 1)], control uint64[1 + sum (64 + nb)] (the array of
+ * lct_encode_fused, with its zeroing and epoch rules).  All jobs share
+ * geometry.steps.  A bounded wait that gives up marks its tensor incomplete
+ * (status 7). */
+#define LCT_MAX_UPDATE_BATCH 8
+typedef struct {
+    const int32_t *encoded;        /* A, 16-byte aligned */
+    const uint8_t *side;           /* 16-byte aligned */
+    const int32_t *shifted_decode;
+    const int32_t *center;
+    int32_t has_overflow;
+    lct_overflow overflow;
+    const void *a_samples;         /* A's BF16 values at the sample positions, or NULL */
+    const void *other;             /* B: bf16[logical_numel] */
+    const int32_t *base_encode;    /* the result distribution's tables */
+    const int32_t *base_decode;
+    int32_t *center_out;           /* int32[1] */
+    int32_t *shifted_decode_out;   /* int32[1024] */
+    uint8_t *side_out;             /* uint8[size], 16-byte aligned */
+    int32_t *encoded_out;          /* int32[nb*256*W + 4] */
+    void *result_samples;          /* uint16[sample_size], or NULL */
+    uint8_t *exponents;            /* uint8[logical_numel] */
+    int32_t *counts;               /* int32[4] */
+    int32_t *blocks;               /* int32[3*nb] */
+    int32_t *descriptor;           /* int32[4] */
+    int64_t size;
+    int64_t logical_numel;
+    int64_t sample_size;
+    lct_geometry geometry;
+    int32_t rare_length;
+} lct_update_job;
+int32_t lct_pointwise_update_batch(const lct_update_job *jobs, int32_t n_jobs, int32_t op,
+                                   int32_t alpha_is_one, int32_t beta_is_one,
+                                   const float *alpha, const float *beta, int32_t *partials,
+                                   int64_t partial_words, uint8_t *extra_starts,
+                                   int64_t extra_bytes, int32_t *summaries,
+                                   int64_t summary_words, uint64_t *control,
+                                   int64_t control_words, uint32_t epoch,
+                                   int32_t *buffer_meta, int32_t max_free_regions,
+                                   uint8_t *arena, const lct_pending_frees *frees,
+                                   hipStream_t stream);
+
 /* ---- single-pass compressed-output alpha*A + B over two compressed
  * operands, step 1 of 2: replaces the center estimate that dispatch.py:33-48
  * makes over the exponent bytes written by dispatch.py:215-286 (dual_mapped,

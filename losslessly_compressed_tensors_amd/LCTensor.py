@@ -16,6 +16,7 @@ from .comp_tensor import CompressedTensor
 from .operations import (
     a_compA_add_B,
     a_compA_add_b_B,
+    a_compA_add_b_B_batch,
     a_compA_add_compB,
     compA_add_B,
     compress,
@@ -100,6 +101,27 @@ class LCTTensor(Tensor):
                                      dense_output=False, distribution=prev.distribution,
                                      buffer=prev.buffer)
         prev.free()
+
+    @staticmethod
+    def mul_add_many(tensors, alpha: Tensor, updates, beta: Tensor | None = None, *,
+                     alpha_is_one: bool = False) -> None:
+        """``t.mul_add_(alpha, u, beta)`` for each pair: the tensors that share
+        a buffer with one launch of each kind per 8 (``a_compA_add_b_B_batch``;
+        a weight's update is a few codec blocks, so one launch per tensor
+        would be bound by one block's latency), the others one by one."""
+        groups: dict[int, list] = {}
+        for tensor, update in zip(tensors, updates):
+            if tensor.x.buffer is None:
+                tensor.mul_add_(alpha, update, beta, alpha_is_one=alpha_is_one)
+            else:
+                groups.setdefault(id(tensor.x.buffer), []).append((tensor, update))
+        for members in groups.values():
+            results = a_compA_add_b_B_batch(
+                [t.x for t, _ in members], alpha, [u for _, u in members], beta,
+                alpha_is_one=alpha_is_one, buffer=members[0][0].x.buffer)
+            for (tensor, _), result in zip(members, results):
+                prev, tensor.x = tensor.x, result
+                prev.free()
 
     def add_comp_(self, update_comp: "LCTTensor", alpha: Tensor):
         """In place ``x <- x + alpha * update_comp`` with both compressed."""

@@ -325,6 +325,119 @@ def pointwise_scale_add_compressed(data: CompressedTensor, other: CompressedTens
                                       distribution=distribution)
 
 
+def fused_update_batch(items, operation: PointwiseOp, buffer: TensorBuffer, *,
+                       alpha: torch.Tensor | None = None, beta: torch.Tensor | None = None,
+                       alpha_is_one: bool = False) -> list[CompressedTensor]:
+    """``operation(compA, B)`` with compressed output into ``buffer`` for each
+    ``(A, B, result_distribution)`` of ``items``: the single-pass update of
+    ``pointwise_compressed_dense(..., dense_output=False)``, with one sampler,
+    one encoder and one compaction launch (``lct_pointwise_update_batch``)
+    per ``hip.MAX_UPDATE_BATCH`` tensors of one step count.  Each record equals
+    that call's, except where in the arena its overflow region lies.  Pairs
+    the batched launch does not take (RAW or empty A, a result geometry other
+    than A's) go through ``pointwise_compressed_dense`` one by one."""
+    if buffer is None:
+        raise ValueError("fused_update_batch stores into a TensorBuffer")
+    if buffer.capacity_bytes % 4:
+        raise ValueError("TensorBuffer capacity must be divisible by 4")
+    if operation is SCALAR_MUL_ADD and alpha is None:
+        raise ValueError("scalar_mul_add requires an alpha argument")
+    scaled = operation is SCALAR_MUL_ADD
+    alpha_is_one = (not scaled) or alpha_is_one
+    beta_is_one = (not scaled) or beta is None
+    alpha_arg = None if alpha_is_one else alpha
+    beta_arg = None if beta_is_one else beta
+    device = buffer.device
+    results: list[CompressedTensor | None] = [None] * len(items)
+    pending: dict[int, list] = {}
+    for index, (data, other, distribution) in enumerate(items):
+        result_distribution = distribution or data.distribution
+        if tuple(other.shape) != data.shape:
+            raise ValueError(f"{operation.name} expects tensors with the same shape")
+        if (data.layout != StorageLayout.COMPRESSED or data.logical_numel == 0
+                or geometry(result_distribution) != data.codec_geometry):
+            results[index] = pointwise_compressed_dense(
+                data, other, operation, alpha=alpha, beta=beta, alpha_is_one=alpha_is_one,
+                dense_output=False, buffer=buffer, distribution=result_distribution)
+            continue
+        dispatch.require_device(data.data, other)
+        other = other.contiguous().view(-1)
+        block_symbols, lanes, steps, fixed_words = data.codec_geometry
+        blocks = data.size // block_symbols
+        streams = blocks * lanes
+        n = data.logical_numel
+        _, _, rare_length = get_distribution_tables(data.distribution, device)
+        base_encode, base_decode, _ = get_distribution_tables(result_distribution, device)
+        sample_size = min(n, CENTER_SAMPLE_SIZE)
+        a_samples = data.sample_values
+        if a_samples is not None and a_samples.numel() != sample_size:
+            a_samples = None
+        payload_bytes = 4 * (streams * fixed_words + 4)
+        packed = torch.empty(data.size + payload_bytes, dtype=torch.uint8, device=device)
+        record = torch.empty(1033 + 3 * blocks, dtype=torch.int32, device=device)
+        result_samples = torch.empty(sample_size, dtype=torch.int16, device=device)
+        # Only the rows of overflowing streams are written (and read back by
+        # the compaction); the rest stays unwritten.
+        exponents = torch.empty(n, dtype=torch.uint8, device=device)
+        overflow = overlay_of(data)
+        p_side, p_record = packed.data_ptr(), record.data_ptr()
+        job = hip.UpdateJob()
+        job.encoded, job.side = data.data.data_ptr(), data.sign_mantissa.data_ptr()
+        job.shifted_decode = shifted_decode_table(data).data_ptr()
+        job.center = data.center.data_ptr()
+        job.has_overflow = int(overflow is not None)
+        if overflow is not None:
+            job.overflow = overflow.as_overflow()
+        job.a_samples = None if a_samples is None else a_samples.data_ptr()
+        job.other = other.data_ptr()
+        job.base_encode, job.base_decode = base_encode.data_ptr(), base_decode.data_ptr()
+        job.center_out, job.shifted_decode_out = p_record + 4 * 1032, p_record
+        job.side_out, job.encoded_out = p_side, p_side + data.size
+        job.result_samples = result_samples.data_ptr()
+        job.exponents = exponents.data_ptr()
+        job.counts, job.descriptor = p_record + 4 * 1024, p_record + 4 * 1028
+        job.blocks = p_record + 4 * 1033
+        job.size, job.logical_numel, job.sample_size = data.size, n, sample_size
+        job.geometry = hip.Geometry(block_symbols, lanes, steps, fixed_words)
+        job.rare_length = rare_length
+        pending.setdefault(steps, []).append(
+            (index, job, (data, other, exponents), packed, record, result_samples,
+             result_distribution, blocks, payload_bytes))
+    stream = torch._C._cuda_getCurrentRawStream(device.index)
+    for members in pending.values():
+        for start in range(0, len(members), hip.MAX_UPDATE_BATCH):
+            part = members[start:start + hip.MAX_UPDATE_BATCH]
+            frees = buffer._take_frees()
+            try:
+                dispatch.pointwise_update_batch_pointers(
+                    [m[1] for m in part], operation.code, alpha_is_one, beta_is_one, alpha_arg,
+                    beta_arg, buffer, frees, device, stream)
+            except BaseException:
+                buffer._restore_frees(frees)
+                raise
+            for (index, _, (data, _, _), packed, record, result_samples, result_distribution,
+                 blocks, payload_bytes) in part:
+                side, payload = packed.split_with_sizes((data.size, payload_bytes))
+                shifted_decode, counts, descriptor, center, blocks_out = record.split_with_sizes(
+                    (1024, 4, 4, 1, 3 * blocks))
+                count_view, used_view = counts.split_with_sizes((1, 1, 2))[:2]
+                results[index] = CompressedTensor(
+                    payload.view(torch.int32), data.size, side,
+                    fallback_blocks=blocks_out,
+                    fallback_buffer=buffer.data,
+                    fallback_descriptor=descriptor,
+                    buffer=buffer,
+                    fallback_count=count_view,
+                    fallback_used=used_view,
+                    distribution=result_distribution, center=center,
+                    decode_table=shifted_decode, shape=data.shape,
+                    layout=StorageLayout.COMPRESSED,
+                    stream_geometry=geometry(result_distribution),
+                    sample_values=result_samples,
+                )
+    return results
+
+
 def pointwise_compressed_dense(data: CompressedTensor, other: torch.Tensor,
                                operation: PointwiseOp, *, alpha: torch.Tensor | None = None,
                                beta: torch.Tensor | None = None, alpha_is_one: bool = False,
@@ -380,4 +493,5 @@ __all__ = [
     "ADD", "MULTIPLY", "SCALAR_MUL_ADD", "POINTWISE_OPS", "PointwiseOp",
     "DENSE_OUTPUT", "COMPRESSED_OUTPUT",
     "pointwise_compressed_dense", "pointwise_scale_add_compressed", "storage_of",
+    "fused_update_batch",
 ]

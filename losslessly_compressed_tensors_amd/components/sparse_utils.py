@@ -278,12 +278,27 @@ class SparseMuon:
             stacked = torch.stack([wide.reshape(-1, *shape[-2:]) for _, wide, _ in members])
             polar = _orthogonalize_wide(stacked.reshape(-1, *shape[-2:]), self.ns_iters)
             polar = polar.reshape(len(members), *shape)
+            params, updates = [], []
             for (index, _, tall), factor in zip(members, polar.unbind(0)):
                 param = self.params[index]
                 update = factor.transpose(-2, -1) if tall else factor
-                update = update.mul(_aspect_scale(param.size(-2), param.size(-1)))
-                self._apply(param, update)
+                params.append(param)
+                updates.append(update.mul(_aspect_scale(param.size(-2), param.size(-1))))
+            self._apply_many(params, updates)
         self.first_step = False
+
+    def _apply_many(self, params, updates) -> None:
+        """``_apply`` of each pair; the compressed weights with one fused-update
+        launch of each kind per 8 (``LCTTensor.mul_add_many``: each weight is
+        a few codec blocks)."""
+        compressed = [(p, u) for p, u in zip(params, updates) if isinstance(p, LCTTensor)]
+        for param, update in zip(params, updates):
+            if not isinstance(param, LCTTensor):
+                self._apply(param, update)
+        if compressed:
+            LCTTensor.mul_add_many([p for p, _ in compressed], self.decay,
+                                   [u for _, u in compressed], beta=self.neg_lr,
+                                   alpha_is_one=self.weight_decay == 0)
 
     def _apply(self, param, update: Tensor) -> None:
         """p <- (1 - lr wd) p - lr u."""

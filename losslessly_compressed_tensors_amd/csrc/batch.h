@@ -1,6 +1,7 @@
 // Job tables of the batched buffered compress (lct_compress_batch): the fused
 // compress of several tensors in one launch (compress.hip), then the
-// compaction of their overflow entries in one more (compaction.hip).  Both
+// compaction of their overflow entries in one more (compaction.hip), which
+// the batched fused update (lct_pointwise_update_batch) uses too.  The
 // tables travel in the kernel arguments; workgroup w works for the last job
 // whose first workgroup is at most w.
 #pragma once
@@ -48,7 +49,7 @@ struct CompressBatch {
 };
 
 // One tensor's compaction into its reservation (compact_blocks_kernel with
-// buffered = 1, BF16 source).
+// buffered = 1).
 struct CompactBatchJob {
     const void *source;
     const int32_t *blocks;
@@ -65,6 +66,7 @@ struct CompactBatch {
     CompactBatchJob jobs[LCT_MAX_COMPRESS_BATCH];
     uint8_t *arena;
     int32_t steps;
+    int32_t precomputed;   // sources are exponent bytes (fused updates), else BF16
 };
 
 // Launchers (the kernels live in their files' anonymous namespaces).

@@ -247,7 +247,7 @@ __global__ __launch_bounds__(kLanes) void compact_batch_kernel(CompactBatch batc
     const CompactBatchJob &job = batch.jobs[j];
     compact_block(job.source, batch.arena, batch.arena, batch.arena, job.descriptor, job.counts,
                   job.blocks, 0, job.extra_starts, job.n_blocks, job.logical_numel, batch.steps,
-                  0, 1, w - batch.first_block[j]);
+                  batch.precomputed, 1, w - batch.first_block[j]);
 }
 
 // Waits of the compacting workgroups for workgroup 0's reservation: polls of

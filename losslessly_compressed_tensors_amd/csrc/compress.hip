@@ -45,45 +45,6 @@
 namespace lct {
 namespace {
 
-// The arena reservation of one tensor of a batch.  The batch's deferred frees
-// belong to job 0, whose bookkeeping applies them right after it takes the
-// lock and then posts `gate`; the other jobs' bookkeeping waits for that word
-// (bounded) before it asks for the lock, so every reservation of the batch
-// follows the frees, as the reservations of consecutive single launches would.
-// Job 0 is dispatched first and waits for nothing of the later jobs.  A gate
-// that does not arrive marks the tensor incomplete.  gate == nullptr (no
-// frees): plain LdsReserve.
-struct GatedReserve {
-    LdsReserve<false> inner;
-    uint64_t *gate;
-    bool post;
-    uint32_t epoch;
-    int32_t polls;
-    bool late;
-
-    __device__ void begin(int32_t *scratch) {
-        __shared__ int32_t arrived;
-        if (gate != nullptr && !post) {
-            if (threadIdx.x == 0) {
-                uint64_t word = control_load(gate);
-                for (int i = 0; !tagged_with(word, epoch) && i < polls; ++i) {
-                    __builtin_amdgcn_s_sleep(8);
-                    word = control_load(gate);
-                }
-                arrived = tagged_with(word, epoch) ? 1 : 0;
-            }
-            __syncthreads();
-            late = arrived == 0;
-        }
-        inner.begin(scratch);
-        if (gate != nullptr && post && threadIdx.x == 0) control_store(gate, tagged_word(epoch, 1));
-    }
-
-    __device__ void finish(int32_t request, int32_t *scratch, bool incomplete) {
-        inner.finish(request, scratch, incomplete || late);
-    }
-};
-
 // Workgroup `group` of one tensor's fused compress (the launch layout above):
 // the single launch runs it for blockIdx.x, the batched launch for its job's
 // share of the grid.  gate: GatedReserve's word (batched launches only).
@@ -333,6 +294,7 @@ extern "C" int32_t lct_compress_batch(const lct_compress_job *jobs, int32_t n_jo
     }
     batch.epoch = epoch;
     batch.steps = compact.steps = jobs[0].geometry.steps;
+    compact.precomputed = 0;
     batch.lock_spins = lock_spins();
     batch.polls = ready_polls();
     // Word 0 of the control array is the frees' gate; job j's words follow

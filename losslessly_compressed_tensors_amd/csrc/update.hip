@@ -31,6 +31,9 @@
 // non-temporal stores of half lines wrote 16% more than the side bytes (C4:
 // 73.6 MB against 62.9 MB per launch; with the default policy 63.3 MB, at
 // equal kernel time).
+#include <algorithm>
+
+#include "batch.h"
 #include "pointwise_ops.h"
 #include "reserve.h"
 
@@ -70,6 +73,8 @@ struct KernelBookkeeping {
     lct_pending_frees frees;
     int32_t lock_spins;
     int32_t polls;
+    uint64_t *gate;      // batched launches: GatedReserve's word (nullptr: none)
+    int32_t post_gate;   // this job applies the frees and posts the gate
 };
 
 // After a block (every thread, past the summary's barriers): its overflow
@@ -101,8 +106,10 @@ __device__ __forceinline__ void publish_block(const KernelBookkeeping &bk,
     if (block != 0) return;
     PolledSummaries polled{bk.control, bk.epoch, static_cast<int32_t>(n_blocks), bk.polls, false};
     if (bk.buffer_meta != nullptr) {
-        LdsReserve<false> reserve{AllocatorMeta(bk.buffer_meta, bk.max_free_regions, bk.lock_spins),
-                                  bk.descriptor, bk.frees, lds_free_list, {}, -1, kStatusOk};
+        GatedReserve reserve{
+            LdsReserve<false>{AllocatorMeta(bk.buffer_meta, bk.max_free_regions, bk.lock_spins),
+                              bk.descriptor, bk.frees, lds_free_list, {}, -1, kStatusOk},
+            bk.gate, bk.post_gate != 0, bk.epoch, bk.polls, false};
         scan_allocate<false>(polled, summaries, bk.counts, bk.blocks,
                              static_cast<int32_t>(n_blocks), reserve);
     } else {
@@ -157,15 +164,17 @@ __device__ __forceinline__ void stream_overlay(const lct_overflow &ov, bool pres
 // when A was made) or, without it, from A's streams: the sampled stream's W
 // words are staged in this thread's LDS column and its pairs decoded up to the
 // sample's step.  The result's values go to result_samples when given.
-__global__ __launch_bounds__(kSampleGroup) void pointwise_sample_kernel(
-    OperandA a, const uint16_t *__restrict__ a_samples, const uint16_t *__restrict__ other,
-    OpArgs args, int64_t n_blocks, int64_t logical_numel, int64_t sample_size, int S, int W,
-    int rare, int32_t *__restrict__ partials, uint16_t *__restrict__ result_samples) {
-    extern __shared__ uint32_t words[];   // (W + 1) rows x kSampleGroup
+// Sample group `group` (the single launch's blockIdx.x); `words`: the dynamic
+// LDS, (W + 1) rows x kSampleGroup.
+__device__ __forceinline__ void pointwise_sample_group(
+    const OperandA &a, const uint16_t *__restrict__ a_samples, const uint16_t *__restrict__ other,
+    const OpArgs &args, int64_t n_blocks, int64_t logical_numel, int64_t sample_size, int S,
+    int W, int rare, int32_t *__restrict__ partials, uint16_t *__restrict__ result_samples,
+    int64_t group, uint32_t *words) {
     __shared__ DecodeTables tb;
     const int t = threadIdx.x;
     if (a_samples != nullptr) {
-        const int64_t i = static_cast<int64_t>(blockIdx.x) * kSampleGroup + t;
+        const int64_t i = group * kSampleGroup + t;
         const bool active = i < sample_size;
         const int shift = __builtin_ctzll(static_cast<uint64_t>(sample_size));
         uint32_t result = 0;
@@ -181,8 +190,8 @@ __global__ __launch_bounds__(kSampleGroup) void pointwise_sample_kernel(
         const int32_t sum = wave_sum(keep ? exp : 0);
         const int32_t kept = wave_sum(keep ? 1 : 0);
         if (t == 0) {
-            partials[2 * blockIdx.x] = sum;
-            partials[2 * blockIdx.x + 1] = kept;
+            partials[2 * group] = sum;
+            partials[2 * group + 1] = kept;
         }
         return;
     }
@@ -193,7 +202,7 @@ __global__ __launch_bounds__(kSampleGroup) void pointwise_sample_kernel(
     const OpParams p = load_op_params(args.op, args.alpha_is_one, args.beta_is_one, args.alpha,
                                       args.beta);
 
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kSampleGroup + t;
+    const int64_t i = group * kSampleGroup + t;
     const bool active = i < sample_size;
     const int shift = __builtin_ctzll(static_cast<uint64_t>(sample_size));
     const int64_t pos = active ? sample_position(i, logical_numel, sample_size, shift) : 0;
@@ -246,9 +255,18 @@ __global__ __launch_bounds__(kSampleGroup) void pointwise_sample_kernel(
     const int32_t sum = wave_sum(keep ? exp : 0);
     const int32_t kept = wave_sum(keep ? 1 : 0);
     if (t == 0) {
-        partials[2 * blockIdx.x] = sum;
-        partials[2 * blockIdx.x + 1] = kept;
+        partials[2 * group] = sum;
+        partials[2 * group + 1] = kept;
     }
+}
+
+__global__ __launch_bounds__(kSampleGroup) void pointwise_sample_kernel(
+    OperandA a, const uint16_t *__restrict__ a_samples, const uint16_t *__restrict__ other,
+    OpArgs args, int64_t n_blocks, int64_t logical_numel, int64_t sample_size, int S, int W,
+    int rare, int32_t *__restrict__ partials, uint16_t *__restrict__ result_samples) {
+    extern __shared__ uint32_t words[];   // (W + 1) rows x kSampleGroup
+    pointwise_sample_group(a, a_samples, other, args, n_blocks, logical_numel, sample_size, S, W,
+                           rare, partials, result_samples, blockIdx.x, words);
 }
 
 // ---- the fused decode -> operation -> encode kernel
@@ -785,17 +803,18 @@ __device__ __forceinline__ void update_block(int32_t form, bool full, const Upda
     }
 }
 
+// Codec block `block` of one fused update (the single launch's blockIdx.x);
+// `stage`: the dynamic LDS, window_stage_bytes(W) (A's payload).
 template <bool kBooked>
-__global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
-    OperandA a, const uint16_t *__restrict__ other, OpArgs args,
+__device__ __forceinline__ void pointwise_encode_block(
+    const OperandA &a, const uint16_t *__restrict__ other, const OpArgs &args,
     const int32_t *__restrict__ partials, int32_t n_groups,
     const int32_t *__restrict__ base_encode, const int32_t *__restrict__ base_decode,
     int32_t *__restrict__ center_out, int32_t *__restrict__ shifted_decode_out,
     uint8_t *__restrict__ side_out, int32_t *__restrict__ encoded_out,
     uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
     uint8_t *__restrict__ exponents, int64_t n_blocks, int64_t logical_numel, int S, int W,
-    int rare, KernelBookkeeping bk) {
-    extern __shared__ uint32_t stage[];   // A's payload: window_stage_bytes(W)
+    int rare, const KernelBookkeeping &bk, int64_t block, uint32_t *stage) {
     __shared__ FloatDecodeTables tb;
     __shared__ uint2 enc[256];
     __shared__ int32_t scratch[kWavesPerBlock];
@@ -808,7 +827,6 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     int32_t *map_offset = map_start + kLanes;
     int32_t *raw_encode = map_offset + kLanes;
     const int t = threadIdx.x;
-    const int64_t block = blockIdx.x;
     const int64_t row_base = block * S;
     const int64_t logical_base = row_base * kLanes;
     const uint32_t block_elems = static_cast<uint32_t>(S) * kLanes;
@@ -871,6 +889,126 @@ __global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
     const int32_t both = block_sum(overflow ? (S - extra) | (1 << 20) : 0, scratch);
     publish_block<kBooked>(bk, summaries, block, n_blocks, both >> 20, both & 0xFFFFF,
                            reinterpret_cast<int32_t *>(stage));
+}
+
+template <bool kBooked>
+__global__ __launch_bounds__(kLanes) void pointwise_encode_kernel(
+    OperandA a, const uint16_t *__restrict__ other, OpArgs args,
+    const int32_t *__restrict__ partials, int32_t n_groups,
+    const int32_t *__restrict__ base_encode, const int32_t *__restrict__ base_decode,
+    int32_t *__restrict__ center_out, int32_t *__restrict__ shifted_decode_out,
+    uint8_t *__restrict__ side_out, int32_t *__restrict__ encoded_out,
+    uint8_t *__restrict__ extra_starts, int32_t *__restrict__ summaries,
+    uint8_t *__restrict__ exponents, int64_t n_blocks, int64_t logical_numel, int S, int W,
+    int rare, KernelBookkeeping bk) {
+    extern __shared__ uint32_t stage[];   // A's payload: window_stage_bytes(W)
+    pointwise_encode_block<kBooked>(a, other, args, partials, n_groups, base_encode, base_decode,
+                                    center_out, shifted_decode_out, side_out, encoded_out,
+                                    extra_starts, summaries, exponents, n_blocks, logical_numel,
+                                    S, W, rare, bk, blockIdx.x, stage);
+}
+
+// ---- several fused updates of one operation in three launches
+//
+// A layer's weights are a few codec blocks each, so one update's sampler,
+// encoder and compaction are each bound by one block's latency; the batched
+// form runs up to LCT_MAX_UPDATE_BATCH tensors' samplers in one launch, their
+// encoders (with the in-launch bookkeeping, buffered) in a second and their
+// compactions in a third.  Workgroup w of a launch works for the last job
+// whose first workgroup is at most w.  The job tables travel in the kernel
+// arguments.
+
+struct UpdateSampleJob {
+    OperandA a;
+    const uint16_t *a_samples;
+    const uint16_t *other;
+    int32_t *partials;
+    uint16_t *result_samples;
+    int64_t n_blocks;
+    int64_t logical_numel;
+    int64_t sample_size;
+    int32_t steps;
+    int32_t fixed_words;
+    int32_t rare;
+};
+
+struct UpdateSampleBatch {
+    int32_t n_jobs;
+    int32_t first_group[LCT_MAX_UPDATE_BATCH + 1];
+    UpdateSampleJob jobs[LCT_MAX_UPDATE_BATCH];
+    OpArgs args;
+};
+
+__global__ __launch_bounds__(kSampleGroup) void pointwise_sample_batch_kernel(
+    UpdateSampleBatch batch) {
+    extern __shared__ uint32_t words[];   // (max W + 1) rows x kSampleGroup
+    const int32_t w = static_cast<int32_t>(blockIdx.x);
+    int j = 0;
+    for (int k = 1; k < batch.n_jobs; ++k)
+        if (w >= batch.first_group[k]) j = k;
+    const UpdateSampleJob &job = batch.jobs[j];
+    pointwise_sample_group(job.a, job.a_samples, job.other, batch.args, job.n_blocks,
+                           job.logical_numel, job.sample_size, job.steps, job.fixed_words,
+                           job.rare, job.partials, job.result_samples,
+                           w - batch.first_group[j], words);
+}
+
+struct UpdateEncodeJob {
+    OperandA a;
+    const uint16_t *other;
+    const int32_t *partials;
+    const int32_t *base_encode;
+    const int32_t *base_decode;
+    int32_t *center_out;
+    int32_t *shifted_decode_out;
+    uint8_t *side_out;
+    int32_t *encoded_out;
+    uint8_t *extra_starts;
+    int32_t *summaries;
+    uint8_t *exponents;
+    uint64_t *control;
+    int32_t *counts;
+    int32_t *blocks;
+    int32_t *descriptor;
+    int64_t n_blocks;
+    int64_t logical_numel;
+    int32_t n_groups;
+    int32_t steps;
+    int32_t fixed_words;
+    int32_t rare;
+};
+
+struct UpdateEncodeBatch {
+    int32_t n_jobs;
+    int32_t first_block[LCT_MAX_UPDATE_BATCH + 1];
+    UpdateEncodeJob jobs[LCT_MAX_UPDATE_BATCH];
+    OpArgs args;
+    int32_t *buffer_meta;
+    int32_t max_free_regions;
+    lct_pending_frees frees;   // job 0 applies them
+    uint64_t *gate;            // nullptr without frees
+    uint32_t epoch;
+    int32_t lock_spins;
+    int32_t polls;
+};
+
+__global__ __launch_bounds__(kLanes) void pointwise_encode_batch_kernel(UpdateEncodeBatch batch) {
+    extern __shared__ uint32_t stage[];   // window_stage_bytes(max W), or the free list
+    const int32_t w = static_cast<int32_t>(blockIdx.x);
+    int j = 0;
+    for (int k = 1; k < batch.n_jobs; ++k)
+        if (w >= batch.first_block[k]) j = k;
+    const UpdateEncodeJob &job = batch.jobs[j];
+    KernelBookkeeping bk{job.control, batch.epoch, job.counts, job.blocks, job.descriptor,
+                         batch.buffer_meta, batch.max_free_regions, batch.frees,
+                         batch.lock_spins, batch.polls, batch.gate, j == 0 ? 1 : 0};
+    if (j != 0) bk.frees.count = 0;
+    pointwise_encode_block<true>(job.a, job.other, batch.args, job.partials, job.n_groups,
+                                 job.base_encode, job.base_decode, job.center_out,
+                                 job.shifted_decode_out, job.side_out, job.encoded_out,
+                                 job.extra_starts, job.summaries, job.exponents, job.n_blocks,
+                                 job.logical_numel, job.steps, job.fixed_words, job.rare, bk,
+                                 w - batch.first_block[j], stage);
 }
 
 // ---- the two-compressed form: alpha * A + B with compressed output
@@ -1731,4 +1869,143 @@ extern "C" int32_t lct_dual_encode_fused(
                               shifted_decode_out, side_out, encoded_out, extra_starts, summaries,
                               exponents, size, logical_numel, g, rare_length, bookkeeping,
                               stream);
+}
+
+extern "C" int32_t lct_pointwise_update_batch(
+    const lct_update_job *jobs, int32_t n_jobs, int32_t op, int32_t alpha_is_one,
+    int32_t beta_is_one, const float *alpha, const float *beta, int32_t *partials,
+    int64_t partial_words, uint8_t *extra_starts, int64_t extra_bytes, int32_t *summaries,
+    int64_t summary_words, uint64_t *control, int64_t control_words, uint32_t epoch,
+    int32_t *buffer_meta, int32_t max_free_regions, uint8_t *arena,
+    const lct_pending_frees *frees, hipStream_t stream) {
+    if (!jobs || !partials || !extra_starts || !summaries || !control || !buffer_meta || !arena)
+        return LCT_E_NULL;
+    if (n_jobs <= 0 || n_jobs > LCT_MAX_UPDATE_BATCH) return LCT_E_ARG;
+    if (int32_t e = check_op(op, alpha_is_one, beta_is_one, alpha, beta)) return e;
+    if (epoch == 0 || (reinterpret_cast<uintptr_t>(control) & 7) != 0) return LCT_E_ARG;
+    if (max_free_regions <= 0 || max_free_regions > 4096
+        || (max_free_regions & (max_free_regions - 1)) != 0)
+        return LCT_E_ARG;
+    UpdateSampleBatch sample{};
+    UpdateEncodeBatch encode{};
+    CompactBatch compact{};
+    sample.n_jobs = encode.n_jobs = compact.n_jobs = n_jobs;
+    sample.args = encode.args = OpArgs{alpha, beta, op, alpha_is_one, beta_is_one};
+    encode.buffer_meta = buffer_meta;
+    encode.max_free_regions = max_free_regions;
+    if (frees != nullptr) {
+        if (frees->count < 0 || frees->count > LCT_MAX_PENDING_FREES) return LCT_E_ARG;
+        for (int i = 0; i < frees->count; ++i)
+            if (frees->descriptor[i] == nullptr) return LCT_E_NULL;
+        encode.frees = *frees;
+    }
+    encode.epoch = epoch;
+    encode.lock_spins = lock_spins();
+    encode.polls = ready_polls();
+    // Word 0 of the control array is the frees' gate; job j's words follow.
+    encode.gate = encode.frees.count > 0 ? control : nullptr;
+    compact.arena = arena;
+    compact.steps = 0;
+    compact.precomputed = 1;
+    int64_t groups = 0, blocks_total = 0, partial_used = 0, extra_used = 0, summary_used = 0,
+            control_used = 1;
+    int max_words = 0;
+    for (int j = 0; j < n_jobs; ++j) {
+        const lct_update_job &in = jobs[j];
+        const lct_geometry &g = in.geometry;
+        const lct_overflow *ov = in.has_overflow ? &in.overflow : nullptr;
+        if (int32_t e = check_operand(in.encoded, in.side, in.shifted_decode, in.center, ov))
+            return e;
+        if (!in.other || !in.base_encode || !in.base_decode || !in.center_out
+            || !in.shifted_decode_out || !in.side_out || !in.encoded_out || !in.exponents
+            || !in.counts || !in.blocks || !in.descriptor)
+            return LCT_E_NULL;
+        if (int32_t e = check_shape(in.size, in.logical_numel, g, in.rare_length)) return e;
+        if (int32_t e = check_samples(in.sample_size, in.logical_numel)) return e;
+        if (((reinterpret_cast<uintptr_t>(in.encoded) | reinterpret_cast<uintptr_t>(in.side)
+              | reinterpret_cast<uintptr_t>(in.side_out)) & 15) != 0)
+            return LCT_E_ARG;
+        const int64_t nb = in.size / g.block_symbols;
+        if (static_cast<int64_t>(g.fixed_words) * nb * kLanes * 4 >= (int64_t{1} << 31))
+            return LCT_E_SIZE;
+        // The compaction launch takes one step count for all its jobs.
+        if (compact.steps != 0 && compact.steps != g.steps) return LCT_E_ARG;
+        compact.steps = g.steps;
+        const int32_t n_groups = sample_groups(in.sample_size);
+        const OperandA a{in.encoded, in.side, in.shifted_decode, in.center,
+                         ov ? *ov : lct_overflow{}, ov != nullptr};
+        UpdateSampleJob &sj = sample.jobs[j];
+        sj.a = a;
+        sj.a_samples = static_cast<const uint16_t *>(in.a_samples);
+        sj.other = static_cast<const uint16_t *>(in.other);
+        sj.partials = partials + partial_used;
+        sj.result_samples = static_cast<uint16_t *>(in.result_samples);
+        sj.n_blocks = nb;
+        sj.logical_numel = in.logical_numel;
+        sj.sample_size = in.sample_size;
+        sj.steps = g.steps;
+        sj.fixed_words = g.fixed_words;
+        sj.rare = in.rare_length;
+        UpdateEncodeJob &ej = encode.jobs[j];
+        ej.a = a;
+        ej.other = sj.other;
+        ej.partials = sj.partials;
+        ej.base_encode = in.base_encode;
+        ej.base_decode = in.base_decode;
+        ej.center_out = in.center_out;
+        ej.shifted_decode_out = in.shifted_decode_out;
+        ej.side_out = in.side_out;
+        ej.encoded_out = in.encoded_out;
+        ej.extra_starts = extra_starts + extra_used;
+        ej.summaries = summaries + summary_used;
+        ej.exponents = in.exponents;
+        ej.control = control + control_used;
+        ej.counts = in.counts;
+        ej.blocks = in.blocks;
+        ej.descriptor = in.descriptor;
+        ej.n_blocks = nb;
+        ej.logical_numel = in.logical_numel;
+        ej.n_groups = n_groups;
+        ej.steps = g.steps;
+        ej.fixed_words = g.fixed_words;
+        ej.rare = in.rare_length;
+        CompactBatchJob &cj = compact.jobs[j];
+        cj.source = in.exponents;
+        cj.blocks = in.blocks;
+        cj.counts = in.counts;
+        cj.descriptor = in.descriptor;
+        cj.extra_starts = ej.extra_starts;
+        cj.n_blocks = nb;
+        cj.logical_numel = in.logical_numel;
+        sample.first_group[j] = static_cast<int32_t>(groups);
+        encode.first_block[j] = compact.first_block[j] = static_cast<int32_t>(blocks_total);
+        groups += n_groups;
+        blocks_total += nb;
+        partial_used += 2 * n_groups;
+        extra_used += nb * kLanes;
+        summary_used += 5 * nb + 1;
+        control_used += kControlPartials + nb;
+        if (g.fixed_words > max_words) max_words = g.fixed_words;
+    }
+    if (partial_used > partial_words || extra_used > extra_bytes
+        || summary_used > summary_words || control_used > control_words)
+        return LCT_E_SIZE;
+    if (blocks_total > 0x7FFFFFFF) return LCT_E_SIZE;
+    sample.first_group[n_jobs] = static_cast<int32_t>(groups);
+    encode.first_block[n_jobs] = compact.first_block[n_jobs] = static_cast<int32_t>(blocks_total);
+
+    const size_t sample_lds = static_cast<size_t>(max_words + 1) * kSampleGroup * 4;
+    hipLaunchKernelGGL(pointwise_sample_batch_kernel, dim3(static_cast<uint32_t>(groups)),
+                       dim3(kSampleGroup), sample_lds, stream, sample);
+    if (hipError_t e = hipGetLastError()) return static_cast<int32_t>(e);
+    const size_t encode_lds = std::max(static_cast<size_t>(window_stage_bytes(max_words)),
+                                       static_cast<size_t>(max_free_regions) * 8);
+    if (hipError_t e = reserve_dynamic_lds(
+            reinterpret_cast<const void *>(&pointwise_encode_batch_kernel), encode_lds))
+        return static_cast<int32_t>(e);
+    hipLaunchKernelGGL(pointwise_encode_batch_kernel, dim3(static_cast<uint32_t>(blocks_total)),
+                       dim3(kLanes), encode_lds, stream, encode);
+    if (hipError_t e = hipGetLastError()) return static_cast<int32_t>(e);
+    return static_cast<int32_t>(
+        launch_compact_batch(compact, static_cast<uint32_t>(blocks_total), stream));
 }

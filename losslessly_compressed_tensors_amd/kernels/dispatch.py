@@ -357,6 +357,33 @@ def compress_batch_pointers(jobs, buffer, frees, device, stream) -> None:
              buffer.max_free_regions, buffer.data.data_ptr(), hip.ctypes.byref(pending), stream)
 
 
+def pointwise_update_batch_pointers(jobs, op, alpha_is_one, beta_is_one, alpha, beta, buffer,
+                                    frees, device, stream) -> None:
+    """``lct_pointwise_update_batch``: the fused compressed-output updates of
+    ``jobs`` (at most ``hip.MAX_UPDATE_BATCH`` ``hip.UpdateJob``s with device
+    addresses, one step count) into ``buffer``, applying the deferred
+    ``frees`` first, on the raw stream handle ``stream`` of ``device``.
+    ``alpha``/``beta``: float32 device scalars or None."""
+    n_blocks = [job.size // job.geometry.block_symbols for job in jobs]
+    total = sum(n_blocks)
+    groups = sum(-(-job.sample_size // 64) for job in jobs)
+    extra_starts, summaries = compress_workspace(device, total + len(jobs), total * 256)
+    control = control_array(device, total + (CONTROL_PARTIALS + 1) * len(jobs))
+    partials = torch.empty(2 * groups, dtype=torch.int32, device=device)
+    pending = hip.PendingFrees()
+    pending.count = len(frees)
+    for i, freed in enumerate(frees):
+        pending.descriptor[i] = freed.data_ptr()
+    array = (hip.UpdateJob * len(jobs))(*jobs)
+    hip.call("lct_pointwise_update_batch", array, len(jobs), int(op), int(alpha_is_one),
+             int(beta_is_one), None if alpha is None else alpha.data_ptr(),
+             None if beta is None else beta.data_ptr(), partials.data_ptr(), partials.numel(),
+             extra_starts.data_ptr(), extra_starts.numel(), summaries.data_ptr(),
+             summaries.numel(), control.data_ptr(), control.numel(), _next_fused_epoch(),
+             buffer.storage.data_ptr(), buffer.max_free_regions, buffer.data.data_ptr(),
+             hip.ctypes.byref(pending), stream)
+
+
 def compact_extra_pointers(source, lanes, starts, tail, descriptor, count, blocks, extra_starts,
                            size, logical_numel, geometry, buffered, stream) -> None:
     """``compact_extra`` over every block whose metadata ``encode_fused`` wrote

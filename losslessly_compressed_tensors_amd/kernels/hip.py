@@ -123,6 +123,40 @@ class CompressJob(ctypes.Structure):
     ]
 
 
+MAX_UPDATE_BATCH = 8   # LCT_MAX_UPDATE_BATCH
+
+
+class UpdateJob(ctypes.Structure):
+    """``lct_update_job``: one tensor of a batched fused update."""
+
+    _fields_ = [
+        ("encoded", _ptr),
+        ("side", _ptr),
+        ("shifted_decode", _ptr),
+        ("center", _ptr),
+        ("has_overflow", _c_int32),
+        ("overflow", Overflow),
+        ("a_samples", _ptr),
+        ("other", _ptr),
+        ("base_encode", _ptr),
+        ("base_decode", _ptr),
+        ("center_out", _ptr),
+        ("shifted_decode_out", _ptr),
+        ("side_out", _ptr),
+        ("encoded_out", _ptr),
+        ("result_samples", _ptr),
+        ("exponents", _ptr),
+        ("counts", _ptr),
+        ("blocks", _ptr),
+        ("descriptor", _ptr),
+        ("size", _c_int64),
+        ("logical_numel", _c_int64),
+        ("sample_size", _c_int64),
+        ("geometry", Geometry),
+        ("rare_length", _c_int32),
+    ]
+
+
 # name -> argument types (all entry points return int32).
 _SIGNATURES = {
     "lct_estimate_and_shift_tables": [_ptr, _c_int32, _c_int64, _c_int64, _ptr, _ptr, _ptr, _ptr,
@@ -175,6 +209,10 @@ _SIGNATURES = {
                          _ptr, _ptr, _ptr, _c_int64, ctypes.c_uint32, _ptr, _ptr, _c_int32,
                          ctypes.POINTER(PendingFrees), _ptr, _c_int64, _c_int64, Geometry,
                          _c_int32, _ptr],
+    "lct_pointwise_update_batch": [ctypes.POINTER(UpdateJob), _c_int32, _c_int32, _c_int32,
+                                   _c_int32, _ptr, _ptr, _ptr, _c_int64, _ptr, _c_int64, _ptr,
+                                   _c_int64, _ptr, _c_int64, ctypes.c_uint32, _ptr, _c_int32,
+                                   _ptr, ctypes.POINTER(PendingFrees), _ptr],
     "lct_compress_batch": [ctypes.POINTER(CompressJob), _c_int32, _ptr, _c_int64, _ptr, _c_int64,
                            _ptr, _c_int64, ctypes.c_uint32, _ptr, _c_int32, _ptr,
                            ctypes.POINTER(PendingFrees), _ptr],

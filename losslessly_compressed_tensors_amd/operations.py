@@ -15,6 +15,7 @@ from .codec.pointwise import (
     ADD,
     MULTIPLY,
     SCALAR_MUL_ADD,
+    fused_update_batch,
     pointwise_compressed_dense,
     pointwise_scale_add_compressed,
 )
@@ -130,6 +131,40 @@ def a_compA_add_b_B(A_comp: CompressedTensor, a: Tensor, B: Tensor, b: Tensor, *
     return pointwise_compressed_dense(A_comp, B, SCALAR_MUL_ADD, alpha=a, beta=b,
                                       alpha_is_one=alpha_is_one, dense_output=dense_output,
                                       buffer=buffer, distribution=distribution)
+
+
+def a_compA_add_b_B_batch(A_comps, a: Tensor, Bs, b: Tensor | None = None, *,
+                          alpha_is_one: bool = False, buffer: TensorBuffer,
+                          distributions=None) -> list:
+    """``a * A + b * B`` (``a * A + B`` when ``b`` is None) with compressed
+    output into ``buffer`` for each pair: the ``dense_output=False`` form of
+    :func:`a_compA_add_B` / :func:`a_compA_add_b_B`, one sampler, encoder and
+    compaction launch per 8 tensors (the reference updates one tensor per
+    call).  ``distributions``: the results' (default: each A's).  The records
+    equal those of the one-tensor calls except where in the buffer's arena
+    each overflow region lies."""
+    A_comps, Bs = list(A_comps), list(Bs)
+    if len(A_comps) != len(Bs):
+        raise ValueError("one B per compressed A")
+    if not A_comps:
+        return []
+    device = A_comps[0].data.device
+    if not isinstance(a, torch.Tensor):
+        raise TypeError("alpha must be a torch.Tensor")
+    if b is None:
+        if not alpha_is_one:
+            a = _alpha_operand(a, device)
+    else:
+        for name, scalar in (("alpha", a), ("beta", b)):
+            if not isinstance(scalar, torch.Tensor):
+                raise TypeError(f"{name} must be a torch.Tensor")
+            if scalar.numel() != 1 or scalar.dtype != torch.float32 or scalar.device != device:
+                raise ValueError(
+                    f"{name} must be a float32 scalar on the compressed tensors' device")
+    if distributions is None:
+        distributions = [A.distribution for A in A_comps]
+    return fused_update_batch(list(zip(A_comps, Bs, distributions)), SCALAR_MUL_ADD, buffer,
+                              alpha=a, beta=b, alpha_is_one=alpha_is_one)
 
 
 def a_compA_add_compB(A_comp: CompressedTensor, a: Tensor, B_comp: CompressedTensor, *,

@@ -227,6 +227,58 @@ def test_compress_batch_rejects_bad_jobs_before_launch(lib):
     assert call(two, frees=ctypes.byref(missing)) == LCT_E_NULL
 
 
+def test_update_batch_rejects_bad_jobs_before_launch(lib):
+    """lct_pointwise_update_batch checks the job count, the operation, every
+    job and the working arrays' sizes before anything is launched (the fake
+    pointers are never dereferenced)."""
+    base = 1 << 20
+
+    def job(steps=128, words=12, blocks=4, logical=None, side_out=base, sample=4096, rare=5):
+        size = blocks * 256 * steps
+        j = hip.UpdateJob()
+        j.encoded = j.side = j.shifted_decode = j.center = base
+        j.other = j.base_encode = j.base_decode = j.center_out = j.shifted_decode_out = base
+        j.side_out = side_out
+        j.encoded_out = j.exponents = j.counts = j.blocks = j.descriptor = base
+        j.size, j.logical_numel = size, size if logical is None else logical
+        j.sample_size = sample
+        j.geometry = hip.Geometry(256 * steps, 256, steps, words)
+        j.rare_length = rare
+        return j
+
+    def call(jobs, op=2, alpha_is_one=1, beta_is_one=1, partials=1 << 20, extra=1 << 20,
+             summaries=1 << 20, control=1 << 20, epoch=7, regions=256, frees=None):
+        array = (hip.UpdateJob * max(len(jobs), 1))(*jobs)
+        return lib.lct_pointwise_update_batch(array, len(jobs), op, alpha_is_one, beta_is_one,
+                                              None, None, base, partials, base, extra, base,
+                                              summaries, base, control, epoch, base, regions,
+                                              base, frees, None)
+
+    two = [job(), job(blocks=9, logical=9 * 32768 - 5)]
+    assert call([]) == LCT_E_ARG                                      # no job
+    assert call([job()] * (hip.MAX_UPDATE_BATCH + 1)) == LCT_E_ARG    # more than the table
+    assert call(two, op=3) == LCT_E_ARG                               # no such operation
+    assert call(two, alpha_is_one=0) == LCT_E_NULL                    # alpha needed, absent
+    assert call(two, epoch=0) == LCT_E_ARG                            # 0 matches a fresh array
+    assert call(two, regions=100) == LCT_E_ARG                        # not a power of two
+    assert call([job(), job(steps=256, words=25)]) == LCT_E_ARG       # two step counts
+    assert call([job(), job(side_out=base + 4)]) == LCT_E_ARG         # not 16-byte aligned
+    assert call([job(), job(sample=3000)]) == LCT_E_ARG               # neither n nor 2^k
+    assert call([job(), job(rare=9)]) == LCT_E_ARG                    # rare length above 8
+    assert call([job(), job(logical=3 * 32768)]) == LCT_E_SIZE        # a block of padding
+    assert call([job(), job(words=1)]) == LCT_E_GEOMETRY
+    # Working arrays: 2 partial words per 64 samples, 256 extra starts per
+    # block, 5 nb + 1 summary words per job, a gate word and 64 + nb control
+    # words per job.
+    assert call(two, partials=2 * 64 * 2 - 1) == LCT_E_SIZE
+    assert call(two, extra=13 * 256 - 1) == LCT_E_SIZE
+    assert call(two, summaries=5 * 13 + 2 - 1) == LCT_E_SIZE
+    assert call(two, control=1 + 2 * 64 + 13 - 1) == LCT_E_SIZE
+    too_many = hip.PendingFrees()
+    too_many.count = hip.MAX_PENDING_FREES + 1
+    assert call(two, frees=ctypes.byref(too_many)) == LCT_E_ARG
+
+
 def test_fused_update_encoders_reject_bad_bookkeeping_before_launch(lib):
     """lct_pointwise_encode_fused and lct_dual_encode_fused check their
     bookkeeping record (control array, epoch, buffer, frees) before anything

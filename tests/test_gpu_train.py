@@ -490,15 +490,16 @@ def test_config5_full_shape_all_compressed_weight_update_matches_oracle(monkeypa
     assert all(isinstance(p, LCTTensor) for p in watched.values())
     before = {name: bits_of(p.decompress()) for name, p in watched.items()}
     seen = {}
-    real_apply = sparse_utils.SparseMuon._apply
+    real_apply_many = sparse_utils.SparseMuon._apply_many
 
-    def recording_apply(self, param, update):
-        for name, p in watched.items():
-            if param is p:
-                seen[name] = bits_of(update)
-        return real_apply(self, param, update)
+    def recording_apply_many(self, params, updates):
+        for param, update in zip(params, updates):
+            for name, p in watched.items():
+                if param is p:
+                    seen[name] = bits_of(update)
+        return real_apply_many(self, params, updates)
 
-    monkeypatch.setattr(sparse_utils.SparseMuon, "_apply", recording_apply)
+    monkeypatch.setattr(sparse_utils.SparseMuon, "_apply_many", recording_apply_many)
     _full_steps(gpt, model, optimizers, 1)
     muon = optimizers[1]
     decay = float(np.float32(1 - muon.lr * muon.weight_decay))
