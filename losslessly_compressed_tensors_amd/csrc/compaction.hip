@@ -44,12 +44,39 @@ struct BlockEntries {
     int32_t first_tail;   // tail byte threadIdx.x of the block (if < bytes)
 };
 
-// Tail byte i of `block`: int8(e - 127) of the exponent at its logical
+// The block's source elements (BF16 bits, or exponent bytes when
+// precomputed) as a buffer resource over the part inside the tensor: loads
+// past the tensor's end return 0, which both kinds map to int8(0 - 127) = -127,
+// the tail byte of a padding position.  Buffer accesses cannot alias LDS, so
+// the compiler keeps them in flight across the entry arrays' LDS accesses (the
+// generic pointers they replace made every load wait for the LDS stores
+// before it, one load latency per tail byte).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_source(const void *__restrict__ source,
+                                                               int64_t block, int S,
+                                                               int64_t logical_numel,
+                                                               int precomputed) {
+    const int64_t first = block * S * kLanes;
+    const int64_t left = logical_numel - first;
+    const int64_t valid = left < int64_t{S} * kLanes ? (left > 0 ? left : 0) : int64_t{S} * kLanes;
+    const int64_t elem = precomputed ? 1 : 2;
+    return make_rsrc(static_cast<const uint8_t *>(source) + first * elem,
+                     static_cast<uint32_t>(valid * elem));
+}
+
+// int8(e - 127) of the element at `offset` within the block.
+__device__ __forceinline__ int32_t tail_value(__amdgpu_buffer_rsrc_t src, uint32_t offset,
+                                              int precomputed) {
+    if (precomputed)
+        return static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b8(src, offset, 0, 0)) - 127;
+    const uint32_t bits = __builtin_amdgcn_raw_buffer_load_b16(src, offset * 2u, 0, 0);
+    return static_cast<int32_t>((bits >> 7) & 255u) - 127;
+}
+
+// Tail byte i of the block: int8(e - 127) of the exponent at its logical
 // position (-127 past the tensor's end), from the entries in LDS.
-__device__ __forceinline__ int32_t tail_byte(const void *__restrict__ source, int32_t i,
-                                             int32_t count, int64_t block, int64_t logical_numel,
-                                             int S, int precomputed,
-                                             const int32_t *entry_offset,
+__device__ __forceinline__ int32_t tail_byte(__amdgpu_buffer_rsrc_t src, int32_t i,
+                                             int32_t count, int64_t block, int S,
+                                             int precomputed, const int32_t *entry_offset,
                                              const int32_t *entry_start,
                                              const int32_t *entry_lane) {
     // Last entry whose offset is <= i.
@@ -61,12 +88,9 @@ __device__ __forceinline__ int32_t tail_byte(const void *__restrict__ source, in
     }
     const int64_t row_base = block * S;
     const int32_t row = entry_start[lo] + (i - entry_offset[lo]);
-    const int64_t logical = (row_base + row) * kLanes
-        + (entry_lane[lo] ^ static_cast<int32_t>((row_base + row) & 254));
-    if (logical >= logical_numel) return -127;
-    if (precomputed) return static_cast<int32_t>(static_cast<const uint8_t *>(source)[logical]) - 127;
-    const int32_t bits = static_cast<const uint16_t *>(source)[logical];
-    return ((bits >> 7) & 255) - 127;
+    const uint32_t offset = static_cast<uint32_t>(row) * kLanes
+        + static_cast<uint32_t>(entry_lane[lo] ^ static_cast<int32_t>((row_base + row) & 254));
+    return tail_value(src, offset, precomputed);
 }
 
 // With `source` given, the block's first 256 tail bytes are also read here
@@ -96,8 +120,9 @@ __device__ __forceinline__ BlockEntries rank_block_start(int32_t start, int64_t 
     }
     __syncthreads();
     e.first_tail = source != nullptr && t < e.bytes
-                       ? tail_byte(source, t, e.count, block, logical_numel, S, precomputed,
-                                   entry_offset, entry_start, entry_lane)
+                       ? tail_byte(block_source(source, block, S, logical_numel, precomputed), t,
+                                   e.count, block, S, precomputed, entry_offset, entry_start,
+                                   entry_lane)
                        : 0;
     return e;
 }
@@ -115,6 +140,101 @@ __device__ __forceinline__ BlockEntries rank_block(const uint8_t *__restrict__ e
                             precomputed);
 }
 
+// Tail bytes of a block with many of them, through LDS: the overflowing rows
+// are staged 64 at a time as exponent bytes (each logical row read whole and
+// contiguous, each byte put at its storage lane: lane l of row r holds logical
+// column l ^ (r & 254)), and then each wave writes whole entries' runs for
+// those rows, one contiguous store of up to 64 bytes per entry and tile, lane j
+// taking row j of the tile.  The staged rows are 260 bytes apart, so the 64
+// lanes' reads of one column fall in 64 different banks.  The search path
+// below costs about one LDS round trip per search step (8 for 256 entries) per
+// byte and thread, and its loads and stores touch one cache line per byte:
+// with 52 KB of tails in one block of 32768 elements it took the compaction to
+// 153 us.
+constexpr int kTileRows = 64;
+constexpr int kTileStride = kLanes + 4;
+constexpr int kStagedTailBytesPerStep = 16;   // take this path from 16 x S tail bytes on
+
+__device__ __forceinline__ void write_tails_staged(__amdgpu_buffer_rsrc_t src,
+                                                   __amdgpu_buffer_rsrc_t dst,
+                                                   const BlockEntries &e,
+                                                   const int32_t *entry_offset,
+                                                   const int32_t *entry_start,
+                                                   const int32_t *entry_lane, int64_t block,
+                                                   int S, int precomputed, uint32_t valid) {
+    __shared__ uint8_t tile[kTileRows * kTileStride];
+    __shared__ int32_t wave_first[kWavesPerBlock];
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = t / kWave;
+    // The first row any entry overflows at (entries <= 256: one per thread).
+    const int32_t mine = wave_min(t < e.count ? entry_start[t] : S);
+    if (lane == 0) wave_first[wave] = mine;
+    __syncthreads();
+    int32_t first_row = wave_first[0];
+    for (int w = 1; w < kWavesPerBlock; ++w) first_row = min(first_row, wave_first[w]);
+    const int64_t row_base = block * S;
+    for (int t0 = first_row & ~(kTileRows - 1); t0 < S; t0 += kTileRows) {
+        // Stage rows t0 .. t0 + 63: thread t takes elements 4t .. 4t + 3 of
+        // each 1024-element quarter of the tile (4 rows), 16 quarters.
+        // All sixteen loads of a thread in flight at once.
+#pragma unroll
+        for (int q = 0; q < kTileRows / 4; ++q) {
+            const int r_local = q * 4 + (t >> 6);
+            const uint32_t mask = static_cast<uint32_t>((row_base + t0 + r_local) & 254);
+            const uint32_t col = static_cast<uint32_t>(t & 63) * 4u;
+            const uint32_t offset = static_cast<uint32_t>(t0 + r_local) * kLanes + col;
+            // Four elements: 8 bytes of BF16 or 4 exponent bytes (0 past the
+            // tensor's end, which gives -127 as in tail_value).  A wide access
+            // that straddles the resource's end reads as 0 whole, so the four
+            // that hold the tensor's last element load one by one.
+            uint32_t e4[4];
+            if (offset < valid && offset + 4 > valid) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    e4[k] = static_cast<uint32_t>(tail_value(src, offset + k, precomputed));
+            } else if (precomputed) {
+                const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(src, offset, 0, 0);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) e4[k] = ((w >> (8 * k)) & 255u) - 127u;
+            } else {
+                using u32x2 = __attribute__((ext_vector_type(2))) uint32_t;
+                const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(src, offset * 2u, 0, 0);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    e4[k] = ((w[k >> 1] >> (16 * (k & 1) + 7)) & 255u) - 127u;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                tile[r_local * kTileStride + ((col + k) ^ mask)] = static_cast<uint8_t>(e4[k]);
+        }
+        __syncthreads();
+        // Wave w writes entries w, w + 4, ...: lane j takes row t0 + j; four
+        // entries at a time, so their LDS reads overlap.
+        const int32_t row = t0 + lane;
+        for (int k0 = wave; k0 < e.count; k0 += 4 * kWavesPerBlock) {
+            int32_t start[4], offset[4];
+            uint32_t value[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int k = k0 + u * kWavesPerBlock;
+                const bool present = k < e.count;
+                start[u] = present ? entry_start[k] : S;   // S: no row of this tile
+                offset[u] = present ? entry_offset[k] : 0;
+                value[u] = tile[lane * kTileStride + (present ? entry_lane[k] : 0)];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                __builtin_amdgcn_raw_buffer_store_b8(
+                    static_cast<uint8_t>(value[u]), dst,
+                    row >= start[u] && row < S ? static_cast<uint32_t>(offset[u] + (row - start[u]))
+                                               : 0x80000000u,
+                    0, 0);
+        }
+        __syncthreads();   // the tile is restaged next
+    }
+}
+
 __device__ __forceinline__ void write_block(
     const void *__restrict__ source, uint8_t *__restrict__ lanes, uint8_t *__restrict__ starts,
     uint8_t *__restrict__ tail, int64_t lane_off, int64_t start_off, int64_t tail_off,
@@ -127,13 +247,27 @@ __device__ __forceinline__ void write_block(
         starts[start_off + first + e.rank] = static_cast<uint8_t>(e.start);
     }
     uint8_t *out = tail + tail_off + byte_base;
+    const __amdgpu_buffer_rsrc_t src = block_source(source, block, S, logical_numel, precomputed);
+    const __amdgpu_buffer_rsrc_t dst = make_rsrc(out, static_cast<uint32_t>(e.bytes));
+    if (e.bytes >= kStagedTailBytesPerStep * S) {
+        // Many tail bytes: staged rows and whole runs per entry (above), so
+        // no byte needs the entry search.
+        const int64_t left = logical_numel - block * S * kLanes;
+        write_tails_staged(src, dst, e, entry_offset, entry_start, entry_lane, block, S,
+                           precomputed,
+                           static_cast<uint32_t>(left < int64_t{S} * kLanes ? left
+                                                                            : int64_t{S} * kLanes));
+        return;
+    }
     // Byte t may have been read by rank_block already (prefetched).  The rest
     // go kTailBatch per thread at a time, every load issued before the batch's
     // stores, so a block with many tail bytes waits for one load latency per
     // batch instead of one per byte.
     int32_t i = t;
     if (prefetched) {
-        if (i < e.bytes) out[i] = static_cast<uint8_t>(e.first_tail);
+        __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(e.first_tail), dst,
+                                             i < e.bytes ? static_cast<uint32_t>(i) : 0x80000000u,
+                                             0, 0);
         i += kLanes;
     }
     constexpr int kTailBatch = 4;
@@ -142,14 +276,17 @@ __device__ __forceinline__ void write_block(
 #pragma unroll
         for (int k = 0; k < kTailBatch; ++k) {
             const int32_t j = i + k * kLanes;
-            x[k] = j < e.bytes ? tail_byte(source, j, e.count, block, logical_numel, S,
-                                           precomputed, entry_offset, entry_start, entry_lane)
+            x[k] = j < e.bytes ? tail_byte(src, j, e.count, block, S, precomputed, entry_offset,
+                                           entry_start, entry_lane)
                                : 0;
         }
 #pragma unroll
         for (int k = 0; k < kTailBatch; ++k) {
             const int32_t j = i + k * kLanes;
-            if (j < e.bytes) out[j] = static_cast<uint8_t>(x[k]);
+            __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(x[k]), dst,
+                                                 j < e.bytes ? static_cast<uint32_t>(j)
+                                                             : 0x80000000u,
+                                                 0, 0);
         }
     }
     __syncthreads();   // the entry arrays are reused by the next block
