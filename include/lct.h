@@ -675,6 +675,22 @@ int32_t lct_buffer_free(int32_t *meta, int32_t max_free_regions,
                         int32_t *descriptor, int32_t *status_out,
                         hipStream_t stream);
 
+/* ---- several frees of one TensorBuffer in one launch.  No counterpart in
+ * the reference, which launches _free_storage_kernel once per descriptor
+ * (LCT/kernels/tensor_buffer_ops.py:5-15); it is for callers that free many
+ * compressed tensors between two reservations (a training step's saved
+ * activations and replaced optimizer state).  descriptors: `count` (1 to
+ * LCT_MAX_FREE_BATCH) device descriptor pointers.  One workgroup takes the
+ * arena lock once and frees them in order, each as lct_buffer_free would (a
+ * descriptor listed twice is freed once; the second gets status 4); the free
+ * list and descriptors end as after lct_buffer_free on each in turn.
+ * status_out: device int32[count] ({0, 3, 4, 6} as lct_buffer_free), or
+ * NULL. */
+#define LCT_MAX_FREE_BATCH 32
+int32_t lct_buffer_free_batch(int32_t *meta, int32_t max_free_regions,
+                              int32_t *const *descriptors, int32_t count,
+                              int32_t *status_out, hipStream_t stream);
+
 /* ---- buffered compress that allocates nothing.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).

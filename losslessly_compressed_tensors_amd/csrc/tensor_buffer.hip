@@ -2,7 +2,8 @@
 //
 // Launch-for-launch replacements of LCT/kernels/tensor_buffer.py:18-34
 // (_reset_kernel), :37-91 (_allocate_kernel) and :182-192
-// (_free_storage_kernel); the algorithms live in allocator.h.
+// (_free_storage_kernel), plus several frees in one launch; the algorithms
+// live in allocator.h.
 #include <atomic>
 
 #include "allocator.h"
@@ -53,6 +54,32 @@ __global__ __launch_bounds__(kLanes) void buffer_free_kernel(int32_t *__restrict
     if (threadIdx.x == 0) status_out[0] = status;
 }
 
+// Descriptors of one lct_buffer_free_batch launch (kernel arguments).
+struct FreeBatch {
+    int32_t count;
+    int32_t *descriptor[LCT_MAX_FREE_BATCH];
+};
+
+// The frees of lct_buffer_free in order under one hold of the lock: each
+// allocator_free_locked ends with a barrier after its metadata writes, and the
+// workgroup shares one vector L1, so the next free reads the updated list.
+__global__ __launch_bounds__(kLanes) void buffer_free_batch_kernel(int32_t *__restrict__ meta,
+                                                                   int32_t regions,
+                                                                   FreeBatch batch,
+                                                                   int32_t *__restrict__ status_out,
+                                                                   int32_t lock_spins) {
+    __shared__ int32_t scratch[kWavesPerBlock];
+    __shared__ int32_t flag;
+    const AllocatorMeta m(meta, regions, lock_spins);
+    const int32_t held = allocator_lock(m.lock, &flag, m.spins);
+    for (int32_t j = 0; j < batch.count; ++j) {
+        const int32_t status =
+            held < 0 ? kStatusLock : allocator_free_locked(m, batch.descriptor[j], scratch);
+        if (threadIdx.x == 0 && status_out != nullptr) status_out[j] = status;
+    }
+    if (held >= 0) allocator_unlock(m.lock, held);
+}
+
 bool regions_ok(int32_t r) { return r > 0 && r <= 4096 && (r & (r - 1)) == 0; }
 
 }  // namespace
@@ -97,6 +124,23 @@ extern "C" int32_t lct_buffer_free(int32_t *meta, int32_t max_free_regions,
     if (!regions_ok(max_free_regions)) return LCT_E_ARG;
     hipLaunchKernelGGL(buffer_free_kernel, dim3(1), dim3(kLanes), 0, stream, meta,
                        max_free_regions, descriptor, status_out, lock_spins());
+    return static_cast<int32_t>(hipGetLastError());
+}
+
+extern "C" int32_t lct_buffer_free_batch(int32_t *meta, int32_t max_free_regions,
+                                         int32_t *const *descriptors, int32_t count,
+                                         int32_t *status_out, hipStream_t stream) {
+    if (!meta || !descriptors) return LCT_E_NULL;
+    if (!regions_ok(max_free_regions) || count < 1 || count > LCT_MAX_FREE_BATCH)
+        return LCT_E_ARG;
+    FreeBatch batch{};
+    batch.count = count;
+    for (int32_t j = 0; j < count; ++j) {
+        if (!descriptors[j]) return LCT_E_NULL;
+        batch.descriptor[j] = descriptors[j];
+    }
+    hipLaunchKernelGGL(buffer_free_batch_kernel, dim3(1), dim3(kLanes), 0, stream, meta,
+                       max_free_regions, batch, status_out, lock_spins());
     return static_cast<int32_t>(hipGetLastError());
 }
 

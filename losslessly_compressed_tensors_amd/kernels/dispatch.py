@@ -770,3 +770,19 @@ def buffer_free(storage, max_free_regions, descriptor, status, *, stream=None) -
     """``stream``: a raw stream handle; the current stream when None."""
     hip.call("lct_buffer_free", _ptr(storage), int(max_free_regions), _ptr(descriptor),
              _ptr(status), _stream(storage) if stream is None else stream)
+
+
+MAX_FREE_BATCH = hip.MAX_FREE_BATCH
+
+
+def buffer_free_batch(storage, max_free_regions, descriptors, status=None, *,
+                      stream=None) -> None:
+    """Free up to ``MAX_FREE_BATCH`` descriptors in order in one launch;
+    ``status``: int32[len(descriptors)] or None.  ``stream`` as for
+    ``buffer_free``."""
+    if not 1 <= len(descriptors) <= MAX_FREE_BATCH:
+        raise ValueError(f"1 to {MAX_FREE_BATCH} descriptors per batch, got {len(descriptors)}")
+    _require_device(storage, *descriptors)
+    array = (hip.ctypes.c_void_p * len(descriptors))(*(d.data_ptr() for d in descriptors))
+    hip.call("lct_buffer_free_batch", _ptr(storage), int(max_free_regions), array,
+             len(descriptors), _ptr(status), _stream(storage) if stream is None else stream)

@@ -51,6 +51,9 @@ class Overflow(ctypes.Structure):
 MAX_PENDING_FREES = 4   # LCT_MAX_PENDING_FREES
 
 
+MAX_FREE_BATCH = 32     # LCT_MAX_FREE_BATCH
+
+
 class PendingFrees(ctypes.Structure):
     """``lct_pending_frees``: descriptors whose frees ride on the next reservation."""
 
@@ -234,6 +237,7 @@ _SIGNATURES = {
     "lct_buffer_reset": [_ptr, _c_int32, _c_int32, _ptr],
     "lct_buffer_allocate": [_ptr, _c_int32, _ptr, _ptr, _c_int32, _ptr, _ptr],
     "lct_buffer_free": [_ptr, _c_int32, _ptr, _ptr, _ptr],
+    "lct_buffer_free_batch": [_ptr, _c_int32, ctypes.POINTER(_ptr), _c_int32, _ptr, _ptr],
     "lct_set_wait_limits": [_c_int32, _c_int32],
     "lct_set_decoder": [_c_int32],
     "lct_bandwidth_probe": [_c_int32, _ptr, _c_int64, _ptr, _c_int64, _c_int32, _ptr],

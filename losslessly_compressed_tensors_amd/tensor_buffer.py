@@ -104,6 +104,17 @@ def _free_now(storage: torch.Tensor, descriptor: torch.Tensor,
     return status
 
 
+def _free_many(storage: torch.Tensor, descriptors: list[torch.Tensor], max_free_regions: int,
+               stream: int | None = None) -> None:
+    """Free ``descriptors`` in order, ``dispatch.MAX_FREE_BATCH`` per launch
+    (``lct_buffer_free_batch``: one hold of the lock each); statuses are not
+    kept, as for the frees that ride on a reservation."""
+    step = dispatch.MAX_FREE_BATCH
+    for i in range(0, len(descriptors), step):
+        dispatch.buffer_free_batch(storage, max_free_regions, descriptors[i:i + step], None,
+                                   stream=stream)
+
+
 @torch.library.custom_op("lct::tensor_buffer_free", mutates_args=("storage", "descriptor"))
 def tensor_buffer_free(storage: torch.Tensor, descriptor: torch.Tensor,
                        max_free_regions: int) -> torch.Tensor:
@@ -167,10 +178,12 @@ class TensorBuffer:
         return torch._C._cuda_getCurrentRawStream(self._storage.get_device())
 
     def _defer_free(self, descriptor: torch.Tensor) -> None:
-        """Free ``descriptor`` at the next reservation on the current stream."""
+        """Free ``descriptor`` at the next reservation on the current stream
+        (up to ``dispatch.MAX_FREE_BATCH`` frees wait; a full list is launched
+        first, in one launch)."""
         stream = self._current_stream()
         if self._pending_frees and (stream != self._pending_stream
-                                    or len(self._pending_frees) == dispatch.MAX_PENDING_FREES):
+                                    or len(self._pending_frees) == dispatch.MAX_FREE_BATCH):
             self._flush_frees()
         self._pending_frees.append(descriptor)
         self._pending_stream = stream
@@ -180,13 +193,19 @@ class TensorBuffer:
         self._pending_frees = [*frees, *self._pending_frees]
 
     def _take_frees(self) -> list[torch.Tensor]:
-        """The deferred frees for a reservation on the current stream (those
-        deferred on another stream are launched there first instead)."""
+        """The deferred frees for a reservation on the current stream: the
+        last ``dispatch.MAX_PENDING_FREES`` (a reservation applies that many);
+        earlier ones are launched first, in one launch, and those deferred on
+        another stream are launched there instead."""
         if not self._pending_frees:
             return []
         if self._pending_stream != self._current_stream():
             self._flush_frees()
             return []
+        keep = dispatch.MAX_PENDING_FREES
+        if len(self._pending_frees) > keep:
+            early, self._pending_frees = self._pending_frees[:-keep], self._pending_frees[-keep:]
+            _free_many(self._storage, early, self.max_free_regions, stream=self._pending_stream)
         frees, self._pending_frees = self._pending_frees, []
         return frees
 
@@ -199,9 +218,7 @@ class TensorBuffer:
         if not self._pending_frees:
             return
         frees, self._pending_frees = self._pending_frees, []
-        for descriptor in frees:
-            _free_now(self._storage, descriptor, self.max_free_regions,
-                      stream=self._pending_stream)
+        _free_many(self._storage, frees, self.max_free_regions, stream=self._pending_stream)
         if self._pending_stream != self._current_stream():
             done = torch.cuda.Event()
             done.record(torch.cuda.ExternalStream(self._pending_stream, device=self.device))

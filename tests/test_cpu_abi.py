@@ -131,6 +131,21 @@ def test_allocate_compact_rejects_bad_frees_and_ready_before_launch(lib):
     assert bad_regions == -4
 
 
+def test_free_batch_rejects_bad_counts_and_null_descriptors_before_launch(lib):
+    fake = ctypes.c_void_p(1 << 20)   # never dereferenced: the checks fail first
+    array = (ctypes.c_void_p * hip.MAX_FREE_BATCH)(*([1 << 20] * hip.MAX_FREE_BATCH))
+
+    def call(count, regions=256, descriptors=array):
+        return lib.lct_buffer_free_batch(fake, regions, descriptors, count, None, None)
+
+    assert call(0) == LCT_E_ARG
+    assert call(-1) == LCT_E_ARG
+    assert call(hip.MAX_FREE_BATCH + 1) == LCT_E_ARG
+    assert call(1, regions=100) == LCT_E_ARG            # not a power of two
+    holes = (ctypes.c_void_p * 3)(1 << 20, None, 1 << 20)
+    assert call(3, descriptors=holes) == LCT_E_NULL
+
+
 def test_no_alloc_compress_rejects_tensors_beyond_its_array(lib):
     """More than 8192 codec blocks exceed the file-scope working array: rejected
     before anything is launched (the fake pointers are never dereferenced)."""

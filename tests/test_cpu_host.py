@@ -215,6 +215,9 @@ def deferral(monkeypatch):
     monkeypatch.setattr(tb.TensorBuffer, "_current_stream", lambda self: state.stream)
     monkeypatch.setattr(tb, "_free_now",
                         lambda storage, d, regions, stream=None: log.append(("free", d, stream)))
+    monkeypatch.setattr(tb, "_free_many",
+                        lambda storage, ds, regions, stream=None: log.append(("free", list(ds),
+                                                                              stream)))
     monkeypatch.setattr(tb.torch.cuda, "Event", lambda: _FakeEvent(log))
     monkeypatch.setattr(tb.torch.cuda, "ExternalStream", lambda handle, device=None: handle)
     monkeypatch.setattr(tb.torch.cuda, "current_stream", lambda device=None: _FakeStream(log))
@@ -232,16 +235,28 @@ def test_deferred_frees_ride_on_the_next_reservation_in_order(deferral):
     assert buf._take_frees() == [] and log == []
 
 
-def test_a_full_pending_list_is_launched_before_the_next_free(deferral):
+def test_a_full_pending_list_is_launched_in_one_batch_before_the_next_free(deferral):
     from losslessly_compressed_tensors_amd.kernels import dispatch
     buf, state, log = deferral
-    names = [f"d{i}" for i in range(dispatch.MAX_PENDING_FREES + 1)]
+    names = [f"d{i}" for i in range(dispatch.MAX_FREE_BATCH + 1)]
     for name in names:
         buf._defer_free(name)
-    launched = [entry[1] for entry in log if entry[0] == "free"]
-    assert launched == names[:dispatch.MAX_PENDING_FREES]   # launched on their own stream
-    assert all(entry[2] == 11 for entry in log if entry[0] == "free")
-    assert buf._take_frees() == names[dispatch.MAX_PENDING_FREES:]
+    # One launch, in order, on the stream the frees were made on.
+    assert log == [("free", names[:dispatch.MAX_FREE_BATCH], 11)]
+    assert buf._take_frees() == names[dispatch.MAX_FREE_BATCH:]
+
+
+def test_a_reservation_takes_the_last_frees_and_launches_the_earlier_ones_first(deferral):
+    from losslessly_compressed_tensors_amd.kernels import dispatch
+    buf, state, log = deferral
+    keep = dispatch.MAX_PENDING_FREES
+    names = [f"d{i}" for i in range(keep + 5)]
+    for name in names:
+        buf._defer_free(name)
+    assert log == []
+    assert buf._take_frees() == names[5:]             # what one reservation applies
+    assert log == [("free", names[:5], 11)]           # launched before it, in one batch
+    assert buf._take_frees() == []
 
 
 def test_a_change_of_stream_launches_pending_frees_and_orders_the_new_stream(deferral):
@@ -249,12 +264,12 @@ def test_a_change_of_stream_launches_pending_frees_and_orders_the_new_stream(def
     buf._defer_free("d1")
     state.stream = 22
     assert buf._take_frees() == []                    # not taken on another stream
-    assert log == [("free", "d1", 11), ("record", 11), ("wait",)]
+    assert log == [("free", ["d1"], 11), ("record", 11), ("wait",)]
     log.clear()
     buf._defer_free("d2")                             # now deferred on stream 22
     state.stream = 33
     buf._defer_free("d3")                             # a free on a third stream flushes d2 first
-    assert log == [("free", "d2", 22), ("record", 22), ("wait",)]
+    assert log == [("free", ["d2"], 22), ("record", 22), ("wait",)]
     assert buf._take_frees() == ["d3"]
 
 
@@ -262,12 +277,12 @@ def test_every_other_buffer_operation_launches_pending_frees_first(deferral):
     buf, state, log = deferral
     buf._defer_free("d1")
     buf.reset()
-    assert log == [("free", "d1", 11), ("reset",)]    # same stream: no wait needed
+    assert log == [("free", ["d1"], 11), ("reset",)]  # same stream: no wait needed
     log.clear()
     buf._defer_free("d2")
     buf._flush_frees()
     buf._flush_frees()                                # idempotent
-    assert log == [("free", "d2", 11)]
+    assert log == [("free", ["d2"], 11)]
 
 
 def test_frees_taken_by_a_reservation_that_fails_to_launch_stay_pending(deferral, monkeypatch):

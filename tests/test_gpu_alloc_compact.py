@@ -383,3 +383,52 @@ def test_freeing_one_tensor_twice_changes_nothing_the_second_time():
     assert torch.equal(cts[1][0].fallback_descriptor, cts[1][1].fallback_descriptor)
     assert _free_regions_snapshot(buf_a) == _free_regions_snapshot(buf_b)
     verify_buffer(buf_b)
+
+
+def test_free_batch_equals_single_frees():
+    """``lct_buffer_free_batch`` against ``lct_buffer_free`` one descriptor at a
+    time on twin buffers: the same statuses, descriptors and free list.  The
+    order lists one descriptor twice (freed once, status 4 the second time)
+    and overfills a four-region free list (status 3), then merges holes."""
+    require_gpu()
+    print("case lct_buffer_free_batch against single frees", flush=True)
+    bufs = [TensorBuffer(1 << 20, max_free_regions=4, device="cuda") for _ in range(2)]
+    request = torch.tensor([1000], dtype=torch.int32, device="cuda")
+    allocs = [[b.allocate(request) for _ in range(12)] for b in bufs]
+    order = [1, 3, 3, 5, 7, 9, 0, 11, 2, 10]
+    single = [int(bufs[0].free(allocs[0][i]).item()) for i in order]
+    status = torch.full((len(order),), -1, dtype=torch.int32, device="cuda")
+    dispatch.buffer_free_batch(bufs[1].storage, 4, [allocs[1][i].descriptor for i in order],
+                               status)
+    torch.cuda.synchronize()
+    assert status.tolist() == single
+    assert 3 in single and 4 in single and 0 in single   # full list, double free, ok
+    for a, b in zip(allocs[0], allocs[1]):
+        assert torch.equal(a.descriptor, b.descriptor)
+    assert _free_regions_snapshot(bufs[0]) == _free_regions_snapshot(bufs[1])
+
+
+def test_many_deferred_frees_equal_immediate_frees():
+    """40 CompressedTensor.free() calls before the next reservation (a full
+    batch launched at the 33rd, the rest before and inside the reservation)
+    against 40 immediate frees."""
+    require_gpu()
+    print("case 40 deferred frees", flush=True)
+    x, dist = _patterns(71, 65536), SPARSE
+    x = x.cuda()
+    buf_a = TensorBuffer(8 << 20, max_free_regions=64, device="cuda")
+    buf_b = TensorBuffer(8 << 20, max_free_regions=64, device="cuda")
+    cts = [(compress(x, dist, buffer=buf_a), compress(x, dist, buffer=buf_b)) for _ in range(48)]
+    for ct_a, ct_b in cts[:40]:
+        buf_a.free(Allocation(ct_a.fallback_descriptor, buf_a))
+        ct_b.free()
+    assert len(buf_b._pending_frees) == 40 - dispatch.MAX_FREE_BATCH
+    ct_a, ct_b = compress(x, dist, buffer=buf_a), compress(x, dist, buffer=buf_b)
+    assert not buf_b._pending_frees
+    torch.cuda.synchronize()
+    _assert_same_allocation(ct_a, ct_b)
+    for a, b in cts[:40]:
+        assert torch.equal(a.fallback_descriptor, b.fallback_descriptor)
+    assert _free_regions_snapshot(buf_a) == _free_regions_snapshot(buf_b)
+    verify_buffer(buf_b)
+    assert torch.equal(decompress(ct_b).view(torch.int16), x.view(torch.int16))
