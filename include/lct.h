@@ -77,7 +77,16 @@ typedef struct {
  * this control array used; counts: int32[4]; blocks: int32[3 * nb];
  * buffer_meta: the TensorBuffer's metadata, or NULL for private storage;
  * descriptor: int32[4] (buffered); max_free_regions: the buffer's R; frees:
- * deferred frees applied first, as lct_allocate_compact applies them. */
+ * deferred frees applied first, as lct_allocate_compact applies them.
+ * a_samples, b_samples (lct_dual_encode_fused; lct_pointwise_encode_fused
+ * does not read them): both operands' values at the center's sample
+ * positions, as lct_dual_sample takes them, or NULL.  When both are given the
+ * launch takes the result's center itself, as lct_encode_fused does: its
+ * first ceil(sample_size / 64) workgroups compute the result at the sample
+ * positions, publish their partial sums in control[0, 64) and write the
+ * result's values to result_samples (NULL: not recorded); `partials` is then
+ * not read and may be NULL.  The outputs equal those of lct_dual_sample
+ * followed by this launch with `partials`. */
 typedef struct {
     uint64_t *control;
     int64_t control_words;
@@ -88,6 +97,9 @@ typedef struct {
     int32_t *buffer_meta;
     int32_t max_free_regions;
     lct_pending_frees frees;
+    const uint16_t *a_samples;
+    const uint16_t *b_samples;
+    uint16_t *result_samples;
 } lct_bookkeeping;
 
 /* Pointwise operation selectors: LCT/codec/pointwise.py:289-304. */

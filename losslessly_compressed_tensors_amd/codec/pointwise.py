@@ -90,18 +90,28 @@ def _launch_pointwise_compressed_dense(data: CompressedTensor, other: torch.Tens
     return output, auxiliary
 
 
+def _bookkept(blocks: int) -> bool:
+    """Whether a fused update's encoder launch does its own overflow
+    bookkeeping (``_encode_with_bookkeeping``)."""
+    return 0 < blocks <= dispatch.MAX_CODEC_BLOCKS
+
+
 def _encode_with_bookkeeping(launch_encoder, exponents, side, encoded, extra_starts, summaries,
                              size, distribution, buffer, shape, *, center, shifted_decode,
-                             logical_numel, sample_values) -> CompressedTensor:
+                             logical_numel, sample_values, samples=None) -> CompressedTensor:
     """Run a fused update's encoder launch, ``launch_encoder(record)``, with
     the overflow bookkeeping in the same launch when the block count allows
     (a ``dispatch.bookkeeping`` record: prefix scan and, for a shared buffer,
     the deferred frees and the reservation), then the compaction; otherwise
     the encoder alone followed by ``finish_encode``'s bookkeeping launches.
-    Either way the stored tensor is the same (``LCT/codec/encode.py:77-186``)."""
+    Either way the stored tensor is the same (``LCT/codec/encode.py:77-186``).
+    ``samples``: the record's in-launch sampling operands (only with the
+    bookkeeping in the launch)."""
     device = encoded.device
     blocks = size // geometry(distribution)[0]
-    if not 0 < blocks <= dispatch.MAX_CODEC_BLOCKS:
+    if not _bookkept(blocks):
+        if samples is not None:
+            raise ValueError("in-launch center sampling needs the in-launch bookkeeping")
         launch_encoder(None)
         return finish_encode(exponents, side, encoded, extra_starts, summaries, size,
                              distribution, buffer, shape, precomputed=True, center=center,
@@ -116,7 +126,7 @@ def _encode_with_bookkeeping(launch_encoder, exponents, side, encoded, extra_sta
         frees = buffer._take_frees()
     try:
         launch_encoder(dispatch.bookkeeping(device, blocks, counts, blocks_out, buffer,
-                                            descriptor, frees))
+                                            descriptor, frees, samples=samples))
     except BaseException:
         # Nothing was launched: the deferred frees wait for the next call.
         if buffer is not None:
@@ -165,7 +175,9 @@ def _fused_compressed_output(data: CompressedTensor, other: torch.Tensor,
     decode_table = shifted_decode_table(data)
     partials = torch.empty(2 * -(-sample_size // 64), dtype=torch.int32, device=device)
     # A's recorded values at the sample positions spare the sampler a walk
-    # through A's streams; the result's are recorded for the next update.
+    # through A's streams; the result's are recorded for the next update.  (The
+    # sampler stays a launch of its own: inside the encoder launch, B's 4096
+    # scattered reads delayed every block's center by more than it costs.)
     a_samples = data.sample_values
     if a_samples is not None and a_samples.numel() != sample_size:
         a_samples = None
@@ -209,8 +221,9 @@ def _fused_dual_compressed_output(data: CompressedTensor, other: CompressedTenso
     result at the center's sample positions (from an operand's recorded
     sample values when it has them, else by decoding the sampled streams'
     prefixes) and ``lct_dual_encode`` decodes both operands, applies
-    ``fma(a, alpha, b)`` and encodes the result as it is computed.  The stored
-    tensor is identical.
+    ``fma(a, alpha, b)`` and encodes the result as it is computed; with both
+    operands' recorded values and the bookkeeping in the encoder launch, that
+    launch also samples.  The stored tensor is identical.
     """
     device = data.data.device
     _, _, rare_a = get_distribution_tables(data.distribution, device)
@@ -232,12 +245,18 @@ def _fused_dual_compressed_output(data: CompressedTensor, other: CompressedTenso
         values = tensor.sample_values
         return values if values is not None and values.numel() == sample_size else None
 
-    partials = torch.empty(2 * -(-sample_size // 64), dtype=torch.int32, device=device)
     result_samples = torch.empty(sample_size, dtype=torch.int16, device=device)
-    dispatch.dual_sample(data.data, data.sign_mantissa, a_table, data.center, a_storage,
-                         other.data, other.sign_mantissa, b_table, other.center, b_storage,
-                         alpha, partials, data.size, a_samples=recorded(data),
-                         b_samples=recorded(other), result_samples=result_samples, **launch)
+    a_samples, b_samples = recorded(data), recorded(other)
+    # With both operands' recorded values and the bookkeeping in the encoder
+    # launch, that launch samples the center itself.
+    in_launch = a_samples is not None and b_samples is not None and _bookkept(blocks)
+    partials = None
+    if not in_launch:
+        partials = torch.empty(2 * -(-sample_size // 64), dtype=torch.int32, device=device)
+        dispatch.dual_sample(data.data, data.sign_mantissa, a_table, data.center, a_storage,
+                             other.data, other.sign_mantissa, b_table, other.center, b_storage,
+                             alpha, partials, data.size, a_samples=a_samples,
+                             b_samples=b_samples, result_samples=result_samples, **launch)
     center = torch.empty(1, dtype=torch.int32, device=device)
     shifted_decode = torch.empty(1024, dtype=torch.int32, device=device)
     side = torch.empty(data.size, dtype=torch.uint8, device=device)
@@ -259,7 +278,9 @@ def _fused_dual_compressed_output(data: CompressedTensor, other: CompressedTenso
     return _encode_with_bookkeeping(launch_encoder, exponents, side, encoded, extra_starts,
                                     summaries, data.size, result_distribution, buffer,
                                     data.shape, center=center, shifted_decode=shifted_decode,
-                                    logical_numel=n, sample_values=result_samples)
+                                    logical_numel=n, sample_values=result_samples,
+                                    samples=(a_samples, b_samples, result_samples) if in_launch
+                                    else None)
 
 
 def _launch_scalar_mul_add_compressed_compressed(data: CompressedTensor,

@@ -75,7 +75,27 @@ struct KernelBookkeeping {
     int32_t polls;
     uint64_t *gate;      // batched launches: GatedReserve's word (nullptr: none)
     int32_t post_gate;   // this job applies the frees and posts the gate
+    // In-launch center sampling of the two-operand launch (sample_groups > 0):
+    // workgroups g < sample_groups publish sample group g's partial sums in
+    // control[g] (tagged), and every block reads the center from there
+    // instead of from `partials`.
+    const uint16_t *a_samples;
+    const uint16_t *b_samples;
+    uint16_t *result_samples;
+    int64_t sample_size;
+    int32_t sample_groups;
 };
+
+// Publish sample group `group`'s kept-exponent sum and count (one wave,
+// compress.hip's layout: sum as int16 in bits 16..31, count in bits 0..15).
+__device__ __forceinline__ void publish_sample_group(const KernelBookkeeping &bk, int64_t group,
+                                                     int32_t sum, int32_t kept) {
+    if (threadIdx.x == 0) {
+        const uint32_t value = (static_cast<uint32_t>(static_cast<uint16_t>(sum)) << 16)
+                               | static_cast<uint32_t>(kept);
+        control_store(bk.control + group, tagged_word(bk.epoch, value));
+    }
+}
 
 // After a block (every thread, past the summary's barriers): its overflow
 // count and tail bytes go to `summaries`, or -- in a fused launch (kBooked:
@@ -90,7 +110,7 @@ template <bool kBooked>
 __device__ __forceinline__ void publish_block(const KernelBookkeeping &bk,
                                               int32_t *__restrict__ summaries, int64_t block,
                                               int64_t n_blocks, int32_t count, int32_t bytes,
-                                              int32_t *lds_free_list) {
+                                              int32_t *lds_free_list, bool failed = false) {
     if (!kBooked) {
         if (threadIdx.x == 0) {
             summaries[block] = count;
@@ -99,8 +119,11 @@ __device__ __forceinline__ void publish_block(const KernelBookkeeping &bk,
         return;
     }
     if (threadIdx.x == 0) {
-        // count <= 256 and bytes <= 256 * 256 fit 9 and 17 bits.
-        const uint32_t value = (static_cast<uint32_t>(count) << 17) | static_cast<uint32_t>(bytes);
+        // count <= 256 and bytes <= 256 * 256 fit 9 and 17 bits; a block
+        // whose center did not arrive is marked failed.
+        const uint32_t value = failed ? (kFailedBlock << 17)
+                                      : (static_cast<uint32_t>(count) << 17)
+                                            | static_cast<uint32_t>(bytes);
         control_store(bk.control + kControlPartials + block, tagged_word(bk.epoch, value));
     }
     if (block != 0) return;
@@ -1471,7 +1494,7 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     __shared__ FloatDecodeTables tba, tbb;
     __shared__ uint2 enc[256];
     __shared__ int32_t scratch[kWavesPerBlock];
-    __shared__ int32_t shared_center;
+    __shared__ int32_t shared_center[2];   // center, and whether its samples failed to arrive
     // The overflow maps (2 KiB) and the raw encode table (1 KiB) are only used
     // before the first side halves are stored, so they share the slices.
     __shared__ __attribute__((aligned(16))) uint8_t slices[kWavesPerBlock][2 * kHalfSlice];
@@ -1482,6 +1505,26 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     uint32_t *stage_b = stages + register_stage_bytes(W) / 4;
     const int t = threadIdx.x;
     const int64_t block = blockIdx.x;
+    const bool sampled_here = kBooked && bk.sample_groups > 0;
+    if (sampled_here && block < bk.sample_groups && t < kWave) {
+        // fma(a, alpha, b) (pointwise_scalar_dual.py:226) at sample group
+        // `block`'s positions from both operands' recorded values.
+        const int64_t i = block * kSampleGroup + t;
+        const bool active = i < bk.sample_size;
+        uint32_t result = 0;
+        if (active) {
+            result = float_to_bf16(__builtin_fmaf(bf16_to_float(bk.a_samples[i]), alpha[0],
+                                                  bf16_to_float(bk.b_samples[i])));
+            if (bk.result_samples != nullptr)
+                bk.result_samples[i] = static_cast<uint16_t>(result);
+        }
+        const int32_t exp = static_cast<int32_t>((result >> 7) & 255u) - 127;
+        const bool keep = active && exp >= -120;
+        const int32_t sum = wave_sum(keep ? exp : 0);
+        const int32_t kept = wave_sum(keep ? 1 : 0);
+        publish_sample_group(bk, block, sum, kept);
+    }
+    if (block >= n_blocks) return;   // a sample group past the last block
     const int64_t n_streams = n_blocks * kLanes;
     const int64_t row_base = block * S;
     const int64_t logical_base = row_base * kLanes;
@@ -1502,14 +1545,20 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     load_register_rows(b.encoded, n_streams, block, wb);
 
     raw_encode[t] = base_encode[t];
-    center_from_partials(partials, n_groups, &shared_center);
+    if (sampled_here) {
+        center_from_control(bk.control, bk.sample_groups, bk.epoch, bk.polls, shared_center);
+    } else {
+        center_from_partials(partials, n_groups, shared_center);
+        if (t == 0) shared_center[1] = 0;
+    }
     build_float_decode_tables(tba, a.shifted_decode);
     build_float_decode_tables(tbb, b.shifted_decode);
     const int32_t a_center = a.center[0], b_center = b.center[0];
     stage_payload_rows(stage_a, a.encoded, n_streams, block, kRegisterRows, W);
     stage_payload_rows(stage_b, b.encoded, n_streams, block, kRegisterRows, W);
     __syncthreads();   // center and raw encode table
-    const int32_t center = shared_center;
+    const int32_t center = shared_center[0];
+    const bool center_failed = shared_center[1] != 0;
     enc[t] = repack_encode_entry(static_cast<uint32_t>(raw_encode[byte_to_index(t, center)]));
     if (block == 0) {
         if (t == 0) center_out[0] = center;
@@ -1559,7 +1608,7 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     // 256 x 256): one block scan.
     const int32_t both = block_sum(overflow ? (S - extra) | (1 << 20) : 0, scratch);
     publish_block<kBooked>(bk, summaries, block, n_blocks, both >> 20, both & 0xFFFFF,
-                           reinterpret_cast<int32_t *>(stages));
+                           reinterpret_cast<int32_t *>(stages), center_failed);
 }
 
 int32_t check_operand(const int32_t *encoded, const uint8_t *side, const int32_t *shifted_decode,
@@ -1797,7 +1846,10 @@ int32_t launch_dual_encode(
         return e;
     if (int32_t e = check_operand(b_encoded, b_side, b_shifted_decode, b_center, b_overflow))
         return e;
-    if (!alpha || !partials || !base_encode || !base_decode || !center_out
+    // With both operands' recorded sample values the launch samples the center.
+    const bool sample_here = bookkeeping != nullptr && bookkeeping->a_samples != nullptr
+        && bookkeeping->b_samples != nullptr;
+    if (!alpha || (!partials && !sample_here) || !base_encode || !base_decode || !center_out
         || !shifted_decode_out || !side_out || !encoded_out || !extra_starts || !summaries
         || !exponents)
         return LCT_E_NULL;
@@ -1822,11 +1874,20 @@ int32_t launch_dual_encode(
     size_t lds = 2 * static_cast<size_t>(register_stage_bytes(g.fixed_words));
     KernelBookkeeping bk;
     if (int32_t e = prepare_bookkeeping(bookkeeping, n_blocks, bk, lds)) return e;
+    int64_t grid = n_blocks;
+    if (sample_here) {
+        bk.a_samples = bookkeeping->a_samples;
+        bk.b_samples = bookkeeping->b_samples;
+        bk.result_samples = bookkeeping->result_samples;
+        bk.sample_size = sample_size;
+        bk.sample_groups = sample_groups(sample_size);
+        grid = std::max<int64_t>(n_blocks, bk.sample_groups);
+    }
     const auto kernel = bk.control != nullptr ? dual_encode_kernel<true>
                                               : dual_encode_kernel<false>;
     if (hipError_t e = reserve_dynamic_lds(reinterpret_cast<const void *>(kernel), lds))
         return static_cast<int32_t>(e);
-    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(n_blocks)), dim3(kLanes),
+    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(grid)), dim3(kLanes),
                        lds, stream, a, b, alpha, partials, sample_groups(sample_size),
                        base_encode, base_decode, center_out, shifted_decode_out, side_out,
                        encoded_out, extra_starts, summaries, exponents, n_blocks, logical_numel,

@@ -250,11 +250,14 @@ def control_array(device: torch.device, n_blocks: int) -> torch.Tensor:
         return array
 
 
-def bookkeeping(device, n_blocks, counts, blocks_out, buffer=None, descriptor=None, frees=()):
+def bookkeeping(device, n_blocks, counts, blocks_out, buffer=None, descriptor=None, frees=(),
+                samples=None):
     """The ``lct_bookkeeping`` record of a fused update encoder launch on the
     current stream of ``device``: its control array and a fresh epoch, the
     totals and block metadata outputs and, for a shared ``buffer``, the
-    reservation's descriptor and the deferred ``frees``."""
+    reservation's descriptor and the deferred ``frees``.  ``samples``:
+    ``(a_samples, b_samples, result_samples)`` for a launch that samples the
+    result's center itself (no sampler launch before it), or None."""
     control = control_array(device, n_blocks)
     record = hip.Bookkeeping()
     record.control = _ptr(control)
@@ -269,6 +272,8 @@ def bookkeeping(device, n_blocks, counts, blocks_out, buffer=None, descriptor=No
         record.frees.count = len(frees)
         for i, freed in enumerate(frees):
             record.frees.descriptor[i] = freed.data_ptr()
+    if samples is not None:
+        record.a_samples, record.b_samples, record.result_samples = (_ptr(t) for t in samples)
     return record
 
 

@@ -77,6 +77,9 @@ class Bookkeeping(ctypes.Structure):
         ("buffer_meta", _ptr),
         ("max_free_regions", _c_int32),
         ("frees", PendingFrees),
+        ("a_samples", _ptr),
+        ("b_samples", _ptr),
+        ("result_samples", _ptr),
     ]
 
 

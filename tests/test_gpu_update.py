@@ -13,6 +13,8 @@ pointwise COMPRESSED_OUTPUT launch followed by the re-encode of its components
 * the two-pass kernel (``lct_pointwise_dense`` with COMPRESSED_OUTPUT), still
   used by the two-compressed path, writes the oracle's components.
 """
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -651,3 +653,39 @@ def test_update_bookkeeping_that_stops_waiting_marks_the_result_incomplete(kind)
     assert torch.equal(decompress(ok).view(torch.int16), expected)
     ok.free()
     verify_buffer(buffer)
+
+
+def _same_record(x, y):
+    """Two compressed tensors store the same fields (private storage; the
+    payload's 4 words of padding are never written)."""
+    B, L, S, W = x.codec_geometry
+    words = x.size // B * L * W
+    assert torch.equal(x.data[:words], y.data[:words])
+    for field in ("sign_mantissa", "center", "decode_table", "fallback_count",
+                  "fallback_used", "fallback_blocks", "fallback_lanes", "fallback_starts",
+                  "fallback_buffer"):
+        u, v = getattr(x, field), getattr(y, field)
+        assert (u is None) == (v is None), field
+        if u is not None:
+            assert torch.equal(u.cpu(), v.cpu()), field
+
+
+@pytest.mark.parametrize("case", DUAL_CASES[:3], ids=[c[0] for c in DUAL_CASES[:3]])
+def test_dual_in_launch_sampling_equals_the_sampler_launch(case):
+    """The weight update with both operands' recorded sample values samples
+    the result's center in its encoder launch (its first 64 workgroups; the
+    gaussian case has 16 codec blocks, so 48 workgroups only sample): against
+    the sampler launch (B's recorded values dropped, so that launch walks B's
+    streams) the stored result and its recorded values are the same, and the
+    result is the oracle's."""
+    require_gpu()
+    print(f"case dual in-launch sampling {case[0]}", flush=True)
+    ca, cb, oa, ob = _dual_operands(case, None, None)
+    assert ca.sample_values is not None and cb.sample_values is not None
+    cb_without = dataclasses.replace(cb, sample_values=None)
+    first = a_compA_add_compB(ca, _scalar(ALPHA), cb, dense_output=False)
+    second = a_compA_add_compB(ca, _scalar(ALPHA), cb_without, dense_output=False)
+    _same_record(first, second)
+    assert torch.equal(first.sample_values, second.sample_values)
+    side, exponents = oracle.dual(oa, ob, ALPHA, policy=1)
+    assert_matches_oracle(first, oracle_from_components(side, exponents, ca.distribution))
