@@ -37,7 +37,7 @@ from losslessly_compressed_tensors_amd.LCTensor import LCTTensor
 from losslessly_compressed_tensors_amd.components.layers import (
     Embedding, FlashAttention, Linear, RMSLinear, RMSNormFunction, Relu2Linear,
     compress_weight, dense_weight, flush_saved, named_trainable_tensors, prefetch_saved,
-    prefetch_weights, rms_norm_qkv,
+    prefetch_weights, queued_saved, rms_norm_qkv,
 )
 from losslessly_compressed_tensors_amd.components.sparse_utils import SparseAdamW, SparseMuon
 from losslessly_compressed_tensors_amd.tensor_buffer import TensorBuffer, _free_regions_snapshot
@@ -227,15 +227,17 @@ class Block(nn.Module):
         # forward and once when its backward starts (the hook on its output),
         # instead of one decode launch per use.
         # Likewise the activations the attention and the MLP save: compressed
-        # together when each part's forward ends (flush_saved), decoded
-        # together when its backward starts (the hooks on the parts' outputs).
+        # together when the block's forward ends (flush_saved), decoded part by
+        # part when that part's backward starts (the hooks on the parts'
+        # outputs).
         weights = self.weights()
         prefetch_weights(weights)
         a = self.attn(x, self.norm1.gains)
-        saved_attn = flush_saved()
+        saved_attn = queued_saved()
         x = x + a
         m = self.mlp(x, self.norm2.gains)
-        saved_mlp = flush_saved()
+        attn_ids = {id(s) for s in saved_attn}
+        saved_mlp = [s for s in flush_saved() if id(s) not in attn_ids]
         out = x + m
         if out.requires_grad:
             if any(isinstance(w, LCTTensor) for w in weights):

@@ -29,7 +29,8 @@ from .ops import rms_norm, rms_norm_backward
 __all__ = [
     "dense_weight", "prefetch_weights", "RMSLinear", "rms_norm_qkv", "RMSNormFunction",
     "Relu2Linear", "FlashAttention", "compress_weight", "Linear", "Embedding",
-    "named_trainable_tensors", "flush_saved", "prefetch_saved", "batch_saved_compression",
+    "named_trainable_tensors", "flush_saved", "queued_saved", "prefetch_saved",
+    "batch_saved_compression",
 ]
 
 # Causal attention scale of the trainer (LCT/components/layers.py:232-236).
@@ -104,6 +105,13 @@ def flush_saved() -> list:
         for saved, value in zip(members, values):
             saved.value, saved.queued, saved.distribution, saved.buffer = value, False, None, None
     return queued
+
+
+def queued_saved() -> list:
+    """The saved activations waiting for the next ``flush_saved`` (a copy of
+    the queue): a caller that compresses two groups in one launch keeps the
+    first group's members apart with it."""
+    return list(_queue)
 
 
 def prefetch_saved(saved) -> None:
