@@ -173,6 +173,36 @@ struct LaneOverlay {
     int32_t lds;           // block-uniform: the block's tails were staged in LDS
 };
 
+// The block's overflow-list header: its entry count (0 also when a buffered
+// tensor's reservation failed), first entry and tail byte base, and where the
+// entries, starts and tails begin.  All independent loads: a prologue that
+// issues them first shares their round trip with its other loads.
+struct OverlayHead {
+    int32_t count;
+    int32_t status;      // the buffered tensor's descriptor status (0: ok)
+    int32_t first;
+    int32_t byte_base;
+    int64_t lane_off, start_off, tail_base;
+};
+
+__device__ __forceinline__ OverlayHead load_overlay_head(const lct_overflow &ov, bool present,
+                                                         int64_t block, int64_t n_blocks) {
+    OverlayHead h{0, 0, 0, 0, 0, 0, ov.base};
+    if (!present) return h;
+    h.count = ov.blocks[block];
+    h.first = ov.blocks[n_blocks + block];
+    h.byte_base = ov.blocks[2 * n_blocks + block];
+    if (ov.descriptor != nullptr) {
+        h.status = ov.descriptor[2];
+        const int64_t arena = ov.descriptor[0];
+        const int64_t total = ov.count[0];
+        h.lane_off = arena;
+        h.start_off = arena + total;
+        h.tail_base = arena + 2 * total;
+    }
+    return h;
+}
+
 // Expand the block's compact overflow list into per-lane (start, offset), as
 // decode.py:195-240 does.  When `tail_lds` is given and the block's tail bytes
 // fit in `tail_cap`, they are copied into tail_lds so the step loop reads its
@@ -180,29 +210,17 @@ struct LaneOverlay {
 // thread of the block must call it, and the caller synchronises once more
 // before reading tail_lds.  A buffered tensor whose allocation failed
 // (descriptor status != 0) has no tails and is decoded without overlay.
-__device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, bool present,
-                                                     int64_t block, int64_t n_blocks, int S,
-                                                     int32_t *map_start, int32_t *map_offset,
-                                                     int32_t *scratch, uint8_t *tail_lds,
-                                                     int32_t tail_cap) {
+__device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, const OverlayHead &h,
+                                                     int S, int32_t *map_start,
+                                                     int32_t *map_offset, int32_t *scratch,
+                                                     uint8_t *tail_lds, int32_t tail_cap) {
     const int t = threadIdx.x;
     LaneOverlay lane{nullptr, S, 0, S, 0};
-    int32_t count = 0;
-    if (present) {
-        count = ov.blocks[block];
-        if (ov.descriptor != nullptr && ov.descriptor[2] != 0) count = 0;
-    }
+    const int32_t count = h.status != 0 ? 0 : h.count;
     if (count <= 0) return lane;   // uniform across the block
-    int64_t lane_off = 0, start_off = 0, tail_base = ov.base;
-    if (ov.descriptor != nullptr) {
-        const int64_t arena = ov.descriptor[0];
-        const int64_t total = ov.count[0];
-        lane_off = arena;
-        start_off = arena + total;
-        tail_base = arena + 2 * total;
-    }
-    const int32_t first = ov.blocks[n_blocks + block];
-    const int32_t byte_base = ov.blocks[2 * n_blocks + block];
+    const int64_t lane_off = h.lane_off, start_off = h.start_off, tail_base = h.tail_base;
+    const int32_t first = h.first;
+    const int32_t byte_base = h.byte_base;
     map_start[t] = S;
     map_offset[t] = 0;
     const bool valid = t < count;
@@ -230,6 +248,15 @@ __device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, boo
     lane.wave_start = __builtin_amdgcn_readfirstlane(wave_min(lane.start));
     lane.lds = staged ? 1 : 0;
     return lane;
+}
+
+__device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, bool present,
+                                                     int64_t block, int64_t n_blocks, int S,
+                                                     int32_t *map_start, int32_t *map_offset,
+                                                     int32_t *scratch, uint8_t *tail_lds,
+                                                     int32_t tail_cap) {
+    return build_overlay(ov, load_overlay_head(ov, present, block, n_blocks), S, map_start,
+                         map_offset, scratch, tail_lds, tail_cap);
 }
 
 // One lane's stream cursor over payload rows kStride words apart in LDS.

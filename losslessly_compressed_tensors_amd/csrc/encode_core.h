@@ -281,6 +281,13 @@ __device__ __forceinline__ bool setup_table(const TableSource &tables, uint2 *ta
         return false;
     }
     raw[t] = tables.base_encode[t];
+    // Workgroup 0 also writes the shifted decode table: its base entries are
+    // loaded with the rest, before the center is known.
+    int32_t base[1024 / kLanes] = {};
+    if (block == 0) {
+#pragma unroll
+        for (int k = 0; k < 1024 / kLanes; ++k) base[k] = tables.base_decode[t + k * kLanes];
+    }
     if (tables.control != nullptr) {
         center_from_control(tables.control, tables.n_groups, tables.epoch, tables.polls, shared);
     } else {
@@ -293,8 +300,9 @@ __device__ __forceinline__ bool setup_table(const TableSource &tables, uint2 *ta
     table[t] = repack_encode_entry(static_cast<uint32_t>(raw[byte_to_index(t, center)]));
     if (block == 0) {
         if (t == 0) tables.center_out[0] = center;
-        for (int i = t; i < 1024; i += kLanes)
-            tables.shifted_decode_out[i] = shifted_decode_entry(tables.base_decode[i], center);
+#pragma unroll
+        for (int k = 0; k < 1024 / kLanes; ++k)
+            tables.shifted_decode_out[t + k * kLanes] = shifted_decode_entry(base[k], center);
     }
     return failed;
 }

@@ -97,6 +97,31 @@ __device__ __forceinline__ void publish_sample_group(const KernelBookkeeping &bk
     }
 }
 
+// Workgroup 0's share of the result's shifted decode table: the base
+// table's 1024 entries, 4 per thread, loaded at the start of its prologue
+// (with the other loads) and shifted once the center is known, so that the
+// workgroup that also writes the table has no extra memory round trip.
+struct BaseDecodeShare {
+    int32_t v[1024 / kLanes];
+};
+
+__device__ __forceinline__ BaseDecodeShare load_base_decode(const int32_t *__restrict__ base_decode,
+                                                            bool needed) {
+    BaseDecodeShare b{};
+    if (needed) {
+#pragma unroll
+        for (int k = 0; k < 1024 / kLanes; ++k) b.v[k] = base_decode[threadIdx.x + k * kLanes];
+    }
+    return b;
+}
+
+__device__ __forceinline__ void store_shifted_decode(int32_t *__restrict__ out,
+                                                     const BaseDecodeShare &b, int32_t center) {
+#pragma unroll
+    for (int k = 0; k < 1024 / kLanes; ++k)
+        out[threadIdx.x + k * kLanes] = shifted_decode_entry(b.v[k], center);
+}
+
 // After a block (every thread, past the summary's barriers): its overflow
 // count and tail bytes go to `summaries`, or -- in a fused launch (kBooked:
 // its own kernel instantiation, so the separate launch's kernel holds none of
@@ -880,6 +905,8 @@ __device__ __forceinline__ void pointwise_encode_block(
     __syncthreads();   // raw_encode is no longer read (it shares the maps' LDS)
     const LaneOverlay lane = build_overlay(a.ov, a.has_overlay != 0, block, n_blocks, S, map_start,
                                            map_offset, scratch, tail_lds, kTailLds);
+    // (Issued here rather than with the prologue's first loads: hoisted, the
+    // measured kernel was 0.8 us slower.)
     const OpParams p = load_op_params(args.op, args.alpha_is_one, args.beta_is_one, args.alpha,
                                       args.beta);
     wait_memory();
@@ -1539,6 +1566,12 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     const __amdgpu_buffer_rsrc_t b_side = make_rsrc(b.side + logical_base, block_elems);
     const u32x2 first_a = fetch_half_side(io.side, half_side_offset(), 0);
     const u32x2 first_b = fetch_half_side(b_side, half_side_offset(), 0);
+    // Loads the prologue needs later, issued now so that they share one round
+    // trip with the tables' loads instead of following its barriers.
+    const OverlayHead head_a = load_overlay_head(a.ov, a.has_overlay != 0, block, n_blocks);
+    const OverlayHead head_b = load_overlay_head(b.ov, b.has_overlay != 0, block, n_blocks);
+    const BaseDecodeShare base0 = load_base_decode(base_decode, block == 0);
+    const float alpha_value = alpha[0];
     // Each stream's first three words: the cursors' initial windows.
     uint32_t wa[kRegisterRows], wb[kRegisterRows];
     load_register_rows(a.encoded, n_streams, block, wa);
@@ -1562,16 +1595,14 @@ __global__ __launch_bounds__(kLanes) void dual_encode_kernel(
     enc[t] = repack_encode_entry(static_cast<uint32_t>(raw_encode[byte_to_index(t, center)]));
     if (block == 0) {
         if (t == 0) center_out[0] = center;
-        for (int i = t; i < 1024; i += kLanes)
-            shifted_decode_out[i] = shifted_decode_entry(base_decode[i], center);
+        store_shifted_decode(shifted_decode_out, base0, center);
     }
     __syncthreads();   // raw_encode is no longer read (it shares the maps' LDS)
-    const LaneOverlay lane_a = build_overlay(a.ov, a.has_overlay != 0, block, n_blocks, S,
-                                             map_start, map_offset, scratch, nullptr, 0);
+    const LaneOverlay lane_a = build_overlay(a.ov, head_a, S, map_start, map_offset, scratch,
+                                             nullptr, 0);
     __syncthreads();   // B's overlay reuses the maps
-    const LaneOverlay lane_b = build_overlay(b.ov, b.has_overlay != 0, block, n_blocks, S,
-                                             map_start, map_offset, scratch, nullptr, 0);
-    const float alpha_value = alpha[0];
+    const LaneOverlay lane_b = build_overlay(b.ov, head_b, S, map_start, map_offset, scratch,
+                                             nullptr, 0);
     wait_memory();
     __syncthreads();   // payloads and encode table visible; maps no longer read
 
