@@ -210,17 +210,17 @@ __device__ __forceinline__ OverlayHead load_overlay_head(const lct_overflow &ov,
 // thread of the block must call it, and the caller synchronises once more
 // before reading tail_lds.  A buffered tensor whose allocation failed
 // (descriptor status != 0) has no tails and is decoded without overlay.
-__device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, const OverlayHead &h,
-                                                     int S, int32_t *map_start,
-                                                     int32_t *map_offset, int32_t *scratch,
-                                                     uint8_t *tail_lds, int32_t tail_cap) {
+// expand_overlay is the part after the block's header: count > 0 entries
+// from `first`, tails from byte_base.
+__device__ __forceinline__ LaneOverlay expand_overlay(const lct_overflow &ov, int32_t count,
+                                                      int32_t first, int32_t byte_base,
+                                                      int64_t lane_off, int64_t start_off,
+                                                      int64_t tail_base, int S,
+                                                      int32_t *map_start, int32_t *map_offset,
+                                                      int32_t *scratch, uint8_t *tail_lds,
+                                                      int32_t tail_cap) {
     const int t = threadIdx.x;
     LaneOverlay lane{nullptr, S, 0, S, 0};
-    const int32_t count = h.status != 0 ? 0 : h.count;
-    if (count <= 0) return lane;   // uniform across the block
-    const int64_t lane_off = h.lane_off, start_off = h.start_off, tail_base = h.tail_base;
-    const int32_t first = h.first;
-    const int32_t byte_base = h.byte_base;
     map_start[t] = S;
     map_offset[t] = 0;
     const bool valid = t < count;
@@ -250,13 +250,41 @@ __device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, con
     return lane;
 }
 
+// With the header loaded up front (load_overlay_head).
+__device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, const OverlayHead &h,
+                                                     int S, int32_t *map_start,
+                                                     int32_t *map_offset, int32_t *scratch,
+                                                     uint8_t *tail_lds, int32_t tail_cap) {
+    const int32_t count = h.status != 0 ? 0 : h.count;
+    if (count <= 0) return LaneOverlay{nullptr, S, 0, S, 0};   // uniform across the block
+    return expand_overlay(ov, count, h.first, h.byte_base, h.lane_off, h.start_off, h.tail_base,
+                          S, map_start, map_offset, scratch, tail_lds, tail_cap);
+}
+
+// Loading the header itself: the entry count first, the rest only for a block
+// with entries (the decoders, whose blocks mostly have none).
 __device__ __forceinline__ LaneOverlay build_overlay(const lct_overflow &ov, bool present,
                                                      int64_t block, int64_t n_blocks, int S,
                                                      int32_t *map_start, int32_t *map_offset,
                                                      int32_t *scratch, uint8_t *tail_lds,
                                                      int32_t tail_cap) {
-    return build_overlay(ov, load_overlay_head(ov, present, block, n_blocks), S, map_start,
-                         map_offset, scratch, tail_lds, tail_cap);
+    int32_t count = 0;
+    if (present) {
+        count = ov.blocks[block];
+        if (ov.descriptor != nullptr && ov.descriptor[2] != 0) count = 0;
+    }
+    if (count <= 0) return LaneOverlay{nullptr, S, 0, S, 0};   // uniform across the block
+    int64_t lane_off = 0, start_off = 0, tail_base = ov.base;
+    if (ov.descriptor != nullptr) {
+        const int64_t arena = ov.descriptor[0];
+        const int64_t total = ov.count[0];
+        lane_off = arena;
+        start_off = arena + total;
+        tail_base = arena + 2 * total;
+    }
+    return expand_overlay(ov, count, ov.blocks[n_blocks + block], ov.blocks[2 * n_blocks + block],
+                          lane_off, start_off, tail_base, S, map_start, map_offset, scratch,
+                          tail_lds, tail_cap);
 }
 
 // One lane's stream cursor over payload rows kStride words apart in LDS.
