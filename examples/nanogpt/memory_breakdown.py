@@ -42,6 +42,12 @@ def _site(frames) -> str:
 PHASES = ("forward", "backward", "adam", "muon")
 
 
+def _events(snapshot, device):
+    """The allocation and free events of ``device`` in the recorded history."""
+    return [ev for ev in snapshot["device_traces"][device.index]
+            if ev["action"] in ("alloc", "free_requested")]
+
+
 def _replay(events, bounds):
     """Replay every event.  ``bounds``: the event index at which each phase
     starts, and the index after the last.  Returns the total just before the
@@ -81,6 +87,9 @@ def measure(device, compressed: bool) -> dict:
         gpt.train_step(model, optimizers, inputs, targets)
     inputs, targets = gpt.random_tokens(gpt.BATCH, gpt.SEQ_LEN, device, seed=2000)
     torch.cuda.synchronize(device)
+    # Where the measured step starts in the trace: a marker's address may also
+    # belong to an earlier, freed allocation, so markers are searched after it.
+    before = len(_events(torch.cuda.memory._snapshot(), device))
     # The measured step, phase by phase (train_gpt_lct.train_step's order);
     # a one-element allocation marks where each phase starts in the trace.
     markers = []
@@ -101,14 +110,16 @@ def measure(device, compressed: bool) -> dict:
     torch.cuda.synchronize(device)
     snapshot = torch.cuda.memory._snapshot()
     torch.cuda.memory._record_memory_history(enabled=None)
-    events = [ev for ev in snapshot["device_traces"][device.index]
-              if ev["action"] in ("alloc", "free_requested")]
+    events = _events(snapshot, device)
     addresses = [m.data_ptr() for m in markers]
     bounds, k = [], 0
-    for i, ev in enumerate(events):
+    for i in range(before, len(events)):
+        ev = events[i]
         if k < len(addresses) and ev["action"] == "alloc" and ev["addr"] == addresses[k]:
             bounds.append(i + 1)
             k += 1
+    if len(bounds) != len(addresses):
+        raise RuntimeError("phase markers not found in the allocator trace")
     del markers
     held, peaks, at_peak, phase = _replay(events, bounds)
     by_site = collections.Counter()
