@@ -432,3 +432,19 @@ def test_many_deferred_frees_equal_immediate_frees():
     assert _free_regions_snapshot(buf_a) == _free_regions_snapshot(buf_b)
     verify_buffer(buf_b)
     assert torch.equal(decompress(ct_b).view(torch.int16), x.view(torch.int16))
+
+
+def test_free_batch_of_stale_descriptors_after_reset():
+    """Descriptors made before a reset are stale (another generation): a batch
+    of them gets status 4 for each and leaves the reset free list whole."""
+    require_gpu()
+    print("case lct_buffer_free_batch after reset", flush=True)
+    buffer = TensorBuffer(1 << 20, max_free_regions=16, device="cuda")
+    request = torch.tensor([2000], dtype=torch.int32, device="cuda")
+    allocs = [buffer.allocate(request) for _ in range(5)]
+    buffer.reset()
+    status = torch.full((5,), -1, dtype=torch.int32, device="cuda")
+    dispatch.buffer_free_batch(buffer.storage, 16, [a.descriptor for a in allocs], status)
+    torch.cuda.synchronize()
+    assert status.tolist() == [4] * 5
+    assert _free_regions_snapshot(buffer) == [(0, 1 << 20)]
