@@ -266,8 +266,22 @@ struct PolledSummaries {
         if (pending != 0) failed = true;
     }
 
-    // Whether any thread saw a failure (uniform).  Contains a barrier.
-    __device__ bool incomplete() const { return __syncthreads_or(failed ? 1 : 0) != 0; }
+    // Whether any thread saw a failure (uniform).  Contains barriers.  A
+    // ballot per wave and one LDS word per wave: HIP's __syncthreads_or
+    // brings 256 bytes of library LDS into every kernel that scans, which
+    // leaves the encoder at W = 19 one workgroup per CU short (LDS is
+    // granted in 1280-byte steps, and five workgroups need <= 32000 bytes).
+    __device__ bool incomplete() const {
+        __shared__ int32_t any[kWavesPerBlock];
+        const bool wave_failed = __ballot(failed) != 0;
+        if (wave_lane() == 0) any[threadIdx.x / kWave] = wave_failed ? 1 : 0;
+        __syncthreads();
+        int32_t seen = 0;
+#pragma unroll
+        for (int w = 0; w < kWavesPerBlock; ++w) seen |= any[w];
+        __syncthreads();   // `any` may be rewritten by the next call
+        return seen != 0;
+    }
 };
 
 // No arena: the scans only (private storage, whose exact-size arrays the host
