@@ -204,8 +204,12 @@ class TensorBuffer:
             return []
         keep = dispatch.MAX_PENDING_FREES
         if len(self._pending_frees) > keep:
-            early, self._pending_frees = self._pending_frees[:-keep], self._pending_frees[-keep:]
-            _free_many(self._storage, early, self.max_free_regions, stream=self._pending_stream)
+            # Dropped from the list once launched: a launch that raises (at
+            # most MAX_FREE_BATCH wait, so it is one launch) leaves them
+            # deferred.
+            _free_many(self._storage, self._pending_frees[:-keep], self.max_free_regions,
+                       stream=self._pending_stream)
+            del self._pending_frees[:-keep]
         frees, self._pending_frees = self._pending_frees, []
         return frees
 
@@ -217,8 +221,9 @@ class TensorBuffer:
         would have followed an immediate free.  That stream must still exist."""
         if not self._pending_frees:
             return
-        frees, self._pending_frees = self._pending_frees, []
-        _free_many(self._storage, frees, self.max_free_regions, stream=self._pending_stream)
+        _free_many(self._storage, self._pending_frees, self.max_free_regions,
+                   stream=self._pending_stream)
+        self._pending_frees = []   # only once launched, as in _take_frees
         if self._pending_stream != self._current_stream():
             done = torch.cuda.Event()
             done.record(torch.cuda.ExternalStream(self._pending_stream, device=self.device))

@@ -307,3 +307,31 @@ def test_frees_taken_by_a_reservation_that_fails_to_launch_stay_pending(deferral
                           logical_numel=32768)
     assert log == []
     assert buf._take_frees() == ["d1", "d2"]
+
+
+def test_frees_whose_batch_launch_raises_stay_pending(deferral, monkeypatch):
+    """A batched free launch that raises frees nothing, so its frees stay
+    deferred, for a flush and for the early frees of a reservation."""
+    from losslessly_compressed_tensors_amd import tensor_buffer as tb
+    from losslessly_compressed_tensors_amd.kernels import dispatch, hip
+
+    buf, state, log = deferral
+    keep = dispatch.MAX_PENDING_FREES
+    names = [f"d{i}" for i in range(keep + 3)]
+    for name in names:
+        buf._defer_free(name)
+
+    def failing_batch(storage, ds, regions, stream=None):
+        raise hip.LCTKernelError("lct_buffer_free_batch failed with code -4")
+
+    monkeypatch.setattr(tb, "_free_many", failing_batch)
+    with pytest.raises(hip.LCTKernelError):
+        buf._take_frees()
+    with pytest.raises(hip.LCTKernelError):
+        buf._flush_frees()
+    assert buf._pending_frees == names and log == []
+    monkeypatch.setattr(tb, "_free_many",
+                        lambda storage, ds, regions, stream=None: log.append(("free", list(ds),
+                                                                              stream)))
+    assert buf._take_frees() == names[3:]
+    assert log == [("free", names[:3], 11)]
