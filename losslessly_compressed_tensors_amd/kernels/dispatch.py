@@ -787,7 +787,12 @@ def buffer_free_batch(storage, max_free_regions, descriptors, status=None, *,
     ``buffer_free``."""
     if not 1 <= len(descriptors) <= MAX_FREE_BATCH:
         raise ValueError(f"1 to {MAX_FREE_BATCH} descriptors per batch, got {len(descriptors)}")
-    _require_device(storage, *descriptors)
+    # The kernel reads 4 ints of each descriptor and writes one status each.
+    if any(d.dtype != torch.int32 or d.numel() < 4 for d in descriptors):
+        raise ValueError("descriptors are int32[4] tensors")
+    if status is not None and (status.dtype != torch.int32 or status.numel() < len(descriptors)):
+        raise ValueError(f"status must be int32[{len(descriptors)}] or None")
+    _require_device(storage, *descriptors, status)
     array = (hip.ctypes.c_void_p * len(descriptors))(*(d.data_ptr() for d in descriptors))
     hip.call("lct_buffer_free_batch", _ptr(storage), int(max_free_regions), array,
              len(descriptors), _ptr(status), _stream(storage) if stream is None else stream)

@@ -335,3 +335,20 @@ def test_frees_whose_batch_launch_raises_stay_pending(deferral, monkeypatch):
                                                                               stream)))
     assert buf._take_frees() == names[3:]
     assert log == [("free", names[:3], 11)]
+
+
+def test_free_batch_checks_descriptor_and_status_sizes_before_launch():
+    """``dispatch.buffer_free_batch`` rejects short descriptors and a status
+    array shorter than the batch before it touches a device."""
+    from losslessly_compressed_tensors_amd.kernels import dispatch
+
+    storage = torch.zeros(64, dtype=torch.int32)
+    good = torch.zeros(4, dtype=torch.int32)
+    with pytest.raises(ValueError, match="descriptors"):
+        dispatch.buffer_free_batch(storage, 4, [good, torch.zeros(3, dtype=torch.int32)])
+    with pytest.raises(ValueError, match="descriptors"):
+        dispatch.buffer_free_batch(storage, 4, [torch.zeros(4, dtype=torch.int64)])
+    with pytest.raises(ValueError, match="status"):
+        dispatch.buffer_free_batch(storage, 4, [good, good], torch.zeros(1, dtype=torch.int32))
+    with pytest.raises(ValueError, match="GPU tensors"):    # sizes fine: the device check
+        dispatch.buffer_free_batch(storage, 4, [good, good], torch.zeros(2, dtype=torch.int32))
