@@ -381,6 +381,7 @@ def fused_update_batch(items, operation: PointwiseOp, buffer: TensorBuffer, *,
                 data, other, operation, alpha=alpha, beta=beta, alpha_is_one=alpha_is_one,
                 dense_output=False, buffer=buffer, distribution=result_distribution)
             continue
+        _require_bf16(other, operation)
         dispatch.require_device(data.data, other)
         other = other.contiguous().view(-1)
         block_symbols, lanes, steps, fixed_words = data.codec_geometry
@@ -459,6 +460,16 @@ def fused_update_batch(items, operation: PointwiseOp, buffer: TensorBuffer, *,
     return results
 
 
+def _require_bf16(other: torch.Tensor, operation: PointwiseOp) -> None:
+    """The kernels read the dense operand as BF16.  The reference's kernel
+    loads it with its own dtype (``LCT/kernels/generic/pointwise.py:154``);
+    here any other dtype raises rather than being read with the wrong
+    element size."""
+    if other.dtype != torch.bfloat16:
+        raise TypeError(f"{operation.name}: the dense operand must be bfloat16, "
+                        f"got {other.dtype}")
+
+
 def pointwise_compressed_dense(data: CompressedTensor, other: torch.Tensor,
                                operation: PointwiseOp, *, alpha: torch.Tensor | None = None,
                                beta: torch.Tensor | None = None, alpha_is_one: bool = False,
@@ -468,6 +479,8 @@ def pointwise_compressed_dense(data: CompressedTensor, other: torch.Tensor,
     (``LCT/codec/pointwise.py:213-278``)."""
     if tuple(other.shape) != data.shape:
         raise ValueError(f"{operation.name} expects tensors with the same shape")
+    if data.layout == StorageLayout.COMPRESSED:
+        _require_bf16(other, operation)
     result_distribution = distribution or data.distribution
     if operation is SCALAR_MUL_ADD and alpha is None:
         raise ValueError("scalar_mul_add requires an alpha argument")

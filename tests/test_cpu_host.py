@@ -352,3 +352,26 @@ def test_free_batch_checks_descriptor_and_status_sizes_before_launch():
         dispatch.buffer_free_batch(storage, 4, [good, good], torch.zeros(1, dtype=torch.int32))
     with pytest.raises(ValueError, match="GPU tensors"):    # sizes fine: the device check
         dispatch.buffer_free_batch(storage, 4, [good, good], torch.zeros(2, dtype=torch.int32))
+
+
+def test_a_dense_operand_that_is_not_bfloat16_raises_before_any_launch():
+    """The fused pointwise kernels read the dense operand as BF16: a float32
+    or int8 operand of the right shape raises TypeError instead of being read
+    with the wrong element size."""
+    from losslessly_compressed_tensors_amd.codec import pointwise as pw
+    from losslessly_compressed_tensors_amd.codec.geometry import geometry
+    from losslessly_compressed_tensors_amd.comp_format import Distribution, StorageLayout
+    from losslessly_compressed_tensors_amd.comp_tensor import CompressedTensor
+
+    dist = Distribution()
+    ct = CompressedTensor(torch.zeros(4, dtype=torch.int32), 65536,
+                          torch.zeros(65536, dtype=torch.uint8), distribution=dist,
+                          shape=(256, 256), layout=StorageLayout.COMPRESSED,
+                          stream_geometry=geometry(dist))
+    alpha = torch.ones(1)
+    for dtype in (torch.float32, torch.int8):
+        other = torch.zeros(256, 256, dtype=dtype)
+        with pytest.raises(TypeError, match="bfloat16"):
+            pw.pointwise_compressed_dense(ct, other, pw.SCALAR_MUL_ADD, alpha=alpha)
+        with pytest.raises(TypeError, match="bfloat16"):
+            pw.pointwise_compressed_dense(ct, other, pw.ADD, dense_output=False)
