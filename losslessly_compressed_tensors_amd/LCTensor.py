@@ -109,6 +109,10 @@ class LCTTensor(Tensor):
         a buffer with one launch of each kind per 8 (``a_compA_add_b_B_batch``;
         a weight's update is a few codec blocks, so one launch per tensor
         would be bound by one block's latency), the others one by one."""
+        tensors, updates = list(tensors), list(updates)
+        if len(tensors) != len(updates):
+            raise ValueError(f"one update per tensor: {len(tensors)} tensors, "
+                             f"{len(updates)} updates")
         groups: dict[int, list] = {}
         for tensor, update in zip(tensors, updates):
             if tensor.x.buffer is None:

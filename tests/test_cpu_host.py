@@ -375,3 +375,12 @@ def test_a_dense_operand_that_is_not_bfloat16_raises_before_any_launch():
             pw.pointwise_compressed_dense(ct, other, pw.SCALAR_MUL_ADD, alpha=alpha)
         with pytest.raises(TypeError, match="bfloat16"):
             pw.pointwise_compressed_dense(ct, other, pw.ADD, dense_output=False)
+
+
+def test_mul_add_many_needs_one_update_per_tensor():
+    """A length mismatch raises before any tensor is updated (zip would
+    silently leave the extra tensors as they were)."""
+    from losslessly_compressed_tensors_amd.LCTensor import LCTTensor
+
+    with pytest.raises(ValueError, match="one update per tensor"):
+        LCTTensor.mul_add_many([object(), object()], torch.ones(1), [torch.zeros(1)])
