@@ -163,6 +163,9 @@ def a_compA_add_b_B_batch(A_comps, a: Tensor, Bs, b: Tensor | None = None, *,
                     f"{name} must be a float32 scalar on the compressed tensors' device")
     if distributions is None:
         distributions = [A.distribution for A in A_comps]
+    distributions = list(distributions)
+    if len(distributions) != len(A_comps):
+        raise ValueError("one distribution per compressed A")
     return fused_update_batch(list(zip(A_comps, Bs, distributions)), SCALAR_MUL_ADD, buffer,
                               alpha=a, beta=b, alpha_is_one=alpha_is_one)
 

@@ -384,3 +384,18 @@ def test_mul_add_many_needs_one_update_per_tensor():
 
     with pytest.raises(ValueError, match="one update per tensor"):
         LCTTensor.mul_add_many([object(), object()], torch.ones(1), [torch.zeros(1)])
+
+
+def test_batched_update_needs_one_distribution_per_tensor():
+    """zip would drop the tensors past the shorter list: a length mismatch
+    raises before any launch."""
+    from losslessly_compressed_tensors_amd.comp_format import Distribution
+    from losslessly_compressed_tensors_amd.operations import a_compA_add_b_B_batch
+
+    class _A:
+        data = torch.zeros(1)
+        distribution = Distribution()
+
+    with pytest.raises(ValueError, match="one distribution per compressed A"):
+        a_compA_add_b_B_batch([_A(), _A()], torch.ones(1), [torch.zeros(1)] * 2,
+                              buffer=None, distributions=[Distribution()])
